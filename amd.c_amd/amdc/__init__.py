@@ -1,0 +1,245 @@
+"""Python access to libamdc_q4.so, the MI355X quantized GEMV/GEMM path.
+
+A thin ctypes mirror of include/amdc_q4.h for the test harness and bench.py:
+the computation is in the HIP kernels (amdc_kernels.hsaco) that the C host
+launches. There is no fallback: without the built library, or without a GPU,
+every operator raises ``AmdcError``.
+
+Names follow the reference's operators (hanw/amd.c src/backend.h:61-64,
+src/hip.c:922-1026): ``quant_q8``, ``gemv_q4``, ``gemv_q4k``, the multi-vector
+``gemv_q4_t`` / ``gemv_q4k_t``, the prefill ``gemm_q4k`` and the dispatcher
+``op_gemv``; ``repack_q4`` / ``repack_q4k`` replace the load-time repack of
+src/model.c:205-267.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "libamdc_q4.so")
+HSACO_PATH = os.path.join(PKG_DIR, "amdc_kernels.hsaco")
+
+KIND_Q4_0, KIND_Q4_K = 0, 3
+_P, _U32 = C.c_void_p, C.c_uint32
+
+# every function of include/amdc_q4.h: name -> (restype, argtypes)
+ABI = {
+    "amdc_last_error": (C.c_char_p, []),
+    "amdc_mat_bytes": (C.c_size_t, [C.c_int, _U32, _U32]),
+    "amdc_repack_q4": (C.c_int, [_P, _U32, _U32, _P]),
+    "amdc_repack_q4k": (C.c_int, [_P, _U32, _U32, _P]),
+    "amdc_open": (C.c_int, [C.c_char_p]),
+    "amdc_close": (None, []),
+    "amdc_cu_count": (C.c_int, []),
+    "amdc_malloc": (C.c_int, [C.POINTER(_P), C.c_size_t]),
+    "amdc_free": (C.c_int, [_P]),
+    "amdc_memcpy_h2d": (C.c_int, [_P, _P, C.c_size_t]),
+    "amdc_memcpy_d2h": (C.c_int, [_P, _P, C.c_size_t]),
+    "amdc_memcpy_d2d": (C.c_int, [_P, _P, C.c_size_t]),
+    "amdc_memset": (C.c_int, [_P, C.c_int, C.c_size_t]),
+    "amdc_sync": (C.c_int, []),
+    "amdc_event_create": (C.c_int, [C.POINTER(_P)]),
+    "amdc_event_destroy": (C.c_int, [_P]),
+    "amdc_event_record": (C.c_int, [_P, _P]),
+    "amdc_event_elapsed_ms": (C.c_int, [C.POINTER(C.c_float), _P, _P]),
+    "amdc_quant_q8": (C.c_int, [_P, _P, _U32, _U32, _U32, _U32, _P]),
+    "amdc_gemv_q4": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
+    "amdc_gemv_q4k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
+    "amdc_gemv_q4_t": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
+    "amdc_gemv_q4k_t": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
+    "amdc_gemm_q4k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
+    "amdc_op_gemv": (C.c_int, [C.c_int, _P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
+    "amdc_block_dots": (C.c_int, [C.c_int, _P, _P, _P, _U32, _U32, _P]),
+    "amdc_set_tuning": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int]),
+}
+
+
+class AmdcError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def lib():
+    """The loaded libamdc_q4.so (raises if it is not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise AmdcError(f"{LIB_PATH} is not built: run __graft_entry__.build() (make -C amd.c_amd)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in ABI.items():
+            f = getattr(L, name)
+            f.restype, f.argtypes = res, args
+        _lib = L
+    return _lib
+
+
+def _check(rc):
+    if rc:
+        raise AmdcError(lib().amdc_last_error().decode(errors="replace"))
+
+
+_opened = False
+
+
+def open_device(hsaco=None):
+    """amdc_open: HIP runtime, device 0, the kernel code object."""
+    global _opened
+    if not _opened:
+        _check(lib().amdc_open((hsaco or HSACO_PATH).encode()))
+        _opened = True
+
+
+def cu_count():
+    return lib().amdc_cu_count()
+
+
+def set_tuning(lanes=0, unroll=0, wgs=0, gemm_tokens=0):
+    _check(lib().amdc_set_tuning(lanes, unroll, wgs, gemm_tokens))
+
+
+def sync():
+    _check(lib().amdc_sync())
+
+
+class DevBuf:
+    """A device allocation (hipMalloc through the library)."""
+
+    def __init__(self, nbytes):
+        open_device()
+        p = _P()
+        _check(lib().amdc_malloc(C.byref(p), max(int(nbytes), 1)))
+        self.ptr, self.nbytes = p.value, int(nbytes)
+
+    @classmethod
+    def of(cls, a):
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a, offset=0):
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        _check(lib().amdc_memcpy_h2d(self.ptr + offset, a.ctypes.data_as(_P), a.nbytes))
+
+    def download(self, dtype, count=None, offset=0):
+        dtype = np.dtype(dtype)
+        count = (self.nbytes - offset) // dtype.itemsize if count is None else count
+        out = np.empty(count, dtype=dtype)
+        _check(lib().amdc_memcpy_d2h(out.ctypes.data_as(_P), self.ptr + offset, out.nbytes))
+        return out
+
+    def fill(self, v=0):
+        _check(lib().amdc_memset(self.ptr, v, self.nbytes))
+
+    def free(self):
+        if self.ptr:
+            _check(lib().amdc_free(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and _lib is not None:
+                _lib.amdc_free(self.ptr)
+        except Exception:
+            pass
+
+
+def _p(x):
+    if x is None:
+        return None
+    return x.ptr if isinstance(x, DevBuf) else int(x)
+
+
+class Event:
+    def __init__(self):
+        open_device()
+        p = _P()
+        _check(lib().amdc_event_create(C.byref(p)))
+        self.ev = p.value
+
+    def record(self, stream=None):
+        _check(lib().amdc_event_record(self.ev, stream))
+
+    def elapsed_ms(self, later):
+        ms = C.c_float()
+        _check(lib().amdc_event_elapsed_ms(C.byref(ms), self.ev, later.ev))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self.ev and _lib is not None:
+                _lib.amdc_event_destroy(self.ev)
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------- load time (host)
+
+def mat_bytes(kind, rows, cols):
+    n = lib().amdc_mat_bytes(kind, rows, cols)
+    if not n:
+        raise AmdcError(f"kind {kind}: {rows}x{cols} is not a valid shape")
+    return n
+
+
+def repack(kind, gguf, rows, cols):
+    """GGUF bytes -> the CDNA4 layout (host numpy uint8)."""
+    src = np.ascontiguousarray(gguf, dtype=np.uint8)
+    dst = np.empty(mat_bytes(kind, rows, cols), dtype=np.uint8)
+    f = lib().amdc_repack_q4 if kind == KIND_Q4_0 else lib().amdc_repack_q4k
+    _check(f(src.ctypes.data_as(_P), rows, cols, dst.ctypes.data_as(_P)))
+    return dst
+
+
+def repack_q4(gguf, rows, cols):
+    return repack(KIND_Q4_0, gguf, rows, cols)
+
+
+def repack_q4k(gguf, rows, cols):
+    return repack(KIND_Q4_K, gguf, rows, cols)
+
+
+# ---------------------------------------------------------------- operators (device pointers)
+
+def quant_q8(x, q, nb, T=1, xs=0, qs=0, stream=None):
+    _check(lib().amdc_quant_q8(_p(x), _p(q), nb, T, xs, qs, stream))
+
+
+def gemv_q4(w, xq, y, rows, nb, bias=None, res=None, stream=None):
+    _check(lib().amdc_gemv_q4(_p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), stream))
+
+
+def gemv_q4k(w, xq, y, rows, nb, bias=None, res=None, stream=None):
+    _check(lib().amdc_gemv_q4k(_p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), stream))
+
+
+def gemv(kind, w, xq, y, rows, nb, bias=None, res=None, stream=None):
+    (gemv_q4k if kind == KIND_Q4_K else gemv_q4)(w, xq, y, rows, nb, bias, res, stream)
+
+
+def gemv_q4_t(w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stream=None):
+    _check(lib().amdc_gemv_q4_t(_p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), T, xs, ys, rs, stream))
+
+
+def gemv_q4k_t(w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stream=None):
+    _check(lib().amdc_gemv_q4k_t(_p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), T, xs, ys, rs, stream))
+
+
+def gemv_t(kind, w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stream=None):
+    (gemv_q4k_t if kind == KIND_Q4_K else gemv_q4_t)(w, xq, y, rows, nb, T, xs, ys, rs, bias, res, stream)
+
+
+def gemm_q4k(w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stream=None):
+    _check(lib().amdc_gemm_q4k(_p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), T, xs, ys, rs, stream))
+
+
+def op_gemv(kind, w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stream=None):
+    _check(lib().amdc_op_gemv(kind, _p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), T, xs, ys, rs, stream))
+
+
+def block_dots(kind, w, xq, out, rows, nb, stream=None):
+    _check(lib().amdc_block_dots(kind, _p(w), _p(xq), _p(out), rows, nb, stream))

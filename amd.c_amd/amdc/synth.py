@@ -1,0 +1,71 @@
+"""Seeded synthetic GGUF weights and activations for the configurations of the
+benchmark (weights: uniform nibbles; Q4_0 f16 d = |N(0,1)| * 0.02; Q4_K f16
+d, dmin = |N(0,1)| * 0.01 and uniform 6-bit scales and mins; activations
+f32 N(0,1)). numpy's float32 -> float16 cast rounds to nearest even, as the
+reference's ie_f32_to_f16 (hanw/amd.c src/common.c:48-67).
+
+GGUF Q4_0 block (18 bytes): f16 d, 16 nibble bytes (core/ie_core.h:66-68).
+GGUF Q4_K super-block (144 bytes): f16 d, f16 dmin, 12 bytes of 6-bit scales
+and mins, 128 nibble bytes (core/ie_core.h:247-251).
+"""
+import numpy as np
+
+KIND_Q4_0, KIND_Q4_K = 0, 3
+GGML = {KIND_Q4_0: 2, KIND_Q4_K: 12}
+
+
+def rng(seed):
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def gguf_q4_0(rows, cols, seed, scale=0.02):
+    """rows x cols Q4_0 weights as GGUF bytes (rows * cols / 32 * 18)."""
+    assert cols % 32 == 0
+    g = rng(seed)
+    n = rows * (cols // 32)
+    blk = np.empty((n, 18), dtype=np.uint8)
+    d = (np.abs(g.standard_normal(n, dtype=np.float32)) * np.float32(scale)).astype(np.float16)
+    blk[:, 0:2] = d.view(np.uint8).reshape(n, 2)
+    blk[:, 2:] = g.integers(0, 256, size=(n, 16), dtype=np.uint8)
+    return blk.reshape(-1)
+
+
+def gguf_q4_k(rows, cols, seed, scale=0.01):
+    """rows x cols Q4_K weights as GGUF bytes (rows * cols / 256 * 144)."""
+    assert cols % 256 == 0
+    g = rng(seed)
+    n = rows * (cols // 256)
+    blk = np.empty((n, 144), dtype=np.uint8)
+    dd = (np.abs(g.standard_normal((n, 2), dtype=np.float32)) * np.float32(scale)).astype(np.float16)
+    blk[:, 0:4] = dd.view(np.uint8).reshape(n, 4)
+    blk[:, 4:] = g.integers(0, 256, size=(n, 140), dtype=np.uint8)
+    return blk.reshape(-1)
+
+
+def gguf(kind, rows, cols, seed):
+    return gguf_q4_k(rows, cols, seed) if kind == KIND_Q4_K else gguf_q4_0(rows, cols, seed)
+
+
+def activations(T, cols, seed):
+    """T f32 ~ N(0,1) vectors of cols elements."""
+    return rng(seed).standard_normal((T, cols), dtype=np.float32)
+
+
+def gguf_bytes(kind, rows, cols):
+    return rows * cols // 32 * 18
+
+
+# The configurations (rows x cols = N outputs x K inputs).
+CONFIGS = {
+    "c0": {"kind": KIND_Q4_0, "T": 1, "shapes": [("q4096x4096", 4096, 4096)]},
+    "c1": {"kind": KIND_Q4_0, "T": 1, "shapes": [
+        ("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
+        ("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008), ("lm_head", 32000, 4096)]},
+    "c2": {"kind": KIND_Q4_K, "T": 1, "shapes": [
+        ("ffn_gate", 17408, 5120), ("ffn_up", 17408, 5120), ("ffn_down", 5120, 17408),
+        ("attn_in", 6144, 5120), ("attn_out", 5120, 6144), ("lm_head", 152064, 5120)]},
+    "c3": {"T": 8, "shapes": [
+        ("q4k_ffn_up", 17408, 5120, KIND_Q4_K), ("q4k_ffn_down", 5120, 17408, KIND_Q4_K),
+        ("q4_0_gate", 11008, 4096, KIND_Q4_0)]},
+    "c4": {"kind": KIND_Q4_K, "T": 256, "shapes": [("ffn_up", 17408, 5120), ("ffn_down", 5120, 17408)]},
+}

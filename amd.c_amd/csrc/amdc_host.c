@@ -1,0 +1,458 @@
+/* amdc_host.c -- the C host of the MI355X quantized GEMV/GEMM path
+ * (libamdc_q4.so; the ABI is include/amdc_q4.h).
+ *
+ * As the reference's GPU host (hanw/amd.c src/hip.c), it needs no ROCm
+ * headers: the HIP runtime is dlopen'ed and the kernels are resolved by name
+ * from a code object (amdc_kernels.hsaco) and launched with
+ * hipModuleLaunchKernel and a void* argument array. It also holds the
+ * load-time repack into the CDNA4 layout (amdc_layout.h), which replaces
+ * repack_q4 / repack_q4k of src/model.c. */
+#define _GNU_SOURCE
+#include "../../include/amdc_q4.h"
+
+#include <dlfcn.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "amdc_layout.h"
+
+typedef uint32_t u32;
+typedef uint64_t u64;
+
+/* ---------------------------------------------------------------- errors */
+
+static char g_err[512];
+
+static int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+const char *amdc_last_error(void) { return g_err; }
+
+/* ---------------------------------------------------------------- repack */
+
+size_t amdc_mat_bytes(int kind, uint32_t rows, uint32_t cols) {
+  if (cols % 32u || (kind == AMDC_KIND_Q4_K && cols % 256u) || (kind != AMDC_KIND_Q4_0 && kind != AMDC_KIND_Q4_K)) return 0;
+  return (size_t)rows * amdc_row_bytes(cols / 32u);
+}
+
+/* GGUF Q4_0: block b of row r = 18 bytes at (r nb + b) 18: f16 d, then
+ * nibble byte j (weight j low, j + 16 high). The 16 nibble bytes go to the
+ * block's slot unchanged, d to its header (src/model.c:205-219 keeps the same
+ * bytes in another order). */
+int amdc_repack_q4(const uint8_t *src, uint32_t rows, uint32_t cols, uint8_t *dst) {
+  if (!src || !dst || !rows || !cols || cols % 32u) return fail(AMDC_EINVAL, "repack_q4: %ux%u (cols must be a multiple of 32)", rows, cols);
+  const u32 nb = cols / 32u, ng = amdc_ngroups(nb);
+  const u64 rb = amdc_row_bytes(nb);
+  memset(dst, 0, (size_t)rows * rb);
+  for (u32 r = 0; r < rows; r++) {
+    uint8_t *row = dst + (u64)r * rb;
+    for (u32 b = 0; b < nb; b++) {
+      const uint8_t *blk = src + ((u64)r * nb + b) * 18u;
+      const u32 g = b >> 3, k = b & 7u;
+      row[amdc_header_off(g) + 2u * k] = blk[0];
+      row[amdc_header_off(g) + 2u * k + 1u] = blk[1];
+      memcpy(row + amdc_nib_off(ng, g, k), blk + 2, 16);
+    }
+  }
+  return AMDC_OK;
+}
+
+/* The 6-bit scale and min of sub-block j of a Q4_K super-block from its 12
+ * scale bytes (ggml's get_scale_min_k4, as src/model.c:24-31). */
+static void q4k_scale_min(u32 j, const uint8_t *s, u32 *sc, u32 *mn) {
+  if (j < 4) {
+    *sc = s[j] & 63u;
+    *mn = s[j + 4] & 63u;
+  } else {
+    *sc = (s[j + 4] & 15u) | ((u32)(s[j - 4] >> 6) << 4);
+    *mn = (u32)(s[j + 4] >> 4) | ((u32)(s[j] >> 6) << 4);
+  }
+}
+
+/* GGUF Q4_K: super-block g of row r = 144 bytes: f16 d, f16 dmin, 12 scale
+ * bytes, 128 nibble bytes (sub-blocks 2i and 2i+1 are the low and high
+ * nibbles of bytes 32i..32i+31). Sub-block k becomes a Q4_0-order block (byte
+ * j: weight j low, j + 16 high), as MAT_Q4K (src/model.c:246-267); the
+ * header keeps d and dmin and packs sc_0..7 and mn_0..7 six bits each. */
+int amdc_repack_q4k(const uint8_t *src, uint32_t rows, uint32_t cols, uint8_t *dst) {
+  if (!src || !dst || !rows || !cols || cols % 256u)
+    return fail(AMDC_EINVAL, "repack_q4k: %ux%u (cols must be a multiple of 256)", rows, cols);
+  const u32 nb = cols / 32u, ng = nb / 8u;
+  const u64 rb = amdc_row_bytes(nb);
+  for (u32 r = 0; r < rows; r++) {
+    uint8_t *row = dst + (u64)r * rb;
+    for (u32 g = 0; g < ng; g++) {
+      const uint8_t *blk = src + ((u64)r * ng + g) * 144u;
+      uint8_t *hd = row + amdc_header_off(g);
+      u64 scs = 0, mns = 0;
+      for (u32 k = 0; k < 8; k++) {
+        u32 sc, mn;
+        q4k_scale_min(k, blk + 4, &sc, &mn);
+        scs |= (u64)sc << (6u * k);
+        mns |= (u64)mn << (6u * k);
+      }
+      memcpy(hd, blk, 4); /* f16 d, f16 dmin */
+      for (u32 i = 0; i < 6; i++) hd[4 + i] = (uint8_t)(scs >> (8u * i)), hd[10 + i] = (uint8_t)(mns >> (8u * i));
+      for (u32 k = 0; k < 8; k++) {
+        const uint8_t *pair = blk + 16 + 32u * (k >> 1);
+        uint8_t *o = row + amdc_nib_off(ng, g, k);
+        for (u32 j = 0; j < 16; j++) {
+          const u32 lo = (k & 1u) ? (u32)pair[j] >> 4 : pair[j] & 15u, hi = (k & 1u) ? (u32)pair[j + 16] >> 4 : pair[j + 16] & 15u;
+          o[j] = (uint8_t)(lo | (hi << 4));
+        }
+      }
+    }
+  }
+  return AMDC_OK;
+}
+
+/* ---------------------------------------------------------------- HIP through dlopen */
+
+typedef int hipError_t;
+typedef void *hipModule_t, *hipFunction_t, *hipStream_t, *hipEvent_t;
+enum { hipMemcpyHostToDevice = 1, hipMemcpyDeviceToHost = 2, hipMemcpyDeviceToDevice = 3 };
+enum { hipDeviceAttributeMultiprocessorCount = 63 };
+
+static struct {
+  void *lib;
+  hipError_t (*GetDeviceCount)(int *);
+  hipError_t (*SetDevice)(int);
+  hipError_t (*DeviceGetAttribute)(int *, int, int);
+  hipError_t (*ModuleLoad)(hipModule_t *, const char *);
+  hipError_t (*ModuleUnload)(hipModule_t);
+  hipError_t (*ModuleGetFunction)(hipFunction_t *, hipModule_t, const char *);
+  hipError_t (*ModuleLaunchKernel)(hipFunction_t, unsigned, unsigned, unsigned, unsigned, unsigned, unsigned, unsigned, hipStream_t,
+                                   void **, void **);
+  hipError_t (*Malloc)(void **, size_t);
+  hipError_t (*Free)(void *);
+  hipError_t (*Memcpy)(void *, const void *, size_t, int);
+  hipError_t (*Memset)(void *, int, size_t);
+  hipError_t (*DeviceSynchronize)(void);
+  hipError_t (*EventCreate)(hipEvent_t *);
+  hipError_t (*EventDestroy)(hipEvent_t);
+  hipError_t (*EventRecord)(hipEvent_t, hipStream_t);
+  hipError_t (*EventSynchronize)(hipEvent_t);
+  hipError_t (*EventElapsedTime)(float *, hipEvent_t, hipEvent_t);
+  const char *(*GetErrorString)(hipError_t);
+} H;
+
+/* The kernels of amdc_kernels.hip. */
+enum {
+  K_QUANT,
+  K_GEMV_Q4_T1,
+  K_GEMV_Q4K_T1,
+  K_GEMV_Q4_T1U1,
+  K_GEMV_Q4K_T1U1,
+  K_GEMV_Q4_T8,
+  K_GEMV_Q4K_T8,
+  K_GEMV_Q4_T16,
+  K_GEMV_Q4K_T16,
+  K_DOTS_Q4,
+  K_DOTS_Q4K,
+  K_GEMM_N128,
+  K_GEMM_N64,
+  K_N
+};
+static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1",  "amdc_gemv_q4_k_t1",  "amdc_gemv_q4_0_t1u1",
+                                       "amdc_gemv_q4_k_t1u1", "amdc_gemv_q4_0_t8",  "amdc_gemv_q4_k_t8",  "amdc_gemv_q4_0_t16",
+                                       "amdc_gemv_q4_k_t16",  "amdc_dots_q4_0",     "amdc_dots_q4_k",     "amdc_gemm_q4_k_n128",
+                                       "amdc_gemm_q4_k_n64"};
+
+static hipModule_t g_mod;
+static hipFunction_t g_k[K_N];
+static int g_open, g_cus;
+static int t_lanes = -1, t_unroll = -1, t_wgs = -1, t_gemm = -1, t_gemm_min = -1;
+
+#define HIPCALL(x)                                                                               \
+  do {                                                                                           \
+    const hipError_t e_ = (x);                                                                   \
+    if (e_) return fail(AMDC_EHIP, "%s: %s (%d)", #x, H.GetErrorString ? H.GetErrorString(e_) : "?", e_); \
+  } while (0)
+#define NEED_OPEN()                                                               \
+  do {                                                                            \
+    if (!g_open) return fail(AMDC_ENOTOPEN, "amdc_open has not been called"); \
+  } while (0)
+
+static int envi(const char *n, int dflt) {
+  const char *v = getenv(n);
+  return v && *v ? atoi(v) : dflt;
+}
+
+static int hip_load(void) {
+  if (H.lib) return AMDC_OK;
+  const char *names[] = {"libamdhip64.so.7", "libamdhip64.so", "/opt/rocm/lib/libamdhip64.so"};
+  for (unsigned i = 0; i < sizeof names / sizeof names[0] && !H.lib; i++) H.lib = dlopen(names[i], RTLD_NOW | RTLD_GLOBAL);
+  if (!H.lib) return fail(AMDC_ENOHIP, "cannot load the HIP runtime (libamdhip64.so): %s", dlerror());
+#define SYM(f, n)                                                                    \
+  do {                                                                               \
+    *(void **)&H.f = dlsym(H.lib, n);                                                \
+    if (!H.f) return fail(AMDC_ENOHIP, "HIP runtime without %s", n);             \
+  } while (0)
+  SYM(GetDeviceCount, "hipGetDeviceCount");
+  SYM(SetDevice, "hipSetDevice");
+  SYM(DeviceGetAttribute, "hipDeviceGetAttribute");
+  SYM(ModuleLoad, "hipModuleLoad");
+  SYM(ModuleUnload, "hipModuleUnload");
+  SYM(ModuleGetFunction, "hipModuleGetFunction");
+  SYM(ModuleLaunchKernel, "hipModuleLaunchKernel");
+  SYM(Malloc, "hipMalloc");
+  SYM(Free, "hipFree");
+  SYM(Memcpy, "hipMemcpy");
+  SYM(Memset, "hipMemset");
+  SYM(DeviceSynchronize, "hipDeviceSynchronize");
+  SYM(EventCreate, "hipEventCreate");
+  SYM(EventDestroy, "hipEventDestroy");
+  SYM(EventRecord, "hipEventRecord");
+  SYM(EventSynchronize, "hipEventSynchronize");
+  SYM(EventElapsedTime, "hipEventElapsedTime");
+  SYM(GetErrorString, "hipGetErrorString");
+#undef SYM
+  return AMDC_OK;
+}
+
+int amdc_open(const char *hsaco) {
+  if (g_open) return AMDC_OK;
+  int rc = hip_load();
+  if (rc) return rc;
+  int n = 0;
+  if (H.GetDeviceCount(&n) || n < 1) return fail(AMDC_ENOHIP, "no HIP device");
+  HIPCALL(H.SetDevice(0));
+  char path[4096];
+  if (!hsaco) { /* next to this library */
+    Dl_info di;
+    if (!dladdr((void *)amdc_open, &di) || !di.dli_fname) return fail(AMDC_EINVAL, "cannot locate libamdc_q4.so");
+    snprintf(path, sizeof path, "%s", di.dli_fname);
+    char *s = strrchr(path, '/');
+    if (s) s[1] = 0;
+    else path[0] = 0;
+    strncat(path, "amdc_kernels.hsaco", sizeof path - strlen(path) - 1);
+    hsaco = path;
+  }
+  HIPCALL(H.ModuleLoad(&g_mod, hsaco));
+  for (int k = 0; k < K_N; k++) HIPCALL(H.ModuleGetFunction(&g_k[k], g_mod, kname[k]));
+  HIPCALL(H.DeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, 0));
+  if (t_lanes < 0) t_lanes = envi("AMDC_GEMV_L", 0);
+  if (t_unroll < 0) t_unroll = envi("AMDC_GEMV_U", 0);
+  if (t_wgs < 0) t_wgs = envi("AMDC_GEMV_WG", 0);
+  if (t_gemm < 0) t_gemm = envi("AMDC_GEMM_N", 0);
+  if (t_gemm_min < 0) t_gemm_min = envi("IE_GEMM_MIN", 17);
+  g_open = 1;
+  return AMDC_OK;
+}
+
+void amdc_close(void) {
+  if (g_open && g_mod) H.ModuleUnload(g_mod);
+  g_mod = NULL;
+  g_open = 0;
+}
+
+int amdc_cu_count(void) { return g_open ? g_cus : 0; }
+
+int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_tokens) {
+  if (gemv_lanes && (gemv_lanes < 4 || gemv_lanes > 64 || (gemv_lanes & (gemv_lanes - 1))))
+    return fail(AMDC_EINVAL, "gemv lanes %d: 4..64, a power of two", gemv_lanes);
+  if (gemv_unroll < 0 || gemv_unroll > 2) return fail(AMDC_EINVAL, "gemv unroll %d: 0, 1 or 2", gemv_unroll);
+  if (gemm_tokens && gemm_tokens != 64 && gemm_tokens != 128) return fail(AMDC_EINVAL, "gemm tokens %d: 64 or 128", gemm_tokens);
+  if (gemv_wgs < 0) return fail(AMDC_EINVAL, "gemv workgroups %d", gemv_wgs);
+  t_lanes = gemv_lanes, t_unroll = gemv_unroll, t_wgs = gemv_wgs, t_gemm = gemm_tokens;
+  return AMDC_OK;
+}
+
+int amdc_malloc(void **p, size_t n) {
+  NEED_OPEN();
+  HIPCALL(H.Malloc(p, n ? n : 1));
+  return AMDC_OK;
+}
+int amdc_free(void *p) {
+  NEED_OPEN();
+  if (p) HIPCALL(H.Free(p));
+  return AMDC_OK;
+}
+int amdc_memcpy_h2d(void *d, const void *s, size_t n) {
+  NEED_OPEN();
+  HIPCALL(H.Memcpy(d, s, n, hipMemcpyHostToDevice));
+  return AMDC_OK;
+}
+int amdc_memcpy_d2h(void *d, const void *s, size_t n) {
+  NEED_OPEN();
+  HIPCALL(H.Memcpy(d, s, n, hipMemcpyDeviceToHost));
+  return AMDC_OK;
+}
+int amdc_memcpy_d2d(void *d, const void *s, size_t n) {
+  NEED_OPEN();
+  HIPCALL(H.Memcpy(d, s, n, hipMemcpyDeviceToDevice));
+  return AMDC_OK;
+}
+int amdc_memset(void *p, int v, size_t n) {
+  NEED_OPEN();
+  HIPCALL(H.Memset(p, v, n));
+  return AMDC_OK;
+}
+int amdc_sync(void) {
+  NEED_OPEN();
+  HIPCALL(H.DeviceSynchronize());
+  return AMDC_OK;
+}
+int amdc_event_create(void **ev) {
+  NEED_OPEN();
+  HIPCALL(H.EventCreate(ev));
+  return AMDC_OK;
+}
+int amdc_event_destroy(void *ev) {
+  NEED_OPEN();
+  HIPCALL(H.EventDestroy(ev));
+  return AMDC_OK;
+}
+int amdc_event_record(void *ev, void *stream) {
+  NEED_OPEN();
+  HIPCALL(H.EventRecord(ev, stream));
+  return AMDC_OK;
+}
+int amdc_event_elapsed_ms(float *ms, void *a, void *b) {
+  NEED_OPEN();
+  HIPCALL(H.EventSynchronize(b));
+  HIPCALL(H.EventElapsedTime(ms, a, b));
+  return AMDC_OK;
+}
+
+/* ---------------------------------------------------------------- launches */
+
+static int launch(int k, unsigned gx, unsigned gy, unsigned lds, void *stream, void **args) {
+  HIPCALL(H.ModuleLaunchKernel(g_k[k], gx, gy, 1, 256, 1, 1, lds, stream, args, NULL));
+  return AMDC_OK;
+}
+
+static int aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+int amdc_quant_q8(const float *x, uint8_t *q, uint32_t nb, uint32_t T, uint32_t xs, uint32_t qs, void *stream) {
+  NEED_OPEN();
+  if (!x || !q || !nb || !T) return fail(AMDC_EINVAL, "quant_q8: null pointer or empty (nb %u, T %u)", nb, T);
+  if (T > 1 && (xs % 4u || qs % 4u || xs < 128u * nb || qs < 40u * nb))
+    return fail(AMDC_EINVAL, "quant_q8: strides xs %u, qs %u too small or unaligned for nb %u", xs, qs, nb);
+  if (T > 65535u) return fail(AMDC_EINVAL, "quant_q8: T %u > 65535", T);
+  void *args[] = {&x, &q, &nb, &xs, &qs};
+  return launch(K_QUANT, (nb + 7u) / 8u, T, 0, stream, args);
+}
+
+static int check_mat(const char *op, int kind, const void *w, const uint8_t *xq, const float *y, uint32_t rows, uint32_t nb) {
+  if (kind != AMDC_KIND_Q4_0 && kind != AMDC_KIND_Q4_K) return fail(AMDC_EINVAL, "%s: kind %d", op, kind);
+  if (!w || !xq || !y) return fail(AMDC_EINVAL, "%s: null pointer", op);
+  if (!rows || !nb || rows >= (1u << 24) || nb >= (1u << 16)) return fail(AMDC_EINVAL, "%s: size %u rows x %u blocks", op, rows, nb);
+  if (kind == AMDC_KIND_Q4_K && nb % 8u) return fail(AMDC_EINVAL, "%s: Q4_K needs nb %% 8 == 0 (nb %u)", op, nb);
+  if (!aligned16(w) || !aligned16(xq)) return fail(AMDC_EINVAL, "%s: w and xq must be 16-byte aligned", op);
+  return AMDC_OK;
+}
+
+/* Lanes per row: the smallest power of two >= the super-groups of a row
+ * (one super-group per lane), 4..64. */
+static u32 gemv_lanes(u32 ng) {
+  if (t_lanes > 0) return (u32)t_lanes;
+  u32 L = 4;
+  while (L < ng && L < 64u) L <<= 1;
+  return L;
+}
+
+/* LDS of the GEMV: 320 bytes per super-group and vector (amdc_kernels.hip). */
+#define GEMV_LDS_T1 (150u * 1024u)
+#define GEMV_LDS_TN (64u * 1024u)
+
+static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
+                       const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  const u32 ng = amdc_ngroups(nb), L = gemv_lanes(ng), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
+  const u32 TT = T == 1u ? 1u : T <= 8u ? 8u : 16u;
+  u32 GC = (TT == 1u ? GEMV_LDS_T1 : GEMV_LDS_TN) / (320u * TT);
+  if (GC > ng) GC = ng;
+  const u32 lds = 320u * TT * GC;
+  const unsigned grid = t_wgs > 0 && (u32)t_wgs < nrg ? (unsigned)t_wgs : nrg;
+  int k;
+  if (TT == 1u) k = t_unroll == 1 ? (kind ? K_GEMV_Q4K_T1U1 : K_GEMV_Q4_T1U1) : (kind ? K_GEMV_Q4K_T1 : K_GEMV_Q4_T1);
+  else k = TT == 8u ? (kind ? K_GEMV_Q4K_T8 : K_GEMV_Q4_T8) : (kind ? K_GEMV_Q4K_T16 : K_GEMV_Q4_T16);
+  void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs, (void *)&L, &GC};
+  return launch(k, grid, 1, lds, stream, args);
+}
+
+int amdc_gemv_q4(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                 void *stream) {
+  NEED_OPEN();
+  int rc = check_mat("gemv_q4", AMDC_KIND_Q4_0, w, xq, y, rows, nb);
+  return rc ? rc : gemv_launch(AMDC_KIND_Q4_0, w, xq, y, rows, nb, bias, res, 1, 0, 0, 0, stream);
+}
+
+int amdc_gemv_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                  void *stream) {
+  NEED_OPEN();
+  int rc = check_mat("gemv_q4k", AMDC_KIND_Q4_K, w, xq, y, rows, nb);
+  return rc ? rc : gemv_launch(AMDC_KIND_Q4_K, w, xq, y, rows, nb, bias, res, 1, 0, 0, 0, stream);
+}
+
+static int check_t(const char *op, uint32_t nb, uint32_t rows, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, const float *res) {
+  if (!T) return fail(AMDC_EINVAL, "%s: T == 0", op);
+  if (T > 1u && (xs % 16u || xs < 40u * nb)) return fail(AMDC_EINVAL, "%s: xs %u (a multiple of 16, >= 40 nb = %u)", op, xs, 40u * nb);
+  if (T > 1u && ys < rows) return fail(AMDC_EINVAL, "%s: ys %u < rows %u", op, ys, rows);
+  if (T > 1u && res && rs < rows) return fail(AMDC_EINVAL, "%s: rs %u < rows %u", op, rs, rows);
+  return AMDC_OK;
+}
+
+static int gemv_t(int kind, const char *op, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
+                  const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  NEED_OPEN();
+  int rc = check_mat(op, kind, w, xq, y, rows, nb);
+  if (!rc) rc = check_t(op, nb, rows, T, xs, ys, rs, res);
+  for (u32 t0 = 0; !rc && t0 < T; t0 += 16u) { /* the weights read once per 16 vectors */
+    const u32 tn = T - t0 < 16u ? T - t0 : 16u;
+    rc = gemv_launch(kind, w, xq + (u64)t0 * xs, y + (u64)t0 * ys, rows, nb, bias, res ? res + (u64)t0 * rs : NULL, tn, xs, ys, rs,
+                     stream);
+  }
+  return rc;
+}
+
+int amdc_gemv_q4_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                   uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  return gemv_t(AMDC_KIND_Q4_0, "gemv_q4_t", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+}
+
+int amdc_gemv_q4k_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                    uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  return gemv_t(AMDC_KIND_Q4_K, "gemv_q4k_t", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+}
+
+int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                  uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  NEED_OPEN();
+  int rc = check_mat("gemm_q4k", AMDC_KIND_Q4_K, w, xq, y, rows, nb);
+  if (!rc) rc = check_t("gemm_q4k", nb, rows, T, xs, ys, rs, res);
+  if (rc) return rc;
+  if (T == 1u) xs = 40u * nb, ys = rows, rs = rows; /* one row: the strides are not used */
+  if (xs % 16u) return fail(AMDC_EINVAL, "gemm_q4k: xs %u not a multiple of 16", xs);
+  const u32 n = t_gemm > 0 ? (u32)t_gemm : T > 64u ? 128u : 64u;
+  const u64 grid = (u64)((rows + 63u) / 64u) * ((T + n - 1u) / n);
+  if (grid > 0x7FFFFFFFull) return fail(AMDC_EINVAL, "gemm_q4k: grid too large");
+  void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs};
+  return launch(n == 128u ? K_GEMM_N128 : K_GEMM_N64, (unsigned)grid, 1, 0, stream, args);
+}
+
+int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
+                 const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  NEED_OPEN();
+  if (T == 1u)
+    return kind == AMDC_KIND_Q4_K ? amdc_gemv_q4k(w, xq, y, rows, nb, bias, res, stream) : amdc_gemv_q4(w, xq, y, rows, nb, bias, res, stream);
+  if (kind == AMDC_KIND_Q4_K && (int)T >= t_gemm_min && nb % 8u == 0u) return amdc_gemm_q4k(w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+  return gemv_t(kind, "op_gemv", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+}
+
+int amdc_block_dots(int kind, const void *w, const uint8_t *xq, int32_t *out, uint32_t rows, uint32_t nb, void *stream) {
+  NEED_OPEN();
+  int rc = check_mat("block_dots", kind, w, xq, (const float *)out, rows, nb);
+  if (rc) return rc;
+  const u64 n = (u64)rows * nb;
+  if ((n + 255u) / 256u > 0x7FFFFFFFull) return fail(AMDC_EINVAL, "block_dots: too large");
+  void *args[] = {&w, &xq, &out, &rows, &nb};
+  return launch(kind == AMDC_KIND_Q4_K ? K_DOTS_Q4K : K_DOTS_Q4, (unsigned)((n + 255u) / 256u), 1, 0, stream, args);
+}

@@ -1,0 +1,403 @@
+// amdc_kernels.hip -- the HIP kernels of the quantized GEMV/GEMM path for
+// MI355X (gfx950, CDNA4, wave64). Built into a code object
+// (amdc_kernels.hsaco) that the C host (amdc_host.c) loads with
+// hipModuleLoad and launches by name, as the reference's host loads its
+// kernels (hanw/amd.c src/hip.c:102-107, 568-598).
+//
+// Kernels (grid x = workgroups, 256 threads each):
+//   amdc_quant_q8      Q8 activation quantization (src/cpu.c:36-53)
+//   amdc_gemv_{q4_0,q4_k}_t{1,8,16}
+//                      y = W x for T <= 1/8/16 Q8 vectors, the weights read
+//                      once per launch (ie_gemv_q4q8, ie_gemv_q4kq8, _tr8, _tr)
+//   amdc_gemm_q4_k_n{64,128}
+//                      the prefill chunk GEMM on int8 MFMA (ie_gemm_q4kr)
+//   amdc_dots_{q4_0,q4_k}
+//                      the per-block int32 dot products (parity check)
+// The weight layout is amdc_layout.h. The Q8 buffer is the reference's:
+// [int8 q[32 nb] | f32 d[nb] | u32 asum[nb]] (src/common.h:25-29).
+#include <hip/hip_runtime.h>
+
+#include "amdc_layout.h"
+
+typedef uint32_t u32;
+typedef uint64_t u64;
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+
+#define NT 256u
+
+// ------------------------------------------------------------------ helpers
+
+__device__ __forceinline__ float h2f(u32 h) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xFFFFu)); }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// The sum of v over aligned segments of L lanes (L = 4, 8, 16, 32 or 64);
+// every lane of a segment gets the sum. DPP inside rows of 16 lanes
+// (quad_perm xor 1, xor 2, row_half_mirror, row_mirror), then ds_swizzle
+// (xor 16) and ds_bpermute (xor 32).
+__device__ __forceinline__ float seg_sum(float v, u32 L) {
+  v += dpp<0xB1>(v); // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v); // quad_perm [2,3,0,1]
+  if (L >= 8u) v += dpp<0x141>(v);
+  if (L >= 16u) v += dpp<0x140>(v);
+  if (L >= 32u) v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+  if (L >= 64u) v += __shfl_xor(v, 32);
+  return v;
+}
+
+__device__ __forceinline__ int sdot4(u32 a, u32 b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
+
+// Sum over j < 32 of nibble_j * a_j: the 16 nibble bytes w (byte j: weight j
+// low, weight j + 16 high) against the 32 activation bytes alo (0..15), ahi
+// (16..31). The nibble bytes are 0..15, so the signed dot4 gives the same
+// integer as the reference's unsigned-by-signed one (core/ie_core.h:113-139,
+// 281-286).
+__device__ __forceinline__ int nib_dot(u32x4 w, u32x4 alo, u32x4 ahi) {
+  const u32 M = 0x0F0F0F0Fu;
+  int s = 0;
+  s = sdot4(w.x & M, alo.x, s);
+  s = sdot4((w.x >> 4) & M, ahi.x, s);
+  s = sdot4(w.y & M, alo.y, s);
+  s = sdot4((w.y >> 4) & M, ahi.y, s);
+  s = sdot4(w.z & M, alo.z, s);
+  s = sdot4((w.z >> 4) & M, ahi.z, s);
+  s = sdot4(w.w & M, alo.w, s);
+  s = sdot4((w.w >> 4) & M, ahi.w, s);
+  return s;
+}
+
+// The 6-bit scale and min of sub-block k of a Q4_K header (amdc_layout.h).
+__device__ __forceinline__ u32 q4k_sc(u32x4 h, u32 k) { return (u32)((((u64)h.z << 32) | h.y) >> (6u * k)) & 63u; }
+__device__ __forceinline__ u32 q4k_mn(u32x4 h, u32 k) { return (u32)((((u64)h.w << 32) | h.z) >> (16u + 6u * k)) & 63u; }
+__device__ __forceinline__ u32 hword(u32x4 h, u32 i) { return i == 0 ? h.x : i == 1 ? h.y : i == 2 ? h.z : h.w; }
+
+// ------------------------------------------------------------------ Q8 quantization
+
+// One 32-lane half of a wave per block of 32: amax by xor shuffles inside
+// the half, d = amax / 127 (IEEE division), q = roundf(x / d) (half away from
+// zero), 0 when d == 0; asum = the u32 sum of the 32 q. Grid: (ceil(nb / 8),
+// T); x and q of token t start t * xs and t * qs bytes in.
+extern "C" __global__ __launch_bounds__(256) void amdc_quant_q8(const float *__restrict__ x, uint8_t *__restrict__ q, u32 nb, u32 xs,
+                                                                u32 qs) {
+  x = (const float *)((const uint8_t *)x + (u64)blockIdx.y * xs);
+  q += (u64)blockIdx.y * qs;
+  const u32 b = blockIdx.x * 8u + (threadIdx.x >> 5), j = threadIdx.x & 31u;
+  if (b >= nb) return; // whole 32-lane halves leave together
+  const float v = x[32u * b + j];
+  float a = __builtin_fabsf(v);
+#pragma unroll
+  for (u32 o = 1; o < 32u; o <<= 1) a = __builtin_fmaxf(a, __shfl_xor(a, (int)o));
+  const float d = a / 127.0f;
+  const int qi = d != 0.0f ? (int)__builtin_roundf(v / d) : 0;
+  ((int8_t *)q)[32u * b + j] = (int8_t)qi;
+  u32 s = (u32)qi;
+#pragma unroll
+  for (u32 o = 1; o < 32u; o <<= 1) s += (u32)__shfl_xor((int)s, (int)o);
+  if (j == 0) {
+    ((float *)(q + 32u * nb))[b] = d;
+    ((u32 *)(q + 36u * nb))[b] = s;
+  }
+}
+
+// ------------------------------------------------------------------ GEMV
+
+// y[t][r] = sum over blocks of W[r] . x_t for the T (<= TT) Q8 vectors x_t
+// (xq + t * xs bytes), then the reference's epilogue (src/cpu.c:513-520):
+// y (+ bias[r]) then (res[t * rs + r] +) y. y[t][r] at y + t * ys.
+//
+// Work split: a wave holds 64 / L rows, L lanes per row (L = 4..64, a power
+// of two); lane l of a row owns the super-groups g = l, l + L, ... and for each
+// reads its 16-byte header and its 8 nibble blocks (9 loads of 128 bits). The
+// L lane sums of a row are added by seg_sum. A workgroup (4 waves) takes
+// 4 * 64 / L rows per pass and loops over row groups (blockIdx.x, + gridDim.x).
+//
+// The activations of GC super-groups (8 GC blocks) of all T vectors sit in
+// LDS, permuted as the weights (block 8g + k at k GC + g - g0), so that the
+// lanes of a row read consecutive 16-byte words: q low half, q high half, d,
+// asum: 40 bytes x 8 GC x T. When GC >= ng they are staged once per
+// workgroup; else once per chunk of GC super-groups and row group.
+//
+// Per block: Q4_0: dot = sum (q - 8) a = nib_dot - 8 asum (u32 wrap as the
+//   reference), acc += (d_w d_a) dot;
+// Q4_K: dq = nib_dot; acc = fma(-(dmin mn), d_a asum, fma((d sc) dq, d_a,
+//   acc)), the operations of src/cpu.c:111-112.
+template <int KIND, int TT, int U>
+__device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
+                                          u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 xs, u32 ys,
+                                          u32 rs, u32 L, u32 GC) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const u32 ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw;
+  const u32 nrg = (rows + rpg - 1u) / rpg;
+  const u64 RB = amdc_row_bytes(nb);
+  const u32 nblk = 8u * GC; // LDS blocks per vector
+  u32x4 *s_lo = (u32x4 *)smem;
+  u32x4 *s_hi = s_lo + (u64)TT * nblk;
+  float *s_d = (float *)(s_hi + (u64)TT * nblk);
+  u32 *s_as = (u32 *)(s_d + (u64)TT * nblk);
+
+  // stage the blocks of super-groups [g0, g1) of the T vectors
+  auto stage = [&](u32 g0, u32 g1) {
+    const u32 n = 8u * (g1 - g0), tot = T * n;
+    for (u32 i = tid; i < tot; i += NT) {
+      const u32 t = i / n, bl = i - t * n, b = 8u * g0 + bl;
+      const u32 p = t * nblk + (bl & 7u) * GC + (bl >> 3);
+      const uint8_t *xt = xq + (u64)t * xs;
+      u32x4 lo = (u32x4)(0u), hi = (u32x4)(0u);
+      float d = 0.0f;
+      u32 as = 0;
+      if (b < nb) {
+        lo = *(const u32x4 *)(xt + 32u * b);
+        hi = *(const u32x4 *)(xt + 32u * b + 16u);
+        d = ((const float *)(xt + 32u * nb))[b];
+        as = ((const u32 *)(xt + 36u * nb))[b];
+      }
+      s_lo[p] = lo;
+      s_hi[p] = hi;
+      s_d[p] = d;
+      s_as[p] = as;
+    }
+  };
+
+  const bool one = GC >= ng;
+  if (one) {
+    stage(0, ng);
+    __syncthreads();
+  }
+  for (u32 rg = blockIdx.x; rg < nrg; rg += gridDim.x) {
+    const u32 r = rg * rpg + wv * rpw + q;
+    const uint8_t *wr = W + (u64)(r < rows ? r : rows - 1u) * RB;
+    float acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[t] = 0.0f;
+    for (u32 g0 = 0; g0 < ng; g0 += GC) {
+      const u32 g1 = g0 + GC < ng ? g0 + GC : ng;
+      if (!one) {
+        __syncthreads();
+        stage(g0, g1);
+        __syncthreads();
+      }
+      for (u32 g = g0 + l; g < g1; g += U * L) {
+        u32x4 hd[U], nbk[U][8];
+        bool ok[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) { // all loads of the step first
+          const u32 gu = g + (u32)u * L;
+          ok[u] = gu < g1;
+          const u32 gc = ok[u] ? gu : g;
+          hd[u] = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_header_off(gc)));
+#pragma unroll
+          for (u32 k = 0; k < 8u; k++) nbk[u][k] = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_nib_off(ng, gc, k)));
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+          if (!ok[u]) continue;
+          const u32 gl = g + (u32)u * L - g0;
+          float dmn = 0.0f, dsc = 0.0f;
+          if (KIND == AMDC_Q4_K) dsc = h2f(hd[u].x), dmn = h2f(hd[u].x >> 16);
+#pragma unroll
+          for (u32 k = 0; k < 8u; k++) {
+            const u32 p = k * GC + gl;
+            float sw, mm = 0.0f;
+            if (KIND == AMDC_Q4_0) sw = h2f(hword(hd[u], k >> 1) >> (16u * (k & 1u)));
+            else sw = dsc * (float)q4k_sc(hd[u], k), mm = dmn * (float)q4k_mn(hd[u], k);
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+              if ((u32)t < T) {
+                const u32 pt = (u32)t * nblk + p;
+                const int dq = nib_dot(nbk[u][k], s_lo[pt], s_hi[pt]);
+                const float da = s_d[pt];
+                const u32 as = s_as[pt];
+                if (KIND == AMDC_Q4_0) {
+                  const int dot = (int)((u32)dq - 8u * as);
+                  acc[t] += (sw * da) * (float)dot;
+                } else {
+                  const float xa = da * (float)(int)as;
+                  acc[t] = __builtin_fmaf(-mm, xa, __builtin_fmaf(sw * (float)dq, da, acc[t]));
+                }
+              }
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+      if ((u32)t < T) {
+        const float v = seg_sum(acc[t], L);
+        if (l == 0u && r < rows) {
+          float o = v;
+          if (bias) o = o + bias[r];
+          if (res) o = res[(u64)t * rs + r] + o;
+          y[(u64)t * ys + r] = o;
+        }
+      }
+    }
+  }
+}
+
+#define GEMV_KERNEL(NAME, KIND, TT, U)                                                                                              \
+  extern "C" __global__ __launch_bounds__(256) void NAME(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,          \
+                                                         const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs, u32 L, \
+                                                         u32 GC) {                                                                  \
+    gemv_body<KIND, TT, U>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, L, GC);                                                    \
+  }
+GEMV_KERNEL(amdc_gemv_q4_0_t1, AMDC_Q4_0, 1, 2)
+GEMV_KERNEL(amdc_gemv_q4_k_t1, AMDC_Q4_K, 1, 2)
+GEMV_KERNEL(amdc_gemv_q4_0_t1u1, AMDC_Q4_0, 1, 1)
+GEMV_KERNEL(amdc_gemv_q4_k_t1u1, AMDC_Q4_K, 1, 1)
+GEMV_KERNEL(amdc_gemv_q4_0_t8, AMDC_Q4_0, 8, 1)
+GEMV_KERNEL(amdc_gemv_q4_k_t8, AMDC_Q4_K, 8, 1)
+GEMV_KERNEL(amdc_gemv_q4_0_t16, AMDC_Q4_0, 16, 1)
+GEMV_KERNEL(amdc_gemv_q4_k_t16, AMDC_Q4_K, 16, 1)
+
+// ------------------------------------------------------------------ block dots (parity)
+
+// out[r * nb + b] = the int32 dot of block b of row r with Q8 block b:
+// Q4_0 sum (q - 8) a (ie_q4q8_block), Q4_K sum q a (ie_q4k_dot), computed by
+// nib_dot as in the GEMV kernels. One thread per block.
+template <int KIND>
+__device__ __forceinline__ void dots_body(const uint8_t *W, const uint8_t *xq, int *out, u32 rows, u32 nb) {
+  const u64 i = (u64)blockIdx.x * NT + threadIdx.x;
+  if (i >= (u64)rows * nb) return;
+  const u32 r = (u32)(i / nb), b = (u32)(i - (u64)r * nb), ng = amdc_ngroups(nb);
+  const u32x4 w = *(const u32x4 *)(W + (u64)r * amdc_row_bytes(nb) + amdc_nib_off(ng, b >> 3, b & 7u));
+  const u32x4 lo = *(const u32x4 *)(xq + 32u * b), hi = *(const u32x4 *)(xq + 32u * b + 16u);
+  const int dq = nib_dot(w, lo, hi);
+  out[i] = KIND == AMDC_Q4_0 ? (int)((u32)dq - 8u * ((const u32 *)(xq + 36u * nb))[b]) : dq;
+}
+extern "C" __global__ __launch_bounds__(256) void amdc_dots_q4_0(const uint8_t *W, const uint8_t *xq, int *out, u32 rows, u32 nb) {
+  dots_body<AMDC_Q4_0>(W, xq, out, rows, nb);
+}
+extern "C" __global__ __launch_bounds__(256) void amdc_dots_q4_k(const uint8_t *W, const uint8_t *xq, int *out, u32 rows, u32 nb) {
+  dots_body<AMDC_Q4_K>(W, xq, out, rows, nb);
+}
+
+// ------------------------------------------------------------------ prefill GEMM
+
+// Y[t][r] = sum over sub-blocks b of (d sc)_rb da_tb dq_rtb - (dmin mn)_rb
+// da_tb asum_tb for Q4_K weights and T Q8 token rows (ie_gemm_q4kr), then
+// the epilogue. The integer dq (sum q a over the 32 weights of a sub-block)
+// comes exact from v_mfma_i32_16x16x32_i8; the min term, a small
+// contraction over the blocks, from v_mfma_f32_16x16x4_f32 in f32 (the
+// reference uses fp16 there: not within 1e-5).
+//
+// Workgroup tile: 64 rows x NTT tokens, 4 waves; wave w: rows 16w..16w+15,
+// all NTT tokens (NTT / 16 MFMA tiles). K loop: tile t of 8 super-groups
+// (header of each row staged in LDS), then plane k = 0..7 of the tile: the
+// 8 blocks b = 8 (8t + gl) + k, gl < gt, whose nibbles are 128 contiguous
+// bytes per row. MFMA operand mapping (lane = 16 h + i): A lane holds row i,
+// K bytes 8h..8h+7 = nibbles (h & 1) * 8 .. + 7, low nibble if h < 2 else
+// high; B lane holds token i, activation bytes 8h..8h+7: both sides use the
+// same K order. Output lane: rows 4h + v (v < 4), token i.
+template <int NTT>
+__device__ __forceinline__ void gemm_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y,
+                                          u32 rows, u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 xs,
+                                          u32 ys, u32 rs) {
+  constexpr u32 NJ = NTT / 16;
+  __shared__ __attribute__((aligned(16))) u32x4 sh_hdr[8][64];        // headers of the tile [gl][row]
+  __shared__ __attribute__((aligned(16))) u32x4 sh_a[8][64];          // plane nibbles [gl][row]
+  __shared__ __attribute__((aligned(16))) u32x4 sh_b[8][NTT][2];      // activations [gl][token][lo/hi]
+  __shared__ __attribute__((aligned(16))) float sh_da[8][NTT];        // d_a [gl][token]
+  __shared__ __attribute__((aligned(16))) float sh_xa[8][NTT];        // d_a * asum [gl][token]
+  __shared__ __attribute__((aligned(16))) float sh_s[8][64];          // d sc [gl][row]
+  __shared__ __attribute__((aligned(16))) float sh_m[8][64];          // -(dmin mn) [gl][row]
+
+  const u32 ng = amdc_ngroups(nb), ntile = (ng + 7u) >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
+  const u32 i16 = lane & 15u, h = lane >> 4;
+  const u32 ntt = (T + NTT - 1u) / NTT, tt = blockIdx.x % ntt, rt = blockIdx.x / ntt;
+  const u32 rbase = rt * 64u, tbase = tt * NTT;
+  const u64 RB = amdc_row_bytes(nb);
+
+  v4f acc[NJ];
+#pragma unroll
+  for (u32 j = 0; j < NJ; j++) acc[j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (u32 t = 0; t < ntile; t++) {
+    const u32 gt = ng - 8u * t < 8u ? ng - 8u * t : 8u;
+    __syncthreads();
+    for (u32 i = tid; i < 64u * gt; i += NT) { // the headers of the tile
+      const u32 gl = i >> 6, r = i & 63u, rr = rbase + r < rows ? rbase + r : rows - 1u;
+      sh_hdr[gl][r] = *(const u32x4 *)(W + (u64)rr * RB + amdc_header_off(8u * t + gl));
+    }
+    for (u32 k = 0; k < 8u; k++) {
+      __syncthreads();
+      for (u32 i = tid; i < 64u * gt; i += NT) { // plane k: nibbles and row scales
+        const u32 gl = i >> 6, r = i & 63u, rr = rbase + r < rows ? rbase + r : rows - 1u;
+        sh_a[gl][r] = *(const u32x4 *)(W + (u64)rr * RB + amdc_nib_off(ng, 8u * t + gl, k));
+        const u32x4 hd = sh_hdr[gl][r];
+        sh_s[gl][r] = h2f(hd.x) * (float)q4k_sc(hd, k);
+        sh_m[gl][r] = -(h2f(hd.x >> 16) * (float)q4k_mn(hd, k));
+      }
+      for (u32 i = tid; i < NTT * gt * 2u; i += NT) { // activations of blocks 8 (8t + gl) + k
+        const u32 half = i & 1u, tk = (i >> 1) % NTT, gl = (i >> 1) / NTT;
+        const u32 gtk = tbase + tk < T ? tbase + tk : T - 1u, b = 8u * (8u * t + gl) + k;
+        const uint8_t *xt = xq + (u64)gtk * xs;
+        sh_b[gl][tk][half] = *(const u32x4 *)(xt + 32u * b + 16u * half);
+        if (half == 0u) {
+          const float da = ((const float *)(xt + 32u * nb))[b];
+          sh_da[gl][tk] = da;
+          sh_xa[gl][tk] = da * (float)(int)((const u32 *)(xt + 36u * nb))[b];
+        }
+      }
+      __syncthreads();
+      for (u32 gl = 0; gl < gt; gl++) {
+        const u32x4 wa = sh_a[gl][16u * w + i16];
+        const u32 w0 = (h & 1u) ? wa.z : wa.x, w1 = (h & 1u) ? wa.w : wa.y, sft = (h >> 1) * 4u;
+        const long af = (long)(((u64)((w1 >> sft) & 0x0F0F0F0Fu) << 32) | ((w0 >> sft) & 0x0F0F0F0Fu));
+        const v4f s4 = *(const v4f *)&sh_s[gl][16u * w + 4u * h];
+#pragma unroll
+        for (u32 j = 0; j < NJ; j++) {
+          const u32x4 bv = sh_b[gl][16u * j + i16][h >> 1];
+          const long bf = (long)((h & 1u) ? (((u64)bv.w << 32) | bv.z) : (((u64)bv.y << 32) | bv.x));
+          const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, (v4i){0, 0, 0, 0}, 0, 0, 0);
+          const float da = sh_da[gl][16u * j + i16];
+#pragma unroll
+          for (u32 v = 0; v < 4u; v++) acc[j][v] = __builtin_fmaf(s4[v] * da, (float)c[v], acc[j][v]);
+        }
+      }
+      // the min term of the plane's blocks: K = gl (zero past gt)
+#pragma unroll
+      for (u32 kk = 0; kk < 8u; kk += 4u) {
+        const u32 gl = kk + h;
+        const float am = gl < gt ? sh_m[gl][16u * w + i16] : 0.0f;
+#pragma unroll
+        for (u32 j = 0; j < NJ; j++) {
+          const float bx = gl < gt ? sh_xa[gl][16u * j + i16] : 0.0f;
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(am, bx, acc[j], 0, 0, 0);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (u32 j = 0; j < NJ; j++) {
+    const u32 tk = tbase + 16u * j + i16;
+    if (tk >= T) continue;
+#pragma unroll
+    for (u32 v = 0; v < 4u; v++) {
+      const u32 r = rbase + 16u * w + 4u * h + v;
+      if (r < rows) {
+        float o = acc[j][v];
+        if (bias) o = o + bias[r];
+        if (res) o = res[(u64)tk * rs + r] + o;
+        y[(u64)tk * ys + r] = o;
+      }
+    }
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void amdc_gemm_q4_k_n128(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+                                                                     const float *bias, const float *res, u32 T, u32 xs, u32 ys,
+                                                                     u32 rs) {
+  gemm_body<128>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs);
+}
+extern "C" __global__ __launch_bounds__(256) void amdc_gemm_q4_k_n64(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys,
+                                                                    u32 rs) {
+  gemm_body<64>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs);
+}

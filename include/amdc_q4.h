@@ -1,0 +1,138 @@
+/* amdc_q4.h -- the C ABI of the MI355X (gfx950) quantized GEMV/GEMM path:
+ * libamdc_q4.so. Plain pointers and sizes; no HIP or ROCm header needed to
+ * use it (the library dlopens the HIP runtime, as the reference's host does,
+ * hanw/amd.c src/hip.c:1-4, 59-99).
+ *
+ * It replaces, for MAT_Q4 / MAT_Q4K matrices, the reference's
+ *  - load-time repack   repack_q4 / repack_q4k      (src/model.c:205, 246)
+ *  - GPU dispatch       OP_QUANT, OP_GEMV_Q4, OP_GEMV_Q4K in launch_op
+ *                                                    (src/hip.c:922-1026)
+ *  - device kernels     ie_quant_q8, ie_gemv_q4q8, ie_gemv_q4kq8(_tr, _tr8,
+ *                       _ts2), ie_gemm_q4kr          (kernels/ie_kernels.c)
+ * with the same argument meaning (rows, nb = cols / 32, bias, res, T, and
+ * the strides xs in bytes, ys / rs in floats) and the same Q8 activation
+ * buffer: [int8 q[32 nb] | float d[nb] | u32 asum[nb]] (src/common.h:25-29).
+ *
+ * Device pointers (w, xq, y, bias, res, x, q) are HIP device addresses, the
+ * stream a hipStream_t (NULL: the default stream). Launches are asynchronous.
+ * Every function returns 0 on success, else an AMDC_E* code; amdc_last_error()
+ * then says why (the reference instead prints and exit(1)s: src/common.c:6-14;
+ * a host that wants that calls ie_die(amdc_last_error())).
+ * Not re-entrant: one thread drives the library (as src/hip.c). */
+#ifndef AMDC_Q4_H
+#define AMDC_Q4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { AMDC_OK = 0, AMDC_EINVAL = 1, AMDC_ENOHIP = 2, AMDC_EHIP = 3, AMDC_ENOTOPEN = 4 };
+
+/* Matrix kinds: the reference's MAT_Q4 and MAT_Q4K (src/model.h:15). */
+enum { AMDC_KIND_Q4_0 = 0, AMDC_KIND_Q4_K = 3 };
+
+const char *amdc_last_error(void);
+
+/* ---------------------------------------------------------------- load time (host only) */
+
+/* Bytes of a repacked rows x cols matrix (cols % 32 == 0; Q4_K: cols % 256
+ * == 0): 144 * ceil(cols / 256) per row, the GGUF size when cols % 256 == 0. */
+size_t amdc_mat_bytes(int kind, uint32_t rows, uint32_t cols);
+
+/* GGUF Q4_0 (18-byte blocks) / Q4_K (144-byte super-blocks) bytes of a
+ * rows x cols matrix -> the CDNA4 layout in dst (amdc_mat_bytes bytes).
+ * Replace repack_q4 (src/model.c:205-219) and repack_q4k (src/model.c:
+ * 246-267); the nibble bytes are kept bit for bit, the scales are regrouped
+ * (6-bit Q4_K scales and mins unpacked as ggml's get_scale_min_k4,
+ * src/model.c:24-31, then repacked 8 per 6 bytes). Host memory only. */
+int amdc_repack_q4(const uint8_t *gguf, uint32_t rows, uint32_t cols, uint8_t *dst);
+int amdc_repack_q4k(const uint8_t *gguf, uint32_t rows, uint32_t cols, uint8_t *dst);
+
+/* ---------------------------------------------------------------- runtime */
+
+/* Load the HIP runtime (dlopen), select device 0 and load the kernel code
+ * object (NULL: amdc_kernels.hsaco next to this library). Replaces the
+ * hsaco load of gpu_open (src/hip.c:568-598). Fails cleanly (AMDC_ENOHIP)
+ * when there is no runtime or no device, like src/hip.c's "no GPU" path. */
+int amdc_open(const char *hsaco);
+void amdc_close(void);
+/* Number of compute units of the device (0 before amdc_open). */
+int amdc_cu_count(void);
+
+/* Plumbing for hosts without their own allocator (tests, bench). */
+int amdc_malloc(void **p, size_t n);
+int amdc_free(void *p);
+int amdc_memcpy_h2d(void *dst, const void *src, size_t n);
+int amdc_memcpy_d2h(void *dst, const void *src, size_t n);
+int amdc_memcpy_d2d(void *dst, const void *src, size_t n);
+int amdc_memset(void *p, int v, size_t n);
+int amdc_sync(void);
+/* HIP events, for timing on a stream. */
+int amdc_event_create(void **ev);
+int amdc_event_destroy(void *ev);
+int amdc_event_record(void *ev, void *stream);
+int amdc_event_elapsed_ms(float *ms, void *start, void *stop);
+
+/* ---------------------------------------------------------------- operators */
+
+/* Q8 quantization of T rows of 32 nb floats: x of token t at x + t * xs
+ * bytes, its Q8 buffer at q + t * qs bytes (xs, qs multiples of 16).
+ * Replaces OP_QUANT / ie_quant_q8(x, q, nb, xs, qs) (src/hip.c:922-927,
+ * kernels/ie_kernels.c:216-222); bitwise equal to cpu_quant_q8
+ * (src/cpu.c:36-53). */
+int amdc_quant_q8(const float *x, uint8_t *q, uint32_t nb, uint32_t T, uint32_t xs, uint32_t qs, void *stream);
+
+/* y = W x for one Q8 vector (decode), then y (+ bias[r]) then (res[r] +) y.
+ * Replace OP_GEMV_Q4 / ie_gemv_q4q8 and OP_GEMV_Q4K / ie_gemv_q4kq8
+ * (src/hip.c:928-933, 1023-1024; kernels/ie_kernels.c:310-347, 401-406)
+ * without the fused-RMSNorm tail (nw, ny, nq, eps, count). w: the repacked
+ * matrix (amdc_repack_q4 / _q4k), 16-byte aligned; xq 16-byte aligned. */
+int amdc_gemv_q4(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                 void *stream);
+int amdc_gemv_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                  void *stream);
+
+/* y_t = W x_t for T Q8 vectors (MTP verify, any T >= 1; the weights are
+ * read once per 16 vectors): x_t at xq + t * xs bytes, y_t at y + t * ys
+ * floats, res_t at res + t * rs floats. Replaces the multi-token branch of
+ * OP_GEMV_Q4K (ie_gemv_q4kq8_ts2 / _tr8 / _tr, src/hip.c:1004-1020); the
+ * Q4_0 form has no reference kernel (the reference runs OP_GEMV_Q4 per
+ * token, src/hip.c:1583-1588) and gives the same values as T calls of
+ * amdc_gemv_q4. */
+int amdc_gemv_q4_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                   uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
+int amdc_gemv_q4k_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                    uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
+
+/* The prefill chunk GEMM for Q4_K weights (nb % 8 == 0): the arguments of
+ * ie_gemm_q4kr (kernels/ie_kernels.c:1289, src/hip.c:998-1001). Integer dot
+ * products on int8 MFMA, exact; f32 outputs within 1e-5 of cpu_gemv_q4k per
+ * token row. */
+int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                  uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
+
+/* The dispatch of launch_op for OP_GEMV_Q4 / OP_GEMV_Q4K over T tokens
+ * (src/hip.c:928-1026): T == 1 -> the decode GEMV; Q4_K with T >=
+ * IE_GEMM_MIN (env, default 17) and nb % 8 == 0 -> the GEMM; else the
+ * multi-vector GEMV. kind: AMDC_KIND_Q4_0 or AMDC_KIND_Q4_K. */
+int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
+                 const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
+
+/* Parity probe: out[r * nb + b] = the int32 dot product of block b of row r
+ * with Q8 block b, as the GEMV kernels compute it: sum (q - 8) a for Q4_0
+ * (core/ie_core.h:161 ie_q4q8_block), sum q a for Q4_K (ie_q4k_dot, :281). */
+int amdc_block_dots(int kind, const void *w, const uint8_t *xq, int32_t *out, uint32_t rows, uint32_t nb, void *stream);
+
+/* Tuning knobs (0 = automatic): lanes per row of the GEMV (4..64, power of
+ * two), its loads unrolled (1 or 2), workgroups of a GEMV launch, tokens
+ * per GEMM workgroup (64 or 128). The same values are also read once from
+ * the environment: AMDC_GEMV_L, AMDC_GEMV_U, AMDC_GEMV_WG, AMDC_GEMM_N. */
+int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_tokens);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

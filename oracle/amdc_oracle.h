@@ -1,0 +1,75 @@
+/* amdc_oracle.h -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A CPU restatement of the reference's quantized GEMV path (hanw/amd.c,
+ * src/cpu.c and the integer spec core/ie_core.h), used as the checker for the
+ * HIP product path. Only tests/, __graft_entry__.smoke() and bench.py's CPU
+ * baseline may call it; the product library never links or loads it.
+ *
+ * Layouts are the reference's own:
+ *  - Q8 activation buffer of nb blocks (src/common.h:25-29):
+ *      [int8 q[32 nb] | float d[nb] | u32 asum[nb]]  (40 nb bytes)
+ *  - MAT_Q4  (src/model.h:17-21, core/ie_core.h:72-77): qw u32[rows*nb*4]
+ *      (byte j of a block: weight j in the low nibble, j+16 in the high),
+ *      qs f16[rows*nb]
+ *  - MAT_Q4K (src/model.h:25-29, core/ie_core.h:247-263): qw as MAT_Q4 (the
+ *      nibbles of each 32-weight sub-block in Q4_0 order), qs u16: (sc|mn<<8)
+ *      per sub-block, then (f16 d, f16 dmin) per 256-weight super-block.
+ */
+#ifndef AMDC_ORACLE_H
+#define AMDC_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+float or_f16_to_f32(uint16_t h);
+uint16_t or_f32_to_f16(float f);
+
+/* Q8 activation quantization (src/cpu.c:36-53). q gets 40*nb bytes. */
+void or_quant_q8(const float *x, uint8_t *q, uint32_t nb);
+
+/* GGUF -> the reference's MAT_Q4 / MAT_Q4K layouts (src/model.c:205-219,
+ * 246-267). qw: rows*nb*4 words; qs: rows*nb (Q4) or rows*nb + rows*nb/4
+ * (Q4K) u16 entries. */
+void or_repack_q4(const uint8_t *src, uint32_t rows, uint32_t nb, uint32_t *qw, uint16_t *qs);
+void or_repack_q4k(const uint8_t *src, uint32_t rows, uint32_t nb, uint32_t *qw, uint16_t *qs);
+size_t or_q4k_qs_n(uint32_t rows, uint32_t nb);
+
+/* y = W x in the reference's order (src/cpu.c:64-87, 93-118): lane l of a
+ * 32-lane wave adds the blocks l, l+32, ... of a row, then the lane sums are
+ * added by the tree 16, 8, 4, 2, 1. Bitwise equal to the reference. */
+void or_gemv_q4(const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32_t nb, const uint8_t *xq, float *y);
+void or_gemv_q4k(const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32_t nb, const uint8_t *xq, float *y);
+
+/* The fused epilogue of a GEMV row (src/cpu.c:513-520): y = y (+ bias[r])
+ * then (res[r] +) y. bias/res may be NULL. */
+void or_epilogue(float *y, uint32_t rows, const float *bias, const float *res);
+
+/* The integer block dots: out[r*nb + b] = ie_q4q8_block (Q4_0: sum (q-8) a,
+ * core/ie_core.h:161-167) or ie_q4k_dot (Q4_K: sum q a, :281-286), as int32. */
+void or_block_dots_q4(const uint32_t *qw, uint32_t rows, uint32_t nb, const uint8_t *xq, int32_t *out);
+void or_block_dots_q4k(const uint32_t *qw, uint32_t rows, uint32_t nb, const uint8_t *xq, int32_t *out);
+
+/* The same integer dots by brute force over the GGUF bytes (int64 element
+ * loop): an independent check of the two functions above. */
+void or_block_dots_gguf(int kind, const uint8_t *src, uint32_t rows, uint32_t nb, const uint8_t *xq, int32_t *out);
+
+/* GGUF dequantization of n weights from element `first` (src/model.c:98-107
+ * for Q4_0, :142-171 for Q4_K). kind: 2 = Q4_0, 12 = Q4_K (GGML ids). */
+void or_dequant(int kind, const uint8_t *src, uint64_t first, uint64_t n, float *out);
+
+/* A double-precision reference of y = W x straight from the GGUF bytes, and
+ * the sum of |terms| of each row (tests/kernel_test.c:59-80): y_ref, mag. */
+void or_gemv_f64(int kind, const uint8_t *src, uint32_t rows, uint32_t nb, const uint8_t *xq, double *y_ref, double *mag);
+
+/* Row-parallel runs of or_gemv_q4 / or_gemv_q4k over nthreads threads: the
+ * same per-row arithmetic, so the same bits. For the CPU baseline. */
+void or_gemv_q4_mt(const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32_t nb, const uint8_t *xq, float *y, int nthreads);
+void or_gemv_q4k_mt(const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32_t nb, const uint8_t *xq, float *y, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

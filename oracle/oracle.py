@@ -1,0 +1,187 @@
+"""TEST INFRASTRUCTURE ONLY: ctypes access to the CPU checkers.
+
+- ``liboracle.so``: the C restatement of the reference's CPU path
+  (``amdc_oracle.c``: hanw/amd.c src/cpu.c:36-118, src/model.c:205-267).
+- ``_ref/libref_cpu.so``: the reference's own src/{common,gguf,model,plan,cpu}.c
+  compiled where they lie (``Makefile``), present only where /root/reference
+  was (it travels with the tree as a built file).
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg use
+this module: it checks the HIP path and is never the thing measured or shipped.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GGML_Q4_0, GGML_Q4_K = 2, 12
+
+_P = C.c_void_p
+_U32 = C.c_uint32
+
+
+def _ptr(a):
+    return a.ctypes.data_as(_P)
+
+
+class Oracle:
+    def __init__(self, path=None):
+        path = path or os.path.join(HERE, "liboracle.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built (make -C oracle)")
+        L = self.lib = C.CDLL(path)
+        L.or_f16_to_f32.restype = C.c_float
+        L.or_f16_to_f32.argtypes = [C.c_uint16]
+        L.or_f32_to_f16.restype = C.c_uint16
+        L.or_f32_to_f16.argtypes = [C.c_float]
+        L.or_quant_q8.argtypes = [_P, _P, _U32]
+        for f in (L.or_repack_q4, L.or_repack_q4k):
+            f.argtypes = [_P, _U32, _U32, _P, _P]
+        for f in (L.or_gemv_q4, L.or_gemv_q4k):
+            f.argtypes = [_P, _P, _U32, _U32, _P, _P]
+        for f in (L.or_gemv_q4_mt, L.or_gemv_q4k_mt):
+            f.argtypes = [_P, _P, _U32, _U32, _P, _P, C.c_int]
+        L.or_epilogue.argtypes = [_P, _U32, _P, _P]
+        for f in (L.or_block_dots_q4, L.or_block_dots_q4k):
+            f.argtypes = [_P, _U32, _U32, _P, _P]
+        L.or_block_dots_gguf.argtypes = [C.c_int, _P, _U32, _U32, _P, _P]
+        L.or_dequant.argtypes = [C.c_int, _P, C.c_uint64, C.c_uint64, _P]
+        L.or_gemv_f64.argtypes = [C.c_int, _P, _U32, _U32, _P, _P, _P]
+        L.or_q4k_qs_n.restype = C.c_size_t
+        L.or_q4k_qs_n.argtypes = [_U32, _U32]
+
+    # -- Q8
+    def quant_q8(self, x):
+        """x: float32 [..., 32 nb] -> uint8 [..., 40 nb] Q8 buffers (src/cpu.c:36-53)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        n = x.shape[-1]
+        assert n % 32 == 0
+        nb = n // 32
+        flat = x.reshape(-1, n)
+        out = np.zeros((flat.shape[0], 40 * nb), dtype=np.uint8)
+        for i in range(flat.shape[0]):
+            self.lib.or_quant_q8(_ptr(flat[i]), _ptr(out[i]), nb)
+        return out.reshape(x.shape[:-1] + (40 * nb,))
+
+    # -- repack to the reference layouts
+    def repack(self, kind, src, rows, nb):
+        src = np.ascontiguousarray(src, dtype=np.uint8)
+        qw = np.zeros(rows * nb * 4, dtype=np.uint32)
+        if kind == GGML_Q4_0:
+            qs = np.zeros(rows * nb, dtype=np.uint16)
+            self.lib.or_repack_q4(_ptr(src), rows, nb, _ptr(qw), _ptr(qs))
+        else:
+            qs = np.zeros(self.lib.or_q4k_qs_n(rows, nb), dtype=np.uint16)
+            self.lib.or_repack_q4k(_ptr(src), rows, nb, _ptr(qw), _ptr(qs))
+        return qw, qs
+
+    def gemv(self, kind, qw, qs, rows, nb, xq, threads=1):
+        """y = W x in the reference's order, bit for bit (src/cpu.c:64-118)."""
+        xq = np.ascontiguousarray(xq, dtype=np.uint8)
+        y = np.zeros(rows, dtype=np.float32)
+        if threads > 1:
+            f = self.lib.or_gemv_q4_mt if kind == GGML_Q4_0 else self.lib.or_gemv_q4k_mt
+            f(_ptr(qw), _ptr(qs), rows, nb, _ptr(xq), _ptr(y), threads)
+        else:
+            f = self.lib.or_gemv_q4 if kind == GGML_Q4_0 else self.lib.or_gemv_q4k
+            f(_ptr(qw), _ptr(qs), rows, nb, _ptr(xq), _ptr(y))
+        return y
+
+    def epilogue(self, y, bias=None, res=None):
+        y = np.array(y, dtype=np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        r = None if res is None else np.ascontiguousarray(res, dtype=np.float32)
+        self.lib.or_epilogue(_ptr(y), y.size, _ptr(b) if b is not None else None, _ptr(r) if r is not None else None)
+        return y
+
+    def block_dots(self, kind, qw, rows, nb, xq):
+        out = np.zeros(rows * nb, dtype=np.int32)
+        f = self.lib.or_block_dots_q4 if kind == GGML_Q4_0 else self.lib.or_block_dots_q4k
+        f(_ptr(qw), rows, nb, _ptr(np.ascontiguousarray(xq)), _ptr(out))
+        return out.reshape(rows, nb)
+
+    def block_dots_gguf(self, kind, src, rows, nb, xq):
+        out = np.zeros(rows * nb, dtype=np.int32)
+        self.lib.or_block_dots_gguf(kind, _ptr(np.ascontiguousarray(src)), rows, nb, _ptr(np.ascontiguousarray(xq)), _ptr(out))
+        return out.reshape(rows, nb)
+
+    def dequant(self, kind, src, n):
+        out = np.zeros(n, dtype=np.float32)
+        self.lib.or_dequant(kind, _ptr(np.ascontiguousarray(src)), 0, n, _ptr(out))
+        return out
+
+    def gemv_f64(self, kind, src, rows, nb, xq):
+        """(y_ref float64, sum |terms| per row) from the GGUF bytes (tests/kernel_test.c:59-80)."""
+        y = np.zeros(rows, dtype=np.float64)
+        m = np.zeros(rows, dtype=np.float64)
+        self.lib.or_gemv_f64(kind, _ptr(np.ascontiguousarray(src)), rows, nb, _ptr(np.ascontiguousarray(xq)), _ptr(y), _ptr(m))
+        return y, m
+
+    def f16_to_f32(self, h):
+        return self.lib.or_f16_to_f32(int(h))
+
+    def f32_to_f16(self, f):
+        return self.lib.or_f32_to_f16(float(f))
+
+
+class RefCPU:
+    """The reference's own cpu.c / model.c (oracle/_ref/libref_cpu.so)."""
+
+    def __init__(self, path=None):
+        path = path or os.path.join(HERE, "_ref", "libref_cpu.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built (make -C oracle ref, needs /root/reference)")
+        L = self.lib = C.CDLL(path)
+        L.ref_quant_q8.argtypes = [_P, _P, _U32]
+        L.ref_mat_new.restype = _P
+        L.ref_mat_new.argtypes = [C.c_int, _P, _U32, _U32]
+        L.ref_mat_kind.argtypes = [_P]
+        L.ref_mat_copy.argtypes = [_P, _P, _P]
+        L.ref_mat_gemv.argtypes = [_P, _P, _P]
+        L.ref_mat_free.argtypes = [_P]
+
+    @staticmethod
+    def available(path=None):
+        return os.path.exists(path or os.path.join(HERE, "_ref", "libref_cpu.so"))
+
+    def quant_q8(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        nb = x.shape[-1] // 32
+        flat = x.reshape(-1, x.shape[-1])
+        out = np.zeros((flat.shape[0], 40 * nb), dtype=np.uint8)
+        for i in range(flat.shape[0]):
+            self.lib.ref_quant_q8(_ptr(flat[i]), _ptr(out[i]), nb)
+        return out.reshape(x.shape[:-1] + (40 * nb,))
+
+    def mat(self, ttype, src, rows, cols):
+        src = np.ascontiguousarray(src, dtype=np.uint8)
+        h = self.lib.ref_mat_new(ttype, _ptr(src), rows, cols)
+        if not h:
+            raise ValueError("not a MAT_Q4 / MAT_Q4K matrix")
+        return RefMat(self, h, ttype, rows, cols // 32)
+
+
+class RefMat:
+    def __init__(self, ref, h, ttype, rows, nb):
+        self.ref, self.h, self.ttype, self.rows, self.nb = ref, h, ttype, rows, nb
+
+    def arrays(self):
+        qw = np.zeros(self.rows * self.nb * 4, dtype=np.uint32)
+        ns = self.rows * self.nb if self.ttype == GGML_Q4_0 else self.rows * self.nb + self.rows * (self.nb // 8) * 2
+        qs = np.zeros(ns, dtype=np.uint16)
+        self.ref.lib.ref_mat_copy(self.h, _ptr(qw), _ptr(qs))
+        return qw, qs
+
+    def gemv(self, xq, y=None):
+        y = np.zeros(self.rows, dtype=np.float32) if y is None else y
+        self.ref.lib.ref_mat_gemv(self.h, _ptr(np.ascontiguousarray(xq)), _ptr(y))
+        return y
+
+    def free(self):
+        if self.h:
+            self.ref.lib.ref_mat_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.free()

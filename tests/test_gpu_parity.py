@@ -1,0 +1,211 @@
+"""Parity of the HIP path (libamdc_q4.so + amdc_kernels.hsaco, through the C
+ABI) with the oracle, on an MI355X.
+
+The bar: Q8 buffers, repacked nibbles and the
+per-block int32 dot products bit-exact; f32 outputs within 1e-5 relative
+error, measured as |y_gpu - y_oracle| / sum |terms| per row (the reference's
+tests/kernel_test.c:59-80 metric: summation order differs, the terms do not).
+"""
+import os
+
+import numpy as np
+import pytest
+
+from amdc import synth
+from oracle import GGML_Q4_0, GGML_Q4_K
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+CPUS = min(16, os.cpu_count() or 1)
+
+
+def ttype(kind):
+    return GGML_Q4_K if kind == synth.KIND_Q4_K else GGML_Q4_0
+
+
+def q8_stride(nb):
+    return (40 * nb + 255) // 256 * 256  # token rows of the Q8 buffer 256-aligned (src/model.c:1194)
+
+
+@pytest.fixture(autouse=True)
+def _tuning_reset(dev):
+    dev.set_tuning(0, 0, 0, 0)
+    yield
+    dev.set_tuning(0, 0, 0, 0)
+
+
+class Case:
+    """Seeded weights and T activation vectors, on the host and the device."""
+
+    def __init__(self, dev, orc, kind, rows, nb, T=1, seed=1, xscale=1.0, upload=True):
+        self.dev, self.orc, self.kind, self.rows, self.nb, self.T = dev, orc, kind, rows, nb, T
+        cols = 32 * nb
+        self.src = synth.gguf(kind, rows, cols, seed)
+        self.x = synth.activations(T, cols, seed + 1) * np.float32(xscale)
+        self.qw, self.qs = orc.repack(ttype(kind), self.src, rows, nb)
+        self.xq = orc.quant_q8(self.x)  # [T, 40 nb]
+        self.xs = q8_stride(nb)
+        if upload:
+            self.W = dev.DevBuf.of(dev.repack(kind, self.src, rows, cols))
+            self.X = dev.DevBuf.of(self.x)
+            self.Q = dev.DevBuf(T * self.xs)
+            self.Q.fill(0)
+            self.Y = dev.DevBuf(T * rows * 4)
+
+    def quant(self):
+        self.dev.quant_q8(self.X, self.Q, self.nb, self.T, 128 * self.nb, self.xs)
+        q = self.Q.download(np.uint8).reshape(self.T, self.xs)[:, :40 * self.nb]
+        return q
+
+    def y_oracle(self, t):
+        return self.orc.gemv(ttype(self.kind), self.qw, self.qs, self.rows, self.nb, self.xq[t], threads=CPUS)
+
+    def mag(self, t):
+        return self.orc.gemv_f64(ttype(self.kind), self.src, self.rows, self.nb, self.xq[t])[1]
+
+    def y_gpu(self):
+        return self.Y.download(np.float32).reshape(self.T, self.rows)
+
+
+def rel_err(y, yref, mag):
+    return float((np.abs(y.astype(np.float64) - yref.astype(np.float64)) / np.maximum(mag, 1e-30)).max())
+
+
+# ---------------------------------------------------------------- Q8
+
+@pytest.mark.parametrize("nb,T", [(1, 1), (3, 2), (33, 1), (128, 5), (544, 3)])
+def test_quant_q8_bitexact(dev, orc, nb, T):
+    c = Case(dev, orc, 0, 1, nb, T, seed=nb + T, xscale=2.0)
+    x = c.x.copy()
+    if nb >= 4:  # special blocks: zeros, a single nonzero, .5 ties, tiny values
+        x[0, 0:32] = 0
+        x[0, 32:64] = 0
+        x[0, 40] = -3.25
+        x[0, 64:96] = np.arange(-16, 16, dtype=np.float32) * np.float32(127.0 / 32.0)
+        x[0, 96:128] *= np.float32(1e-30)
+        c.X.upload(x)
+        c.xq = orc.quant_q8(x)
+    q = c.quant()
+    assert np.array_equal(q, c.xq.reshape(T, -1))
+
+
+# ---------------------------------------------------------------- integer dots
+
+@pytest.mark.parametrize("kind,rows,nb", [(0, 1, 1), (0, 7, 3), (0, 9, 11), (0, 13, 33), (0, 3, 100), (0, 2, 511), (0, 5, 128),
+                                          (3, 1, 8), (3, 7, 16), (3, 9, 40), (3, 5, 72), (3, 3, 544)])
+def test_block_dots_bitexact(dev, orc, kind, rows, nb):
+    c = Case(dev, orc, kind, rows, nb, seed=rows * 31 + nb, xscale=3.0)
+    c.quant()
+    out = dev.DevBuf(rows * nb * 4)
+    dev.block_dots(kind, c.W, c.Q, out, rows, nb)
+    got = out.download(np.int32).reshape(rows, nb)
+    assert np.array_equal(got, orc.block_dots(ttype(kind), c.qw, rows, nb, c.xq[0]))
+    assert np.array_equal(got, orc.block_dots_gguf(ttype(kind), c.src, rows, nb, c.xq[0]))
+
+
+# ---------------------------------------------------------------- decode GEMV (T = 1)
+
+SHAPES_Q4_0 = [(1, 1), (7, 3), (9, 11), (8, 32), (13, 33), (17, 36), (5, 64), (3, 100), (2, 511), (64, 128), (33, 344)]
+SHAPES_Q4_K = [(1, 8), (7, 16), (9, 40), (3, 64), (5, 72), (37, 160), (19, 544), (8, 192)]
+
+
+@pytest.mark.parametrize("kind,rows,nb", [(0, r, n) for r, n in SHAPES_Q4_0] + [(3, r, n) for r, n in SHAPES_Q4_K])
+def test_gemv_t1(dev, orc, kind, rows, nb):
+    c = Case(dev, orc, kind, rows, nb, seed=rows + 100 * nb)
+    assert np.array_equal(c.quant()[0], c.xq[0])
+    dev.gemv(kind, c.W, c.Q, c.Y, rows, nb)
+    err = rel_err(c.y_gpu()[0], c.y_oracle(0), c.mag(0))
+    assert err < TOL, err
+
+
+@pytest.mark.parametrize("lanes", [4, 8, 16, 32, 64])
+@pytest.mark.parametrize("unroll", [1, 2])
+@pytest.mark.parametrize("kind,rows,nb", [(0, 70, 344), (3, 45, 160), (3, 6, 544)])
+def test_gemv_t1_tunings(dev, orc, kind, rows, nb, lanes, unroll):
+    c = Case(dev, orc, kind, rows, nb, seed=lanes + unroll)
+    c.quant()
+    dev.set_tuning(lanes, unroll, 3, 0)  # 3 workgroups: each loops over several row groups
+    dev.gemv(kind, c.W, c.Q, c.Y, rows, nb)
+    err = rel_err(c.y_gpu()[0], c.y_oracle(0), c.mag(0))
+    assert err < TOL, err
+
+
+@pytest.mark.parametrize("kind", [0, 3])
+def test_gemv_epilogue_bias_res(dev, orc, kind):
+    rows, nb = 50, 64
+    c = Case(dev, orc, kind, rows, nb, seed=77)
+    c.quant()
+    g = np.random.default_rng(5)
+    bias, res = g.standard_normal(rows).astype(np.float32), g.standard_normal(rows).astype(np.float32)
+    B, R = dev.DevBuf.of(bias), dev.DevBuf.of(res)
+    dev.gemv(kind, c.W, c.Q, c.Y, rows, nb, bias=B, res=R)
+    want = orc.epilogue(c.y_oracle(0), bias, res)
+    err = rel_err(c.y_gpu()[0], want, c.mag(0) + np.abs(bias) + np.abs(res))
+    assert err < TOL, err
+    dev.gemv(kind, c.W, c.Q, c.Y, rows, nb, res=R)
+    err = rel_err(c.y_gpu()[0], orc.epilogue(c.y_oracle(0), None, res), c.mag(0) + np.abs(res))
+    assert err < TOL, err
+
+
+# ---------------------------------------------------------------- multi-vector GEMV (verify)
+
+@pytest.mark.parametrize("T", [2, 5, 8, 9, 16, 19])
+@pytest.mark.parametrize("kind,rows,nb", [(0, 40, 128), (3, 33, 160), (3, 21, 544)])
+def test_gemv_multi(dev, orc, kind, rows, nb, T):
+    c = Case(dev, orc, kind, rows, nb, T, seed=T * 13 + nb)
+    assert np.array_equal(c.quant(), c.xq)
+    res = np.random.default_rng(T).standard_normal((T, rows)).astype(np.float32)
+    R = dev.DevBuf.of(res)
+    dev.gemv_t(kind, c.W, c.Q, c.Y, rows, nb, T, c.xs, rows, rows, res=R)
+    y = c.y_gpu()
+    # and the single-vector kernel per token: the same values within the bound
+    Y1 = dev.DevBuf(rows * 4)
+    for t in range(T):
+        want = orc.epilogue(c.y_oracle(t), None, res[t])
+        mag = c.mag(t) + np.abs(res[t])
+        assert rel_err(y[t], want, mag) < TOL, t
+        dev.gemv(kind, c.W, c.Q.ptr + t * c.xs, Y1, rows, nb, res=R.ptr + 4 * t * rows)
+        assert rel_err(Y1.download(np.float32), want, mag) < TOL, t
+
+
+# ---------------------------------------------------------------- prefill GEMM
+
+@pytest.mark.parametrize("ntok", [64, 128])
+@pytest.mark.parametrize("rows,nb,T", [(1, 8, 17), (63, 16, 64), (64, 160, 65), (130, 40, 130), (300, 24, 256), (70, 544, 33)])
+def test_gemm_q4k(dev, orc, rows, nb, T, ntok):
+    c = Case(dev, orc, 3, rows, nb, T, seed=rows + T)
+    assert np.array_equal(c.quant(), c.xq)
+    g = np.random.default_rng(T)
+    bias = g.standard_normal(rows).astype(np.float32)
+    B = dev.DevBuf.of(bias)
+    dev.set_tuning(0, 0, 0, ntok)
+    dev.gemm_q4k(c.W, c.Q, c.Y, rows, nb, T, c.xs, rows, bias=B)
+    y = c.y_gpu()
+    for t in sorted({0, 1, T // 2, T - 1}):
+        want = orc.epilogue(c.y_oracle(t), bias, None)
+        assert rel_err(y[t], want, c.mag(t) + np.abs(bias)) < TOL, t
+    # all tokens against the oracle with the magnitude of token 0 scaled by the row norms
+    for t in range(T):
+        want = orc.epilogue(c.y_oracle(t), bias, None)
+        assert np.allclose(y[t], want, rtol=1e-4, atol=1e-4), t
+
+
+def test_op_gemv_dispatch(dev, orc):
+    rows, nb = 48, 64
+    for kind, T in ((0, 1), (3, 1), (0, 8), (3, 8), (0, 20), (3, 20)):
+        c = Case(dev, orc, kind, rows, nb, T, seed=T + kind)
+        c.quant()
+        dev.op_gemv(kind, c.W, c.Q, c.Y, rows, nb, T, c.xs, rows)
+        y = c.y_gpu()
+        for t in range(T):
+            assert rel_err(y[t], c.y_oracle(t), c.mag(t)) < TOL, (kind, T, t)
+
+
+def test_errors_do_not_launch(dev, orc):
+    c = Case(dev, orc, 3, 8, 16, seed=3)
+    with pytest.raises(dev.AmdcError):
+        dev.gemv_q4k(c.W, c.Q, c.Y, 8, 12)  # Q4_K nb % 8 != 0
+    with pytest.raises(dev.AmdcError):
+        dev.gemv_q4(c.W.ptr + 4, c.Q, c.Y, 8, 16)  # misaligned weights
+    with pytest.raises(dev.AmdcError):
+        dev.gemv_q4k_t(c.W, c.Q, c.Y, 8, 16, 2, 100, 8)  # xs not a multiple of 16
