@@ -52,6 +52,8 @@ ABI = {
     "amdc_op_gemv": (C.c_int, [C.c_int, _P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_block_dots": (C.c_int, [C.c_int, _P, _P, _P, _U32, _U32, _P]),
     "amdc_set_tuning": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int]),
+    "amdc_probe_read": (C.c_int, [_P, C.c_size_t, _P, _U32, _P]),
+    "amdc_probe_copy": (C.c_int, [_P, _P, C.c_size_t, _U32, _P]),
 }
 
 
@@ -243,3 +245,11 @@ def op_gemv(kind, w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stre
 
 def block_dots(kind, w, xq, out, rows, nb, stream=None):
     _check(lib().amdc_block_dots(kind, _p(w), _p(xq), _p(out), rows, nb, stream))
+
+
+def probe_read(src, nbytes, scratch, grid, stream=None):
+    _check(lib().amdc_probe_read(_p(src), nbytes, _p(scratch), grid, stream))
+
+
+def probe_copy(dst, src, nbytes, grid, stream=None):
+    _check(lib().amdc_probe_copy(_p(dst), _p(src), nbytes, grid, stream))

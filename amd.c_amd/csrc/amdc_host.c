@@ -158,12 +158,17 @@ enum {
   K_DOTS_Q4K,
   K_GEMM_N128,
   K_GEMM_N64,
+  K_GEMV_Q4_P1,
+  K_GEMV_Q4K_P1,
+  K_PROBE_READ,
+  K_PROBE_COPY,
   K_N
 };
 static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1",  "amdc_gemv_q4_k_t1",  "amdc_gemv_q4_0_t1u1",
                                        "amdc_gemv_q4_k_t1u1", "amdc_gemv_q4_0_t8",  "amdc_gemv_q4_k_t8",  "amdc_gemv_q4_0_t16",
                                        "amdc_gemv_q4_k_t16",  "amdc_dots_q4_0",     "amdc_dots_q4_k",     "amdc_gemm_q4_k_n128",
-                                       "amdc_gemm_q4_k_n64"};
+                                       "amdc_gemm_q4_k_n64",  "amdc_gemv_q4_0_p1",  "amdc_gemv_q4_k_p1",  "amdc_probe_read",
+                                       "amdc_probe_copy"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -371,6 +376,11 @@ static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uin
   if (GC > ng) GC = ng;
   const u32 lds = 320u * TT * GC;
   const unsigned grid = t_wgs > 0 && (u32)t_wgs < nrg ? (unsigned)t_wgs : nrg;
+  if (TT == 1u && t_unroll <= 0 && 320u * ng <= GEMV_LDS_T1) { /* the pipelined decode kernel */
+    const unsigned g1 = t_wgs > 0 && (u32)t_wgs < nrg ? (unsigned)t_wgs : nrg;
+    void *a1[] = {&w, &xq, &y, &rows, &nb, &bias, &res, (void *)&L};
+    return launch(kind ? K_GEMV_Q4K_P1 : K_GEMV_Q4_P1, g1, 1, 320u * ng, stream, a1);
+  }
   int k;
   if (TT == 1u) k = t_unroll == 1 ? (kind ? K_GEMV_Q4K_T1U1 : K_GEMV_Q4_T1U1) : (kind ? K_GEMV_Q4K_T1 : K_GEMV_Q4_T1);
   else k = TT == 8u ? (kind ? K_GEMV_Q4K_T8 : K_GEMV_Q4_T8) : (kind ? K_GEMV_Q4K_T16 : K_GEMV_Q4_T16);
@@ -455,4 +465,20 @@ int amdc_block_dots(int kind, const void *w, const uint8_t *xq, int32_t *out, ui
   if ((n + 255u) / 256u > 0x7FFFFFFFull) return fail(AMDC_EINVAL, "block_dots: too large");
   void *args[] = {&w, &xq, &out, &rows, &nb};
   return launch(kind == AMDC_KIND_Q4_K ? K_DOTS_Q4K : K_DOTS_Q4, (unsigned)((n + 255u) / 256u), 1, 0, stream, args);
+}
+
+int amdc_probe_read(const void *src, size_t nbytes, void *scratch, uint32_t grid, void *stream) {
+  NEED_OPEN();
+  if (!src || !scratch || nbytes % 16u || !aligned16(src) || !grid) return fail(AMDC_EINVAL, "probe_read: bad arguments");
+  u64 n = nbytes / 16u;
+  void *args[] = {&src, &n, &scratch};
+  return launch(K_PROBE_READ, grid, 1, 0, stream, args);
+}
+
+int amdc_probe_copy(void *dst, const void *src, size_t nbytes, uint32_t grid, void *stream) {
+  NEED_OPEN();
+  if (!src || !dst || nbytes % 16u || !aligned16(src) || !aligned16(dst) || !grid) return fail(AMDC_EINVAL, "probe_copy: bad arguments");
+  u64 n = nbytes / 16u;
+  void *args[] = {&src, &dst, &n};
+  return launch(K_PROBE_COPY, grid, 1, 0, stream, args);
 }

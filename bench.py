@@ -1,0 +1,292 @@
+"""Benchmark of the quantized GEMV/GEMM hot path on one MI355X.
+
+One "step" = one pass of the hot path over one batch-1 input through the
+configuration's GEMV set: for c1 (the headline, Llama-7B layer shapes, Q4_0)
+x -> Q8 -> q, k, v; Q8 -> o; Q8 -> gate, up; Q8 -> down; Q8 -> lm_head (5
+quantizations, 8 GEMVs), with weight copies rotated so that the weights
+streamed per step come from HBM (the copies total >= 2 GB, far above the 256
+MB Infinity Cache). value = weight bytes of the step (the reference's
+rows * nb * 18, src/hip.c:1831) / step time, inputs resident in HBM.
+
+Also measured, in "detail": c0 (one 4096x4096 Q4_0 GEMV), c2 (Q4_K 27B
+shapes), c3 (T = 8 verify GEMV, weights counted once) and c4 (the T = 256
+prefill GEMM, TOPS = 2 T rows cols / time), each from HIP events around every
+launch on the stream the kernels run on.
+
+CPU baseline: the reference's own cpu_gemv_q4 (oracle/_ref/libref_cpu.so,
+compiled from hanw/amd.c src/cpu.c), one core, on a bounded sample of the
+same c1 step (else the C restatement in oracle/, kind "port").
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "amd.c_amd"), os.path.join(ROOT, "oracle")]
+
+import amdc  # noqa: E402
+from amdc import synth  # noqa: E402
+
+METRIC = "Q4 GEMV weight-read GB/s (% of 8 TB/s HBM) at batch 1; prefill GEMM TOPS"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+ROTATE_BYTES = 2 << 30
+
+
+def wbytes(rows, cols):
+    return rows * (cols // 32) * 18
+
+
+def q8_stride(nb):
+    return (40 * nb + 255) // 256 * 256
+
+
+class Mats:
+    """copies x [matrices] of repacked weights on the device."""
+
+    def __init__(self, kind, shapes, seed, min_bytes=ROTATE_BYTES):
+        self.kind, self.shapes = kind, shapes
+        self.set_bytes = sum(wbytes(r, c) for _, r, c in shapes)
+        self.copies = max(1, -(-min_bytes // self.set_bytes))
+        host = [amdc.repack(kind, synth.gguf(kind, r, c, seed + i), r, c) for i, (_, r, c) in enumerate(shapes)]
+        self.dev = []
+        for _ in range(self.copies):
+            self.dev.append([amdc.DevBuf.of(h) for h in host])
+
+
+def events(n):
+    return [amdc.Event() for _ in range(n)]
+
+
+def time_step(step, steps, warmup):
+    """ms per step over `steps` back-to-back steps (after `warmup`), HIP events."""
+    for i in range(warmup):
+        step(i)
+    amdc.sync()
+    e0, e1 = amdc.Event(), amdc.Event()
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(steps):
+        step(warmup + i)
+    e1.record()
+    amdc.sync()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return e0.elapsed_ms(e1) / steps, wall
+
+
+def time_launches(launch, n, warmup):
+    """average ms of one launch, from event pairs around each of n launches."""
+    for i in range(warmup):
+        launch(i)
+    amdc.sync()
+    ev = events(2 * n)
+    for i in range(n):
+        ev[2 * i].record()
+        launch(warmup + i)
+        ev[2 * i + 1].record()
+    amdc.sync()
+    return float(np.mean([ev[2 * i].elapsed_ms(ev[2 * i + 1]) for i in range(n)]))
+
+
+# ---------------------------------------------------------------- c1 (headline) and c0 / c2 sets
+
+def gemv_set(cfg_name, steps, warmup, seed):
+    """Per-step and per-launch timing of a batch-1 GEMV set (c0, c1, c2)."""
+    cfg = synth.CONFIGS[cfg_name]
+    kind, shapes = cfg["kind"], cfg["shapes"]
+    M = Mats(kind, shapes, seed)
+    cols_max = max(c for _, _, c in shapes)
+    X = amdc.DevBuf.of(synth.activations(1, cols_max, seed + 99)[0])
+    Q = amdc.DevBuf(q8_stride(cols_max // 32))
+    Y = amdc.DevBuf(4 * max(r for _, r, _ in shapes))
+    # the quantization points of a layer: a new Q8 vector before a matrix whose input differs
+    # from the previous one's (q/k/v share, gate/up share)
+    share = {"k": "q", "v": "q", "up": "gate", "ffn_up": "ffn_gate"}
+
+    def gemv(ci, i):
+        _, r, c = shapes[i]
+        amdc.gemv(kind, M.dev[ci][i], Q, Y, r, c // 32)
+
+    def step(s):
+        ci = s % M.copies
+        for i, (name, r, c) in enumerate(shapes):
+            if name not in share:
+                amdc.quant_q8(X, Q, c // 32)
+            gemv(ci, i)
+
+    ms, wall = time_step(step, steps, warmup)
+    per = {}
+    tot_b, tot_ms = 0, 0.0
+    for i, (name, r, c) in enumerate(shapes):
+        amdc.quant_q8(X, Q, c // 32)
+        n = max(8, min(64, steps * 4))
+        t = time_launches(lambda j, i=i: gemv(j % M.copies, i), n, 4)
+        b = wbytes(r, c)
+        per[name] = {"rows": r, "cols": c, "us": round(t * 1e3, 3), "GB/s": round(b / t / 1e6, 1),
+                     "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4)}
+        tot_b += b
+        tot_ms += t
+    del M
+    return {"set_bytes": sum(wbytes(r, c) for _, r, c in shapes), "ms_per_step": ms, "wall_ms_per_step": wall,
+            "per_shape": per, "kernel_GBps": tot_b / tot_ms / 1e6, "kernel_us_total": tot_ms * 1e3}
+
+
+def verify_set(steps, seed):
+    """c3: T = 8 vectors against each matrix (weights read once per launch)."""
+    cfg = synth.CONFIGS["c3"]
+    T = cfg["T"]
+    out = {}
+    for i, (name, r, c, kind) in enumerate(cfg["shapes"]):
+        M = Mats(kind, [(name, r, c)], seed + i, min_bytes=1 << 30)
+        nb = c // 32
+        xs = q8_stride(nb)
+        X = amdc.DevBuf.of(synth.activations(T, c, seed + 50 + i))
+        Q = amdc.DevBuf(T * xs)
+        Y = amdc.DevBuf(4 * T * r)
+        amdc.quant_q8(X, Q, nb, T, 4 * c, xs)
+        t = time_launches(lambda j: amdc.gemv_t(kind, M.dev[j % M.copies][0], Q, Y, r, nb, T, xs, r), max(8, steps * 4), 4)
+        b = wbytes(r, c)
+        out[name] = {"rows": r, "cols": c, "T": T, "us": round(t * 1e3, 3), "GB/s": round(b / t / 1e6, 1),
+                     "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4)}
+        del M
+    return out
+
+
+def prefill_set(steps, seed):
+    """c4: the T = 256 prefill GEMM, TOPS = 2 T rows cols / time."""
+    cfg = synth.CONFIGS["c4"]
+    T = cfg["T"]
+    out = {}
+    for i, (name, r, c) in enumerate(cfg["shapes"]):
+        M = Mats(cfg["kind"], [(name, r, c)], seed + i, min_bytes=1 << 30)
+        nb = c // 32
+        xs = q8_stride(nb)
+        X = amdc.DevBuf.of(synth.activations(T, c, seed + 70 + i))
+        Q = amdc.DevBuf(T * xs)
+        Y = amdc.DevBuf(4 * T * r)
+        amdc.quant_q8(X, Q, nb, T, 4 * c, xs)
+        t = time_launches(lambda j: amdc.gemm_q4k(M.dev[j % M.copies][0], Q, Y, r, nb, T, xs, r), max(6, steps * 2), 2)
+        tops = 2.0 * T * r * c / t / 1e9
+        out[name] = {"rows": r, "cols": c, "T": T, "us": round(t * 1e3, 3), "TOPS": round(tops, 1),
+                     "int8_mfma_frac": round(tops / INT8_PEAK_TOPS, 4)}
+        del M
+    return out
+
+
+# ---------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(seed, budget_s=12.0):
+    """The c1 step on one host core: reference cpu_gemv_q4 (oracle/_ref) or the restatement."""
+    from oracle import GGML_Q4_0, Oracle, RefCPU
+
+    shapes = synth.CONFIGS["c1"]["shapes"]
+    x = synth.activations(1, 11008, seed + 99)[0]
+    srcs = [synth.gguf(synth.KIND_Q4_0, r, c, seed + i) for i, (_, r, c) in enumerate(shapes)]
+    if RefCPU.available():
+        ref = RefCPU()
+        kind = "reference"
+        mats = [ref.mat(GGML_Q4_0, s, r, c) for s, (_, r, c) in zip(srcs, shapes)]
+        xq = {c: ref.quant_q8(x[:c]) for _, _, c in shapes}
+
+        def run():
+            for m, (_, r, c) in zip(mats, shapes):
+                m.gemv(xq[c])
+    else:
+        orc = Oracle()
+        kind = "port"
+        arrs = [orc.repack(GGML_Q4_0, s, r, c // 32) for s, (_, r, c) in zip(srcs, shapes)]
+        xq = {c: orc.quant_q8(x[:c]) for _, _, c in shapes}
+
+        def run():
+            for (qw, qs), (_, r, c) in zip(arrs, shapes):
+                orc.gemv(GGML_Q4_0, qw, qs, r, c // 32, xq[c])
+    set_bytes = sum(wbytes(r, c) for _, r, c in shapes)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        run()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 50:
+            break
+    return {"value": round(set_bytes * n / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{n} c1 steps (8 Q4_0 GEMVs, {set_bytes / 1e6:.1f} MB of weights each) in {el:.1f} s, single thread, "
+                      f"{'cpu_gemv_q4 of hanw/amd.c src/cpu.c' if kind == 'reference' else 'oracle/amdc_oracle.c'}"}
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC summary, if any."""
+    p = os.path.join(ROOT, "profiles", "gemv_q4_0_c1_traffic.txt")
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        if line.startswith("traffic_bytes_per_launch_c1_avg:"):
+            return float(line.split(":")[1])
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--quick", action="store_true", help="headline only (no c0/c2/c3/c4 detail, no CPU baseline)")
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU; the GEMV path shards by rows across GPUs by design only "
+              "(see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    amdc.open_device()
+    print(f"bench: {amdc.cu_count()} CUs", file=sys.stderr, flush=True)
+
+    c1 = gemv_set("c1", a.steps, a.warmup, a.seed)
+    value = c1["set_bytes"] / (c1["ms_per_step"] * 1e-3) / 1e9
+    print(f"bench: c1 {value:.1f} GB/s per step, kernels {c1['kernel_GBps']:.1f} GB/s", file=sys.stderr, flush=True)
+    detail = {"c1": c1}
+    if not a.quick:
+        for name in ("c0", "c2"):
+            detail[name] = gemv_set(name, max(4, a.steps // 2), 2, a.seed + 1000)
+            print(f"bench: {name} kernels {detail[name]['kernel_GBps']:.1f} GB/s", file=sys.stderr, flush=True)
+        detail["c3"] = verify_set(a.steps, a.seed + 2000)
+        print(f"bench: c3 {json.dumps(detail['c3'])}", file=sys.stderr, flush=True)
+        detail["c4"] = prefill_set(a.steps, a.seed + 3000)
+        print(f"bench: c4 {json.dumps(detail['c4'])}", file=sys.stderr, flush=True)
+    cpu = None
+    if not a.quick and not a.no_cpu:
+        cpu = cpu_baseline(a.seed)
+        print(f"bench: cpu {json.dumps(cpu)}", file=sys.stderr, flush=True)
+    ach = c1["kernel_GBps"]
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(c1["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded: uniform nibbles, f16 |N(0,1)|*0.02 scales, N(0,1) activations)",
+        "config": {"workload": "c1: Llama-7B layer GEMV set, Q4_0 x Q8, batch 1 (q,k,v,o 4096x4096; gate,up 11008x4096; "
+                               "down 4096x11008; lm_head 32000x4096) + 5 Q8 quantizations per step",
+                   "weight_bytes_per_step": c1["set_bytes"], "rotation_copies_bytes": ROTATE_BYTES, "batch": 1},
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
+                     "kernel": "amdc_gemv_q4_0_t1", "bytes_per_launch_avg": c1["set_bytes"] / len(c1["per_shape"])},
+        "cpu_baseline": cpu,
+        "detail": detail,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -127,10 +127,19 @@ int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t 
 int amdc_block_dots(int kind, const void *w, const uint8_t *xq, int32_t *out, uint32_t rows, uint32_t nb, void *stream);
 
 /* Tuning knobs (0 = automatic): lanes per row of the GEMV (4..64, power of
- * two), its loads unrolled (1 or 2), workgroups of a GEMV launch, tokens
+ * two), the decode kernel (0: the pipelined one; 1 or 2: the multi-vector
+ * kernel with 1 or 2 super-groups of loads per step), workgroups of a GEMV
+ * launch, tokens
  * per GEMM workgroup (64 or 128). The same values are also read once from
  * the environment: AMDC_GEMV_L, AMDC_GEMV_U, AMDC_GEMV_WG, AMDC_GEMM_N. */
 int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_tokens);
+
+/* Bandwidth yardsticks (no reference counterpart): stream nbytes (a multiple
+ * of 16) through a plain read kernel (one u32 per workgroup may be written to
+ * scratch) or a copy kernel, grid workgroups of 256 threads. They give the
+ * achievable HBM rate and calibrate the FETCH_SIZE / WRITE_SIZE counters. */
+int amdc_probe_read(const void *src, size_t nbytes, void *scratch, uint32_t grid, void *stream);
+int amdc_probe_copy(void *dst, const void *src, size_t nbytes, uint32_t grid, void *stream);
 
 #ifdef __cplusplus
 }

@@ -119,7 +119,7 @@ def test_gemv_t1(dev, orc, kind, rows, nb):
 
 
 @pytest.mark.parametrize("lanes", [4, 8, 16, 32, 64])
-@pytest.mark.parametrize("unroll", [1, 2])
+@pytest.mark.parametrize("unroll", [0, 1, 2])
 @pytest.mark.parametrize("kind,rows,nb", [(0, 70, 344), (3, 45, 160), (3, 6, 544)])
 def test_gemv_t1_tunings(dev, orc, kind, rows, nb, lanes, unroll):
     c = Case(dev, orc, kind, rows, nb, seed=lanes + unroll)
@@ -181,13 +181,9 @@ def test_gemm_q4k(dev, orc, rows, nb, T, ntok):
     dev.set_tuning(0, 0, 0, ntok)
     dev.gemm_q4k(c.W, c.Q, c.Y, rows, nb, T, c.xs, rows, bias=B)
     y = c.y_gpu()
-    for t in sorted({0, 1, T // 2, T - 1}):
-        want = orc.epilogue(c.y_oracle(t), bias, None)
-        assert rel_err(y[t], want, c.mag(t) + np.abs(bias)) < TOL, t
-    # all tokens against the oracle with the magnitude of token 0 scaled by the row norms
     for t in range(T):
         want = orc.epilogue(c.y_oracle(t), bias, None)
-        assert np.allclose(y[t], want, rtol=1e-4, atol=1e-4), t
+        assert rel_err(y[t], want, c.mag(t) + np.abs(bias)) < TOL, t
 
 
 def test_op_gemv_dispatch(dev, orc):
