@@ -43,6 +43,13 @@ ABI = {
     "amdc_event_destroy": (C.c_int, [_P]),
     "amdc_event_record": (C.c_int, [_P, _P]),
     "amdc_event_elapsed_ms": (C.c_int, [C.POINTER(C.c_float), _P, _P]),
+    "amdc_stream_create": (C.c_int, [C.POINTER(_P)]),
+    "amdc_stream_destroy": (C.c_int, [_P]),
+    "amdc_stream_sync": (C.c_int, [_P]),
+    "amdc_graph_begin": (C.c_int, [_P]),
+    "amdc_graph_end": (C.c_int, [_P, C.POINTER(_P)]),
+    "amdc_graph_launch": (C.c_int, [_P, _P]),
+    "amdc_graph_destroy": (C.c_int, [_P]),
     "amdc_quant_q8": (C.c_int, [_P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_gemv_q4": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
     "amdc_gemv_q4k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
@@ -51,7 +58,7 @@ ABI = {
     "amdc_gemm_q4k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_op_gemv": (C.c_int, [C.c_int, _P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_block_dots": (C.c_int, [C.c_int, _P, _P, _P, _U32, _U32, _P]),
-    "amdc_set_tuning": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int]),
+    "amdc_set_tuning": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "amdc_probe_read": (C.c_int, [_P, C.c_size_t, _P, _U32, _P]),
     "amdc_probe_copy": (C.c_int, [_P, _P, C.c_size_t, _U32, _P]),
 }
@@ -98,8 +105,8 @@ def cu_count():
     return lib().amdc_cu_count()
 
 
-def set_tuning(lanes=0, unroll=0, wgs=0, gemm_tokens=0):
-    _check(lib().amdc_set_tuning(lanes, unroll, wgs, gemm_tokens))
+def set_tuning(lanes=0, unroll=0, wgs=0, gemm_kernel=0, gemm_ksplit=0):
+    _check(lib().amdc_set_tuning(lanes, unroll, wgs, gemm_kernel, gemm_ksplit))
 
 
 def sync():
@@ -175,6 +182,51 @@ class Event:
         try:
             if self.ev and _lib is not None:
                 _lib.amdc_event_destroy(self.ev)
+        except Exception:
+            pass
+
+
+class Stream:
+    """A HIP stream (default priority)."""
+
+    def __init__(self):
+        open_device()
+        p = _P()
+        _check(lib().amdc_stream_create(C.byref(p)))
+        self.s = p.value
+
+    def sync(self):
+        _check(lib().amdc_stream_sync(self.s))
+
+    def __del__(self):
+        try:
+            if self.s and _lib is not None:
+                _lib.amdc_stream_destroy(self.s)
+        except Exception:
+            pass
+
+
+class Graph:
+    """The operators that fn(stream) launches on `stream`, captured once; launch() replays them."""
+
+    def __init__(self, stream, fn):
+        self.stream = stream
+        _check(lib().amdc_graph_begin(stream.s))
+        try:
+            fn(stream.s)
+        finally:
+            p = _P()
+            rc = lib().amdc_graph_end(stream.s, C.byref(p))
+        _check(rc)
+        self.exec = p.value
+
+    def launch(self):
+        _check(lib().amdc_graph_launch(self.exec, self.stream.s))
+
+    def __del__(self):
+        try:
+            if self.exec and _lib is not None:
+                _lib.amdc_graph_destroy(self.exec)
         except Exception:
             pass
 

@@ -116,7 +116,8 @@ int amdc_repack_q4k(const uint8_t *src, uint32_t rows, uint32_t cols, uint8_t *d
 /* ---------------------------------------------------------------- HIP through dlopen */
 
 typedef int hipError_t;
-typedef void *hipModule_t, *hipFunction_t, *hipStream_t, *hipEvent_t;
+typedef void *hipModule_t, *hipFunction_t, *hipStream_t, *hipEvent_t, *hipGraph_t, *hipGraphExec_t;
+enum { hipStreamCaptureModeRelaxed = 2 };
 enum { hipMemcpyHostToDevice = 1, hipMemcpyDeviceToHost = 2, hipMemcpyDeviceToDevice = 3 };
 enum { hipDeviceAttributeMultiprocessorCount = 63 };
 
@@ -141,6 +142,15 @@ static struct {
   hipError_t (*EventSynchronize)(hipEvent_t);
   hipError_t (*EventElapsedTime)(float *, hipEvent_t, hipEvent_t);
   const char *(*GetErrorString)(hipError_t);
+  hipError_t (*StreamCreate)(hipStream_t *);
+  hipError_t (*StreamDestroy)(hipStream_t);
+  hipError_t (*StreamSynchronize)(hipStream_t);
+  hipError_t (*StreamBeginCapture)(hipStream_t, int);
+  hipError_t (*StreamEndCapture)(hipStream_t, hipGraph_t *);
+  hipError_t (*GraphInstantiate)(hipGraphExec_t *, hipGraph_t, void *, char *, size_t);
+  hipError_t (*GraphDestroy)(hipGraph_t);
+  hipError_t (*GraphLaunch)(hipGraphExec_t, hipStream_t);
+  hipError_t (*GraphExecDestroy)(hipGraphExec_t);
 } H;
 
 /* The kernels of amdc_kernels.hip. */
@@ -162,18 +172,26 @@ enum {
   K_GEMV_Q4K_P1,
   K_PROBE_READ,
   K_PROBE_COPY,
+  K_Q8_PREP,
+  K_GEMMH_M64_N128,
+  K_GEMMH_M64_N64,
+  K_GEMM_REDUCE,
   K_N
 };
 static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1",  "amdc_gemv_q4_k_t1",  "amdc_gemv_q4_0_t1u1",
                                        "amdc_gemv_q4_k_t1u1", "amdc_gemv_q4_0_t8",  "amdc_gemv_q4_k_t8",  "amdc_gemv_q4_0_t16",
                                        "amdc_gemv_q4_k_t16",  "amdc_dots_q4_0",     "amdc_dots_q4_k",     "amdc_gemm_q4_k_n128",
                                        "amdc_gemm_q4_k_n64",  "amdc_gemv_q4_0_p1",  "amdc_gemv_q4_k_p1",  "amdc_probe_read",
-                                       "amdc_probe_copy"};
+                                       "amdc_probe_copy",     "amdc_q8_prep",       "amdc_gemmh_m64_n128", "amdc_gemmh_m64_n64",
+                                       "amdc_gemm_reduce"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
 static int g_open, g_cus;
-static int t_lanes = -1, t_unroll = -1, t_wgs = -1, t_gemm = -1, t_gemm_min = -1;
+static int t_lanes = -1, t_unroll = -1, t_wgs = -1, t_gemm = -1, t_gemm_min = -1, t_ksplit = -1;
+/* The GEMM's device workspace (prepared activations, split-K partial sums): grown on demand. */
+static void *g_ws;
+static size_t g_ws_bytes;
 
 #define HIPCALL(x)                                                                               \
   do {                                                                                           \
@@ -218,6 +236,15 @@ static int hip_load(void) {
   SYM(EventSynchronize, "hipEventSynchronize");
   SYM(EventElapsedTime, "hipEventElapsedTime");
   SYM(GetErrorString, "hipGetErrorString");
+  SYM(StreamCreate, "hipStreamCreate");
+  SYM(StreamDestroy, "hipStreamDestroy");
+  SYM(StreamSynchronize, "hipStreamSynchronize");
+  SYM(StreamBeginCapture, "hipStreamBeginCapture");
+  SYM(StreamEndCapture, "hipStreamEndCapture");
+  SYM(GraphInstantiate, "hipGraphInstantiate");
+  SYM(GraphDestroy, "hipGraphDestroy");
+  SYM(GraphLaunch, "hipGraphLaunch");
+  SYM(GraphExecDestroy, "hipGraphExecDestroy");
 #undef SYM
   return AMDC_OK;
 }
@@ -246,13 +273,16 @@ int amdc_open(const char *hsaco) {
   if (t_lanes < 0) t_lanes = envi("AMDC_GEMV_L", 0);
   if (t_unroll < 0) t_unroll = envi("AMDC_GEMV_U", 0);
   if (t_wgs < 0) t_wgs = envi("AMDC_GEMV_WG", 0);
-  if (t_gemm < 0) t_gemm = envi("AMDC_GEMM_N", 0);
+  if (t_gemm < 0) t_gemm = envi("AMDC_GEMM_KERNEL", 0);
+  if (t_ksplit < 0) t_ksplit = envi("AMDC_GEMM_KSPLIT", 0);
   if (t_gemm_min < 0) t_gemm_min = envi("IE_GEMM_MIN", 17);
   g_open = 1;
   return AMDC_OK;
 }
 
 void amdc_close(void) {
+  if (g_open && g_ws) H.Free(g_ws);
+  g_ws = NULL, g_ws_bytes = 0;
   if (g_open && g_mod) H.ModuleUnload(g_mod);
   g_mod = NULL;
   g_open = 0;
@@ -260,13 +290,14 @@ void amdc_close(void) {
 
 int amdc_cu_count(void) { return g_open ? g_cus : 0; }
 
-int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_tokens) {
+int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kernel, int gemm_ksplit) {
   if (gemv_lanes && (gemv_lanes < 4 || gemv_lanes > 64 || (gemv_lanes & (gemv_lanes - 1))))
     return fail(AMDC_EINVAL, "gemv lanes %d: 4..64, a power of two", gemv_lanes);
   if (gemv_unroll < 0 || gemv_unroll > 2) return fail(AMDC_EINVAL, "gemv unroll %d: 0, 1 or 2", gemv_unroll);
-  if (gemm_tokens && gemm_tokens != 64 && gemm_tokens != 128) return fail(AMDC_EINVAL, "gemm tokens %d: 64 or 128", gemm_tokens);
+  if (gemm_kernel < 0 || gemm_kernel > 4) return fail(AMDC_EINVAL, "gemm kernel %d: 0..4", gemm_kernel);
+  if (gemm_ksplit < 0 || gemm_ksplit > 16) return fail(AMDC_EINVAL, "gemm ksplit %d: 0..16", gemm_ksplit);
   if (gemv_wgs < 0) return fail(AMDC_EINVAL, "gemv workgroups %d", gemv_wgs);
-  t_lanes = gemv_lanes, t_unroll = gemv_unroll, t_wgs = gemv_wgs, t_gemm = gemm_tokens;
+  t_lanes = gemv_lanes, t_unroll = gemv_unroll, t_wgs = gemv_wgs, t_gemm = gemm_kernel, t_ksplit = gemm_ksplit;
   return AMDC_OK;
 }
 
@@ -324,6 +355,50 @@ int amdc_event_elapsed_ms(float *ms, void *a, void *b) {
   NEED_OPEN();
   HIPCALL(H.EventSynchronize(b));
   HIPCALL(H.EventElapsedTime(ms, a, b));
+  return AMDC_OK;
+}
+
+/* Streams (default priority) and graphs: an op sequence captured once and
+ * replayed, so that the GPU runs it without a host launch per kernel. The
+ * operators record no memset, so their graphs hold kernel nodes only. */
+int amdc_stream_create(void **s) {
+  NEED_OPEN();
+  HIPCALL(H.StreamCreate(s));
+  return AMDC_OK;
+}
+int amdc_stream_destroy(void *s) {
+  NEED_OPEN();
+  HIPCALL(H.StreamDestroy(s));
+  return AMDC_OK;
+}
+int amdc_stream_sync(void *s) {
+  NEED_OPEN();
+  HIPCALL(H.StreamSynchronize(s));
+  return AMDC_OK;
+}
+int amdc_graph_begin(void *stream) {
+  NEED_OPEN();
+  if (!stream) return fail(AMDC_EINVAL, "graph_begin: capture needs a created stream, not the default stream");
+  HIPCALL(H.StreamBeginCapture(stream, hipStreamCaptureModeRelaxed));
+  return AMDC_OK;
+}
+int amdc_graph_end(void *stream, void **exec) {
+  NEED_OPEN();
+  hipGraph_t g = NULL;
+  HIPCALL(H.StreamEndCapture(stream, &g));
+  const hipError_t e = H.GraphInstantiate(exec, g, NULL, NULL, 0);
+  H.GraphDestroy(g);
+  if (e) return fail(AMDC_EHIP, "hipGraphInstantiate: %s (%d)", H.GetErrorString(e), e);
+  return AMDC_OK;
+}
+int amdc_graph_launch(void *exec, void *stream) {
+  NEED_OPEN();
+  HIPCALL(H.GraphLaunch(exec, stream));
+  return AMDC_OK;
+}
+int amdc_graph_destroy(void *exec) {
+  NEED_OPEN();
+  HIPCALL(H.GraphExecDestroy(exec));
   return AMDC_OK;
 }
 
@@ -433,6 +508,22 @@ int amdc_gemv_q4k_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, u
   return gemv_t(AMDC_KIND_Q4_K, "gemv_q4k_t", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
 }
 
+static int ws_reserve(size_t n) {
+  if (n <= g_ws_bytes) return AMDC_OK;
+  if (g_ws) HIPCALL(H.Free(g_ws));
+  g_ws = NULL, g_ws_bytes = 0;
+  n = (n + (1u << 20) - 1u) & ~(size_t)((1u << 20) - 1u);
+  HIPCALL(H.Malloc(&g_ws, n));
+  g_ws_bytes = n;
+  return AMDC_OK;
+}
+
+/* The f16-MFMA GEMM kernels: rows x tokens per workgroup. */
+static const struct {
+  int k;
+  u32 mr, nt, threads;
+} gh[2] = {{K_GEMMH_M64_N128, 64, 128, 256}, {K_GEMMH_M64_N64, 64, 64, 256}};
+
 int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                   uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
   NEED_OPEN();
@@ -441,11 +532,55 @@ int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uin
   if (rc) return rc;
   if (T == 1u) xs = 40u * nb, ys = rows, rs = rows; /* one row: the strides are not used */
   if (xs % 16u) return fail(AMDC_EINVAL, "gemm_q4k: xs %u not a multiple of 16", xs);
-  const u32 n = t_gemm > 0 ? (u32)t_gemm : T > 64u ? 128u : 64u;
-  const u64 grid = (u64)((rows + 63u) / 64u) * ((T + n - 1u) / n);
+  if (t_gemm == 1 || t_gemm == 2) { /* the int8-MFMA kernel */
+    const u32 n = t_gemm == 2 ? 128u : 64u;
+    const u64 grid = (u64)((rows + 63u) / 64u) * ((T + n - 1u) / n);
+    if (grid > 0x7FFFFFFFull) return fail(AMDC_EINVAL, "gemm_q4k: grid too large");
+    void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs};
+    return launch(n == 128u ? K_GEMM_N128 : K_GEMM_N64, (unsigned)grid, 1, 0, stream, args);
+  }
+  /* the f16-MFMA kernel: pick the tile and the K split that fill the CUs best */
+  const u32 ng = nb / 8u, cus = g_cus > 0 ? (u32)g_cus : 256u;
+  int v = t_gemm >= 3 ? t_gemm - 3 : -1;
+  u32 ks = t_ksplit > 0 ? (u32)t_ksplit : 0u;
+  if (v < 0 || !ks) {
+    double best = -1.0;
+    for (int c = 0; c < 2; c++) {
+      if (v >= 0 && c != v) continue;
+      for (u32 k = 1; k <= 4u; k <<= 1) {
+        if (ks && k != ks) continue;
+        if (k > 1u && ng < 8u * k) continue;
+        const u64 tiles = (u64)((rows + gh[c].mr - 1u) / gh[c].mr) * ((T + gh[c].nt - 1u) / gh[c].nt) * k;
+        const u64 slots = (u64)cus * 2u; /* workgroups resident at once */
+        const double rounds = (double)((tiles + slots - 1u) / slots), fill = (double)tiles / (rounds * (double)slots);
+        /* useful work per round slot, larger tiles reuse more; each split costs a reduction pass */
+        const double score = fill * (gh[c].nt >= 128u ? 1.0 : 0.85) /
+                             (1.0 + 0.04 * (double)(k - 1u));
+        if (score > best) best = score, v = c, ks = k;
+      }
+    }
+  }
+  if (ks > ng) ks = ng;
+  const u32 Tp = (T + 127u) / 128u * 128u, K = 32u * nb;
+  const size_t xh_b = (size_t)Tp * K * 2u, sc_b = (size_t)nb * Tp * 4u, part_b = ks > 1u ? (size_t)ks * T * rows * 4u : 0u;
+  rc = ws_reserve(xh_b + 2u * sc_b + part_b);
+  if (rc) return rc;
+  uint8_t *ws = g_ws;
+  void *xh = ws, *da = ws + xh_b, *xa = ws + xh_b + sc_b, *part = ks > 1u ? (void *)(ws + xh_b + 2u * sc_b) : NULL;
+  const u64 np = (u64)nb * Tp;
+  void *pa[] = {&xq, &nb, &T, &xs, &xh, &da, &xa, (void *)&Tp};
+  rc = launch(K_Q8_PREP, (unsigned)((np + 255u) / 256u), 1, 0, stream, pa);
+  if (rc) return rc;
+  const u64 grid = (u64)((rows + gh[v].mr - 1u) / gh[v].mr) * ((T + gh[v].nt - 1u) / gh[v].nt);
   if (grid > 0x7FFFFFFFull) return fail(AMDC_EINVAL, "gemm_q4k: grid too large");
-  void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs};
-  return launch(n == 128u ? K_GEMM_N128 : K_GEMM_N64, (unsigned)grid, 1, 0, stream, args);
+  void *ga[] = {&w, &xh, &da, &xa, &y, &rows, &nb, &bias, &res, &T, (void *)&Tp, &ys, &rs, &part};
+  HIPCALL(H.ModuleLaunchKernel(g_k[gh[v].k], (unsigned)grid, ks, 1, gh[v].threads, 1, 1, 0, stream, ga, NULL));
+  if (ks > 1u) {
+    const u64 n = (u64)rows * T;
+    void *ra[] = {&part, &ks, &y, &rows, &T, &bias, &res, &ys, &rs};
+    return launch(K_GEMM_REDUCE, (unsigned)((n + 255u) / 256u), 1, 0, stream, ra);
+  }
+  return AMDC_OK;
 }
 
 int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,

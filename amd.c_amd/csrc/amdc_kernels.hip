@@ -533,3 +533,293 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemm_q4_k_n64(const uint8
                                                                     u32 rs) {
   gemm_body<64>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs);
 }
+
+// ------------------------------------------------------------------ prefill GEMM on the f16 MFMA, exact integer sums
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+// The prefill activations as the GEMM reads them, from the Q8 buffers of T
+// tokens (token t at xq + t xs): xh[t][32 nb] = the int8 values as f16
+// (exact), da[b][t] = d_a, xa[b][t] = d_a * asum, for t < Tp; tokens T..Tp-1
+// are zeros. One thread per (token, block).
+extern "C" __global__ __launch_bounds__(256) void amdc_q8_prep(const uint8_t *__restrict__ xq, u32 nb, u32 T, u32 xs,
+                                                               _Float16 *__restrict__ xh, float *__restrict__ da, float *__restrict__ xa,
+                                                               u32 Tp) {
+  const u64 i = (u64)blockIdx.x * NT + threadIdx.x;
+  if (i >= (u64)nb * Tp) return;
+  const u32 t = (u32)(i / nb), b = (u32)(i - (u64)t * nb);
+  u32x4 o[4] = {(u32x4)(0u), (u32x4)(0u), (u32x4)(0u), (u32x4)(0u)};
+  float d = 0.0f, x = 0.0f;
+  if (t < T) {
+    const uint8_t *xt = xq + (u64)t * xs;
+    const u32x4 lo = *(const u32x4 *)(xt + 32u * b), hi = *(const u32x4 *)(xt + 32u * b + 16u);
+    const u32 w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+    for (u32 k = 0; k < 16u; k++) {
+      const int e0 = (int)(int8_t)(w[k >> 1] >> (16u * (k & 1u))), e1 = (int)(int8_t)(w[k >> 1] >> (16u * (k & 1u) + 8u));
+      const u32 v = (u32)__builtin_bit_cast(unsigned short, (_Float16)e0) | ((u32)__builtin_bit_cast(unsigned short, (_Float16)e1) << 16);
+      o[k >> 2][k & 3u] = v;
+    }
+    d = ((const float *)(xt + 32u * nb))[b];
+    x = d * (float)(int)((const u32 *)(xt + 36u * nb))[b];
+  }
+  u32x4 *dst = (u32x4 *)(xh + ((u64)t * nb + b) * 32u);
+#pragma unroll
+  for (u32 k = 0; k < 4u; k++) dst[k] = o[k];
+  da[(u64)b * Tp + t] = d;
+  xa[(u64)b * Tp + t] = x;
+}
+
+// Four nibbles (bytes 0..15 of n) -> two f16 pairs (1024 + q): each byte
+// below 0x64, the exponent byte of 1024 (v_perm_b32 picks the bytes).
+__device__ __forceinline__ void nib_to_h(u32 n, h2 &a, h2 &b) {
+  a = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, n, 0x04010400u));
+  b = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, n, 0x04030402u));
+}
+
+// The A operand of one 16 x 32 block tile: lane (row i, h) holds weights
+// 8h..8h+7 of its row's block, q sc as f16 (exact: q sc <= 945). w0, w1: the
+// 8 nibble bytes (h & 1) * 8 .. + 7 of the block; the low nibbles for h < 2.
+__device__ __forceinline__ h8 a_frag(u32 w0, u32 w1, u32 h, _Float16 sc) {
+  const u32 sft = (h >> 1) * 4u;
+  const u32 n0 = (w0 >> sft) & 0x0F0F0F0Fu, n1 = (w1 >> sft) & 0x0F0F0F0Fu;
+  h2 p0, p1, p2, p3;
+  nib_to_h(n0, p0, p1);
+  nib_to_h(n1, p2, p3);
+  const h2 s2 = {sc, sc}, c2 = {(_Float16)(-1024.0f) * sc, (_Float16)(-1024.0f) * sc}; // (1024 + q) sc - 1024 sc, one rounding
+  p0 = __builtin_elementwise_fma(p0, s2, c2);
+  p1 = __builtin_elementwise_fma(p1, s2, c2);
+  p2 = __builtin_elementwise_fma(p2, s2, c2);
+  p3 = __builtin_elementwise_fma(p3, s2, c2);
+  return (h8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// Y[t][r] for Q4_K weights and T tokens (the arguments of ie_gemm_q4kr plus the
+// prepared activations of amdc_q8_prep): per sub-block b of super-block g
+//   X_rtb = sum_k (q sc)_rk a_tk          v_mfma_f32_16x16x32_f16, exact
+//   tmp_rt += da_tb X_rtb                  one fma per element and block
+//   acc_rt += d_rg tmp_rt                  per super-block
+//   acc_rt -= sum_b (dmin mn)_rb xa_tb     v_mfma_f32_16x16x4_f32 per super-block
+// the reference's terms (d sc)_rb da_tb dq_rtb - (dmin mn)_rb da_tb asum_tb
+// regrouped, the integer sums sc dq kept exact.
+//
+// Workgroup: 4 waves, 2 x 2; wave (wm, wn): 32 rows (2 row tiles of 16) x
+// 16 NJ tokens; the workgroup tile is 64 rows x 32 NJ tokens. K in stages of
+// 4 blocks (half a super-block): the stage's f16 activations (and d_a) are
+// written to LDS (double buffer, one barrier per stage) from registers loaded
+// a stage ahead; each wave reads its weights' nibble bytes straight from
+// memory, also a stage ahead. Inside a block all MFMAs are issued before
+// their results are used, and the next block's operands are read meanwhile.
+// Split K (gridDim.y > 1): super-blocks [g0, g1) per split; the partial sums
+// go to part[split][t][r] and amdc_gemm_reduce adds them in split order.
+template <int NJ>
+__device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const _Float16 *__restrict__ xh, const float *__restrict__ DA,
+                                           const float *__restrict__ XA, float *__restrict__ y, u32 rows, u32 nb,
+                                           const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 Tp, u32 ys, u32 rs,
+                                           float *__restrict__ part) {
+  constexpr u32 NTH = 256u, MR = 64u, NTT = 32u * NJ;
+  constexpr u32 BSTR = 136u; // halves per token per stage: 4 blocks x 32 + 8 of padding
+  __shared__ __attribute__((aligned(16))) _Float16 sb[2][NTT * BSTR];
+  __shared__ __attribute__((aligned(16))) float sda[2][4][NTT];
+  const u32 ng = nb >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6, wm = w & 1u, wn = w >> 1;
+  const u32 i16 = lane & 15u, h = lane >> 4;
+  const u32 ntt = (T + NTT - 1u) / NTT, tt = blockIdx.x % ntt, rt = blockIdx.x / ntt;
+  const u32 rbase = rt * MR + 32u * wm, tbase = tt * NTT, twave = 16u * NJ * wn;
+  const u32 ks = blockIdx.y, nks = gridDim.y, g0 = ng * ks / nks, g1 = ng * (ks + 1u) / nks;
+  const u64 RB = amdc_row_bytes(nb), K = 32ull * nb;
+  const uint8_t *wr[2];
+#pragma unroll
+  for (u32 i = 0; i < 2u; i++) {
+    const u32 r = rbase + 16u * i + i16;
+    wr[i] = W + (u64)(r < rows ? r : rows - 1u) * RB;
+  }
+  v4f acc[2][NJ], tmp[2][NJ];
+#pragma unroll
+  for (u32 i = 0; i < 2u; i++)
+#pragma unroll
+    for (u32 j = 0; j < NJ; j++) acc[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f}, tmp[i][j] = acc[i][j];
+
+  // stage s = blocks 4s .. 4s+3 (super-block s / 2, its half s % 2)
+  constexpr u32 NCH = NTT * 16u / NTH; // 16-byte chunks of activations per thread (256 bytes per token)
+  constexpr u32 NDA = 4u * NTT / NTH;  // d_a values per thread
+  u32x4 rb[NCH];
+  float rd[NDA];
+  auto fetch = [&](u32 s) {
+#pragma unroll
+    for (u32 c = 0; c < NCH; c++) {
+      const u32 ch = tid + c * NTH, tk = ch >> 4, p16 = ch & 15u;
+      rb[c] = *(const u32x4 *)(xh + (u64)(tbase + tk) * K + 128u * s + 8u * p16);
+    }
+#pragma unroll
+    for (u32 c = 0; c < NDA; c++) {
+      const u32 e = tid + c * NTH;
+      rd[c] = DA[(u64)(4u * s + e / NTT) * Tp + tbase + e % NTT];
+    }
+  };
+  auto store = [&](u32 bf) {
+#pragma unroll
+    for (u32 c = 0; c < NCH; c++) {
+      const u32 ch = tid + c * NTH, tk = ch >> 4, p16 = ch & 15u;
+      *(u32x4 *)(&sb[bf][tk * BSTR + 8u * p16]) = rb[c];
+    }
+#pragma unroll
+    for (u32 c = 0; c < NDA; c++) {
+      const u32 e = tid + c * NTH;
+      sda[bf][e / NTT][e % NTT] = rd[c];
+    }
+  };
+  // the lane's 8 nibble bytes of the stage's 4 blocks, 2 row tiles
+  auto load_w = [&](u32 s, u32 (&wv)[4][2][2]) {
+    const u32 g = s >> 1, kb = 4u * (s & 1u);
+#pragma unroll
+    for (u32 bb = 0; bb < 4u; bb++)
+#pragma unroll
+      for (u32 i = 0; i < 2u; i++) {
+        const uint64_t v = *(const uint64_t *)(wr[i] + amdc_nib_off(ng, g, kb + bb) + 8u * (h & 1u));
+        wv[bb][i][0] = (u32)v, wv[bb][i][1] = (u32)(v >> 32);
+      }
+  };
+  auto load_g = [&](u32 g, u32x4 (&hd)[2], float (&xa)[2][NJ]) {
+#pragma unroll
+    for (u32 i = 0; i < 2u; i++) hd[i] = *(const u32x4 *)(wr[i] + amdc_header_off(g));
+#pragma unroll
+    for (u32 q = 0; q < 2u; q++)
+#pragma unroll
+      for (u32 j = 0; j < NJ; j++) xa[q][j] = XA[(u64)(8u * g + 4u * q + h) * Tp + tbase + twave + 16u * j + i16];
+  };
+
+  const u32 s0 = 2u * g0, s1 = 2u * g1;
+  u32 wv[4][2][2], wvn[4][2][2];
+  u32x4 hd[2], hdn[2];
+  float xa[2][NJ], xan[2][NJ];
+  if (s0 < s1) { // a split may own no super-block (then its partial sums are 0)
+    fetch(s0);
+    store(0);
+    load_w(s0, wv);
+    load_g(g0, hd, xa);
+  }
+  __syncthreads();
+  u32 bf = 0;
+  for (u32 s = s0; s < s1; s++) {
+    const u32 kb = 4u * (s & 1u);
+    const bool more = s + 1u < s1, opens = ((s + 1u) & 1u) == 0u;
+    if (more) { // the next stage's global data, in flight during this stage
+      fetch(s + 1u);
+      load_w(s + 1u, wvn);
+      if (opens) load_g((s + 1u) >> 1, hdn, xan);
+    }
+    const _Float16 *lb = &sb[bf][(twave + i16) * BSTR + 8u * h];
+    h8 bq[NJ];
+#pragma unroll
+    for (u32 j = 0; j < NJ; j++) bq[j] = *(const h8 *)(lb + 16u * j * BSTR);
+    h8 af[2];
+#pragma unroll
+    for (u32 i = 0; i < 2u; i++) af[i] = a_frag(wv[0][i][0], wv[0][i][1], h, (_Float16)(float)q4k_sc(hd[i], kb));
+#pragma unroll
+    for (u32 bb = 0; bb < 4u; bb++) {
+      v4f x[2][NJ];
+#pragma unroll
+      for (u32 j = 0; j < NJ; j++)
+#pragma unroll
+        for (u32 i = 0; i < 2u; i++) x[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bq[j], (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+      float dj[NJ];
+#pragma unroll
+      for (u32 j = 0; j < NJ; j++) dj[j] = sda[bf][bb][twave + 16u * j + i16];
+      if (bb + 1u < 4u) { // the next block's operands while the MFMAs run
+#pragma unroll
+        for (u32 j = 0; j < NJ; j++) bq[j] = *(const h8 *)(lb + 16u * j * BSTR + 32u * (bb + 1u));
+#pragma unroll
+        for (u32 i = 0; i < 2u; i++)
+          af[i] = a_frag(wv[bb + 1u][i][0], wv[bb + 1u][i][1], h, (_Float16)(float)q4k_sc(hd[i], kb + bb + 1u));
+      }
+#pragma unroll
+      for (u32 j = 0; j < NJ; j++)
+#pragma unroll
+        for (u32 i = 0; i < 2u; i++)
+#pragma unroll
+          for (u32 v = 0; v < 4u; v++) tmp[i][j][v] = __builtin_fmaf(dj[j], x[i][j][v], tmp[i][j][v]);
+    }
+    if (s & 1u) { // the super-block is done: d, and the min term
+#pragma unroll
+      for (u32 i = 0; i < 2u; i++) {
+        const float dmine = h2f(hd[i].x), dmn = h2f(hd[i].x >> 16);
+        float dv[4];
+#pragma unroll
+        for (u32 v = 0; v < 4u; v++) dv[v] = __shfl(dmine, (int)(4u * h + v));
+        float am[2];
+#pragma unroll
+        for (u32 q = 0; q < 2u; q++) am[q] = -(dmn * (float)q4k_mn(hd[i], 4u * q + h));
+#pragma unroll
+        for (u32 j = 0; j < NJ; j++) {
+#pragma unroll
+          for (u32 v = 0; v < 4u; v++) acc[i][j][v] = __builtin_fmaf(dv[v], tmp[i][j][v], acc[i][j][v]);
+          tmp[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (u32 q = 0; q < 2u; q++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(am[q], xa[q][j], acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+    if (more) {
+      store(bf ^ 1u); // that buffer was last read in the previous stage, before its barrier
+      __syncthreads();
+      bf ^= 1u;
+#pragma unroll
+      for (u32 bb = 0; bb < 4u; bb++)
+#pragma unroll
+        for (u32 i = 0; i < 2u; i++) wv[bb][i][0] = wvn[bb][i][0], wv[bb][i][1] = wvn[bb][i][1];
+      if (opens) {
+#pragma unroll
+        for (u32 i = 0; i < 2u; i++) hd[i] = hdn[i];
+#pragma unroll
+        for (u32 q = 0; q < 2u; q++)
+#pragma unroll
+          for (u32 j = 0; j < NJ; j++) xa[q][j] = xan[q][j];
+      }
+    }
+  }
+#pragma unroll
+  for (u32 i = 0; i < 2u; i++)
+#pragma unroll
+    for (u32 j = 0; j < NJ; j++) {
+      const u32 tk = tbase + twave + 16u * j + i16;
+      if (tk >= T) continue;
+#pragma unroll
+      for (u32 v = 0; v < 4u; v++) {
+        const u32 r = rbase + 16u * i + 4u * h + v;
+        if (r >= rows) continue;
+        if (part) {
+          part[((u64)ks * T + tk) * rows + r] = acc[i][j][v];
+        } else {
+          float o = acc[i][j][v];
+          if (bias) o = o + bias[r];
+          if (res) o = res[(u64)tk * rs + r] + o;
+          y[(u64)tk * ys + r] = o;
+        }
+      }
+    }
+}
+
+#define GEMMH_KERNEL(NAME, NJ)                                                                                                     \
+  extern "C" __global__ __launch_bounds__(256) void NAME(const uint8_t *W, const _Float16 *xh, const float *DA, const float *XA,  \
+                                                         float *y, u32 rows, u32 nb, const float *bias, const float *res, u32 T,  \
+                                                         u32 Tp, u32 ys, u32 rs, float *part) {                                   \
+    gemmh_body<NJ>(W, xh, DA, XA, y, rows, nb, bias, res, T, Tp, ys, rs, part);                                                   \
+  }
+GEMMH_KERNEL(amdc_gemmh_m64_n128, 4)
+GEMMH_KERNEL(amdc_gemmh_m64_n64, 2)
+
+// The split-K sums: y[t][r] = part[0][t][r] + part[1][t][r] + ... (in split
+// order), then the epilogue.
+extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *__restrict__ part, u32 nks, float *__restrict__ y, u32 rows,
+                                                                   u32 T, const float *__restrict__ bias, const float *__restrict__ res,
+                                                                   u32 ys, u32 rs) {
+  const u64 i = (u64)blockIdx.x * NT + threadIdx.x;
+  if (i >= (u64)rows * T) return;
+  const u32 t = (u32)(i / rows), r = (u32)(i - (u64)t * rows);
+  float o = part[i];
+  for (u32 k = 1; k < nks; k++) o += part[(u64)k * rows * T + i];
+  if (bias) o = o + bias[r];
+  if (res) o = res[(u64)t * rs + r] + o;
+  y[(u64)t * ys + r] = o;
+}

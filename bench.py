@@ -8,10 +8,14 @@ streamed per step come from HBM (the copies total >= 2 GB, far above the 256
 MB Infinity Cache). value = weight bytes of the step (the reference's
 rows * nb * 18, src/hip.c:1831) / step time, inputs resident in HBM.
 
-Also measured, in "detail": c0 (one 4096x4096 Q4_0 GEMV), c2 (Q4_K 27B
+The step is captured once per weight copy as a HIP graph and the graphs are
+replayed back to back (no host launch per kernel), timed by HIP events on
+their stream; each GEMV's own duration comes from a graph of that GEMV
+launched back to back over the weight copies (the roofline's "achieved"). Also measured, in "detail": c0 (one 4096x4096 Q4_0 GEMV), c2 (Q4_K 27B
 shapes), c3 (T = 8 verify GEMV, weights counted once) and c4 (the T = 256
 prefill GEMM, TOPS = 2 T rows cols / time), each from HIP events around every
-launch on the stream the kernels run on.
+launch on the stream the kernels run on (graphs of back-to-back launches over
+rotating weight copies, averaged).
 
 CPU baseline: the reference's own cpu_gemv_q4 (oracle/_ref/libref_cpu.so,
 compiled from hanw/amd.c src/cpu.c), one core, on a bounded sample of the
@@ -64,40 +68,39 @@ def events(n):
     return [amdc.Event() for _ in range(n)]
 
 
-def time_step(step, steps, warmup):
-    """ms per step over `steps` back-to-back steps (after `warmup`), HIP events."""
-    for i in range(warmup):
-        step(i)
-    amdc.sync()
-    e0, e1 = amdc.Event(), amdc.Event()
-    t0 = time.perf_counter()
-    e0.record()
-    for i in range(steps):
-        step(warmup + i)
-    e1.record()
-    amdc.sync()
-    wall = (time.perf_counter() - t0) * 1e3 / steps
-    return e0.elapsed_ms(e1) / steps, wall
+class Timer:
+    """HIP events on one stream around graph replays (the GPU runs a replay without host launches)."""
 
+    def __init__(self):
+        self.S = amdc.Stream()
 
-def time_launches(launch, n, warmup):
-    """average ms of one launch, from event pairs around each of n launches."""
-    for i in range(warmup):
-        launch(i)
-    amdc.sync()
-    ev = events(2 * n)
-    for i in range(n):
-        ev[2 * i].record()
-        launch(warmup + i)
-        ev[2 * i + 1].record()
-    amdc.sync()
-    return float(np.mean([ev[2 * i].elapsed_ms(ev[2 * i + 1]) for i in range(n)]))
+    def graph(self, fn):
+        return amdc.Graph(self.S, fn)
+
+    def replay_ms(self, graphs, reps, warmup=2):
+        """ms per replay of the graphs, launched round robin back to back (reps replays)."""
+        for i in range(warmup):
+            graphs[i % len(graphs)].launch()
+        self.S.sync()
+        e0, e1 = amdc.Event(), amdc.Event()
+        e0.record(self.S.s)
+        for i in range(reps):
+            graphs[i % len(graphs)].launch()
+        e1.record(self.S.s)
+        self.S.sync()
+        return e0.elapsed_ms(e1) / reps
+
+    def per_launch_ms(self, launch, n, reps=4):
+        """average ms of one launch: n launches (launch(i, stream)) in one graph, replayed."""
+        g = self.graph(lambda s: [launch(i, s) for i in range(n)])
+        return self.replay_ms([g], reps) / n
 
 
 # ---------------------------------------------------------------- c1 (headline) and c0 / c2 sets
 
-def gemv_set(cfg_name, steps, warmup, seed):
-    """Per-step and per-launch timing of a batch-1 GEMV set (c0, c1, c2)."""
+def gemv_set(cfg_name, steps, warmup, seed, timer):
+    """A batch-1 GEMV set (c0, c1, c2): the step as HIP graphs (one per weight copy), replayed;
+    and each GEMV alone, back to back over the weight copies in one graph."""
     cfg = synth.CONFIGS[cfg_name]
     kind, shapes = cfg["kind"], cfg["shapes"]
     M = Mats(kind, shapes, seed)
@@ -105,39 +108,36 @@ def gemv_set(cfg_name, steps, warmup, seed):
     X = amdc.DevBuf.of(synth.activations(1, cols_max, seed + 99)[0])
     Q = amdc.DevBuf(q8_stride(cols_max // 32))
     Y = amdc.DevBuf(4 * max(r for _, r, _ in shapes))
-    # the quantization points of a layer: a new Q8 vector before a matrix whose input differs
-    # from the previous one's (q/k/v share, gate/up share)
-    share = {"k": "q", "v": "q", "up": "gate", "ffn_up": "ffn_gate"}
+    # a new Q8 vector before a matrix whose input differs from the previous one's (q/k/v, gate/up share)
+    share = {"k", "v", "up", "ffn_up"}
 
-    def gemv(ci, i):
-        _, r, c = shapes[i]
-        amdc.gemv(kind, M.dev[ci][i], Q, Y, r, c // 32)
-
-    def step(s):
-        ci = s % M.copies
+    def step_ops(ci, s):
         for i, (name, r, c) in enumerate(shapes):
             if name not in share:
-                amdc.quant_q8(X, Q, c // 32)
-            gemv(ci, i)
+                amdc.quant_q8(X, Q, c // 32, stream=s)
+            amdc.gemv(kind, M.dev[ci][i], Q, Y, r, c // 32, stream=s)
 
-    ms, wall = time_step(step, steps, warmup)
-    per = {}
-    tot_b, tot_ms = 0, 0.0
+    graphs = [timer.graph(lambda s, ci=ci: step_ops(ci, s)) for ci in range(M.copies)]
+    ms = timer.replay_ms(graphs, steps, warmup)
+    del graphs
+    # each GEMV alone: one graph of back-to-back launches over the weight copies
+    per, tot = {}, 0.0
     for i, (name, r, c) in enumerate(shapes):
         amdc.quant_q8(X, Q, c // 32)
-        n = max(8, min(64, steps * 4))
-        t = time_launches(lambda j, i=i: gemv(j % M.copies, i), n, 4)
+        t = timer.per_launch_ms(lambda j, s, i=i, r=r, c=c: amdc.gemv(kind, M.dev[j % M.copies][i], Q, Y, r, c // 32, stream=s),
+                                M.copies, reps=max(2, steps // 4))
         b = wbytes(r, c)
         per[name] = {"rows": r, "cols": c, "us": round(t * 1e3, 3), "GB/s": round(b / t / 1e6, 1),
                      "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4)}
-        tot_b += b
-        tot_ms += t
+        tot += t
+    set_bytes = sum(wbytes(r, c) for _, r, c in shapes)
+    copies = M.copies
     del M
-    return {"set_bytes": sum(wbytes(r, c) for _, r, c in shapes), "ms_per_step": ms, "wall_ms_per_step": wall,
-            "per_shape": per, "kernel_GBps": tot_b / tot_ms / 1e6, "kernel_us_total": tot_ms * 1e3}
+    return {"set_bytes": set_bytes, "ms_per_step": ms, "per_shape": per, "kernel_GBps": set_bytes / tot / 1e6,
+            "kernel_us_total": tot * 1e3, "weight_copies": copies}
 
 
-def verify_set(steps, seed):
+def verify_set(steps, seed, timer):
     """c3: T = 8 vectors against each matrix (weights read once per launch)."""
     cfg = synth.CONFIGS["c3"]
     T = cfg["T"]
@@ -150,7 +150,7 @@ def verify_set(steps, seed):
         Q = amdc.DevBuf(T * xs)
         Y = amdc.DevBuf(4 * T * r)
         amdc.quant_q8(X, Q, nb, T, 4 * c, xs)
-        t = time_launches(lambda j: amdc.gemv_t(kind, M.dev[j % M.copies][0], Q, Y, r, nb, T, xs, r), max(8, steps * 4), 4)
+        t = timer.per_launch_ms(lambda j, s: amdc.gemv_t(kind, M.dev[j % M.copies][0], Q, Y, r, nb, T, xs, r, stream=s), M.copies)
         b = wbytes(r, c)
         out[name] = {"rows": r, "cols": c, "T": T, "us": round(t * 1e3, 3), "GB/s": round(b / t / 1e6, 1),
                      "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4)}
@@ -158,7 +158,7 @@ def verify_set(steps, seed):
     return out
 
 
-def prefill_set(steps, seed):
+def prefill_set(steps, seed, timer):
     """c4: the T = 256 prefill GEMM, TOPS = 2 T rows cols / time."""
     cfg = synth.CONFIGS["c4"]
     T = cfg["T"]
@@ -171,7 +171,8 @@ def prefill_set(steps, seed):
         Q = amdc.DevBuf(T * xs)
         Y = amdc.DevBuf(4 * T * r)
         amdc.quant_q8(X, Q, nb, T, 4 * c, xs)
-        t = time_launches(lambda j: amdc.gemm_q4k(M.dev[j % M.copies][0], Q, Y, r, nb, T, xs, r), max(6, steps * 2), 2)
+        amdc.gemm_q4k(M.dev[0][0], Q, Y, r, nb, T, xs, r)  # sizes the library's workspace before the capture
+        t = timer.per_launch_ms(lambda j, s: amdc.gemm_q4k(M.dev[j % M.copies][0], Q, Y, r, nb, T, xs, r, stream=s), M.copies, reps=2)
         tops = 2.0 * T * r * c / t / 1e9
         out[name] = {"rows": r, "cols": c, "T": T, "us": round(t * 1e3, 3), "TOPS": round(tops, 1),
                      "int8_mfma_frac": round(tops / INT8_PEAK_TOPS, 4)}
@@ -238,6 +239,8 @@ def main():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--quick", action="store_true", help="headline only (no c0/c2/c3/c4 detail, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="first run the probe copy kernel over 256 MiB 3 times (the FETCH_SIZE / WRITE_SIZE yardstick)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU; the GEMV path shards by rows across GPUs by design only "
@@ -245,18 +248,27 @@ def main():
         sys.exit(2)
     amdc.open_device()
     print(f"bench: {amdc.cu_count()} CUs", file=sys.stderr, flush=True)
+    if a.calibrate:
+        n = 256 << 20
+        A, B = amdc.DevBuf(n), amdc.DevBuf(n)
+        A.fill(1)
+        for _ in range(3):
+            amdc.probe_copy(B, A, n, 4096)
+        amdc.sync()
+        del A, B
 
-    c1 = gemv_set("c1", a.steps, a.warmup, a.seed)
+    timer = Timer()
+    c1 = gemv_set("c1", a.steps, a.warmup, a.seed, timer)
     value = c1["set_bytes"] / (c1["ms_per_step"] * 1e-3) / 1e9
     print(f"bench: c1 {value:.1f} GB/s per step, kernels {c1['kernel_GBps']:.1f} GB/s", file=sys.stderr, flush=True)
     detail = {"c1": c1}
     if not a.quick:
         for name in ("c0", "c2"):
-            detail[name] = gemv_set(name, max(4, a.steps // 2), 2, a.seed + 1000)
+            detail[name] = gemv_set(name, a.steps, 2, a.seed + 1000, timer)
             print(f"bench: {name} kernels {detail[name]['kernel_GBps']:.1f} GB/s", file=sys.stderr, flush=True)
-        detail["c3"] = verify_set(a.steps, a.seed + 2000)
+        detail["c3"] = verify_set(a.steps, a.seed + 2000, timer)
         print(f"bench: c3 {json.dumps(detail['c3'])}", file=sys.stderr, flush=True)
-        detail["c4"] = prefill_set(a.steps, a.seed + 3000)
+        detail["c4"] = prefill_set(a.steps, a.seed + 3000, timer)
         print(f"bench: c4 {json.dumps(detail['c4'])}", file=sys.stderr, flush=True)
     cpu = None
     if not a.quick and not a.no_cpu:

@@ -75,6 +75,17 @@ int amdc_event_create(void **ev);
 int amdc_event_destroy(void *ev);
 int amdc_event_record(void *ev, void *stream);
 int amdc_event_elapsed_ms(float *ms, void *start, void *stop);
+/* Streams (default priority) and HIP graphs: operators launched on a stream
+ * between amdc_graph_begin and amdc_graph_end are captured (kernel nodes
+ * only: the operators record no memset) and replayed by amdc_graph_launch
+ * with one host call. The device pointers of a graph are fixed at capture. */
+int amdc_stream_create(void **stream);
+int amdc_stream_destroy(void *stream);
+int amdc_stream_sync(void *stream);
+int amdc_graph_begin(void *stream);
+int amdc_graph_end(void *stream, void **exec);
+int amdc_graph_launch(void *exec, void *stream);
+int amdc_graph_destroy(void *exec);
 
 /* ---------------------------------------------------------------- operators */
 
@@ -108,9 +119,13 @@ int amdc_gemv_q4k_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, u
                     uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 
 /* The prefill chunk GEMM for Q4_K weights (nb % 8 == 0): the arguments of
- * ie_gemm_q4kr (kernels/ie_kernels.c:1289, src/hip.c:998-1001). Integer dot
- * products on int8 MFMA, exact; f32 outputs within 1e-5 of cpu_gemv_q4k per
- * token row. */
+ * ie_gemm_q4kr (kernels/ie_kernels.c:1289, src/hip.c:998-1001). The integer
+ * sums of the sub-blocks are exact: by default on the f16 MFMA with the 6-bit
+ * scale folded into the weights (q sc <= 945 and the int8 activations are f16
+ * integers; every partial sum is an integer below 2^24), or on the int8 MFMA
+ * (tuning); f32 outputs within 1e-5 of cpu_gemv_q4k per token row. Uses a
+ * device workspace that the library allocates on the first call of a size
+ * (call once outside graph capture before capturing). */
 int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                   uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 
@@ -127,12 +142,13 @@ int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t 
 int amdc_block_dots(int kind, const void *w, const uint8_t *xq, int32_t *out, uint32_t rows, uint32_t nb, void *stream);
 
 /* Tuning knobs (0 = automatic): lanes per row of the GEMV (4..64, power of
- * two), the decode kernel (0: the pipelined one; 1 or 2: the multi-vector
- * kernel with 1 or 2 super-groups of loads per step), workgroups of a GEMV
- * launch, tokens
- * per GEMM workgroup (64 or 128). The same values are also read once from
- * the environment: AMDC_GEMV_L, AMDC_GEMV_U, AMDC_GEMV_WG, AMDC_GEMM_N. */
-int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_tokens);
+ * two); the decode kernel (0: the pipelined one; 1 or 2: the multi-vector
+ * kernel with 1 or 2 super-groups of loads per step); workgroups of a GEMV
+ * launch; the GEMM kernel (1, 2: int8 MFMA with 64 or 128 tokens per
+ * workgroup; 3, 4: f16 MFMA, rows x tokens 64x128, 64x64);
+ * the GEMM's K split (1..16). Also read once from the environment:
+ * AMDC_GEMV_L, AMDC_GEMV_U, AMDC_GEMV_WG, AMDC_GEMM_KERNEL, AMDC_GEMM_KSPLIT. */
+int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kernel, int gemm_ksplit);
 
 /* Bandwidth yardsticks (no reference counterpart): stream nbytes (a multiple
  * of 16) through a plain read kernel (one u32 per workgroup may be written to

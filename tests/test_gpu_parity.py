@@ -29,9 +29,9 @@ def q8_stride(nb):
 
 @pytest.fixture(autouse=True)
 def _tuning_reset(dev):
-    dev.set_tuning(0, 0, 0, 0)
+    dev.set_tuning()
     yield
-    dev.set_tuning(0, 0, 0, 0)
+    dev.set_tuning()
 
 
 class Case:
@@ -124,7 +124,7 @@ def test_gemv_t1(dev, orc, kind, rows, nb):
 def test_gemv_t1_tunings(dev, orc, kind, rows, nb, lanes, unroll):
     c = Case(dev, orc, kind, rows, nb, seed=lanes + unroll)
     c.quant()
-    dev.set_tuning(lanes, unroll, 3, 0)  # 3 workgroups: each loops over several row groups
+    dev.set_tuning(lanes, unroll, 3)  # 3 workgroups: each loops over several row groups
     dev.gemv(kind, c.W, c.Q, c.Y, rows, nb)
     err = rel_err(c.y_gpu()[0], c.y_oracle(0), c.mag(0))
     assert err < TOL, err
@@ -170,15 +170,17 @@ def test_gemv_multi(dev, orc, kind, rows, nb, T):
 
 # ---------------------------------------------------------------- prefill GEMM
 
-@pytest.mark.parametrize("ntok", [64, 128])
+@pytest.mark.parametrize("kern,ks", [(0, 0), (1, 0), (2, 0), (3, 1), (4, 2), (3, 4), (4, 3)])
 @pytest.mark.parametrize("rows,nb,T", [(1, 8, 17), (63, 16, 64), (64, 160, 65), (130, 40, 130), (300, 24, 256), (70, 544, 33)])
-def test_gemm_q4k(dev, orc, rows, nb, T, ntok):
+def test_gemm_q4k(dev, orc, rows, nb, T, kern, ks):
     c = Case(dev, orc, 3, rows, nb, T, seed=rows + T)
     assert np.array_equal(c.quant(), c.xq)
     g = np.random.default_rng(T)
     bias = g.standard_normal(rows).astype(np.float32)
     B = dev.DevBuf.of(bias)
-    dev.set_tuning(0, 0, 0, ntok)
+    if ks and nb // 8 < ks:
+        pytest.skip("fewer super-blocks than splits")
+    dev.set_tuning(gemm_kernel=kern, gemm_ksplit=ks)
     dev.gemm_q4k(c.W, c.Q, c.Y, rows, nb, T, c.xs, rows, bias=B)
     y = c.y_gpu()
     for t in range(T):
@@ -205,3 +207,38 @@ def test_errors_do_not_launch(dev, orc):
         dev.gemv_q4(c.W.ptr + 4, c.Q, c.Y, 8, 16)  # misaligned weights
     with pytest.raises(dev.AmdcError):
         dev.gemv_q4k_t(c.W, c.Q, c.Y, 8, 16, 2, 100, 8)  # xs not a multiple of 16
+
+
+def test_graph_replay_matches_eager(dev, orc):
+    """A captured op sequence (quant, decode GEMV, multi-vector GEMV, GEMM) replayed several times, with eager
+    work and synchronizations between the replays: every replay equals the eager run bit for bit."""
+    rows, nb, T = 100, 160, 20
+    c = Case(dev, orc, 3, rows, nb, T, seed=4)
+    Y1, YT, YG = dev.DevBuf(4 * rows), dev.DevBuf(4 * rows * T), dev.DevBuf(4 * rows * T)
+    S = dev.Stream()
+
+    def ops(s):
+        dev.quant_q8(c.X, c.Q, nb, T, 128 * nb, c.xs, stream=s)
+        dev.gemv_q4k(c.W, c.Q, Y1, rows, nb, stream=s)
+        dev.gemv_q4k_t(c.W, c.Q, YT, rows, nb, 8, c.xs, rows, stream=s)
+        dev.gemm_q4k(c.W, c.Q, YG, rows, nb, T, c.xs, rows, stream=s)
+
+    for b in (c.Q, Y1, YT, YG):
+        b.fill(0)  # YT is written for 8 of its 20 token rows: the rest must not hold stale memory
+    dev.sync()
+    ops(S.s)
+    S.sync()
+    want = [b.download(np.uint32) for b in (c.Q, Y1, YT, YG)]
+    g = dev.Graph(S, ops)
+    other = Case(dev, orc, 0, 64, 128, seed=9)
+    for rep in range(3):
+        for b in (c.Q, Y1, YT, YG):
+            b.fill(0)
+        other.quant()
+        dev.gemv_q4(other.W, other.Q, other.Y, 64, 128)  # eager work between replays
+        dev.sync()
+        g.launch()
+        S.sync()
+        for b, w in zip((c.Q, Y1, YT, YG), want):
+            assert np.array_equal(b.download(np.uint32), w), rep
+    assert rel_err(Y1.download(np.float32), c.y_oracle(0), c.mag(0)) < TOL
