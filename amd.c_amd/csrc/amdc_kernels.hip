@@ -17,6 +17,8 @@
 // [int8 q[32 nb] | f32 d[nb] | u32 asum[nb]] (src/common.h:25-29).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "amdc_layout.h"
 
 typedef uint32_t u32;
@@ -24,6 +26,11 @@ typedef uint64_t u64;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+typedef u32 u32x2 __attribute__((ext_vector_type(2)));
+
+// A buffer resource over n bytes from p (raw, no stride): loads through it take
+// a 32-bit lane offset and a 32-bit scalar offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, u32 n) { return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)n, 0x00020000); }
 
 #define NT 256u
 
@@ -606,11 +613,13 @@ __device__ __forceinline__ h8 a_frag(u32 w0, u32 w1, u32 h, _Float16 sc) {
 //
 // Workgroup: 4 waves, 2 x 2; wave (wm, wn): 32 rows (2 row tiles of 16) x
 // 16 NJ tokens; the workgroup tile is 64 rows x 32 NJ tokens. K in stages of
-// 4 blocks (half a super-block): the stage's f16 activations (and d_a) are
-// written to LDS (double buffer, one barrier per stage) from registers loaded
-// a stage ahead; each wave reads its weights' nibble bytes straight from
-// memory, also a stage ahead. Inside a block all MFMAs are issued before
-// their results are used, and the next block's operands are read meanwhile.
+// 2 blocks; a super-block is 4 stages. The stage's f16 activations, d_a and
+// d_a asum are written to LDS (double buffer, one barrier per stage) from
+// registers loaded a stage ahead; each wave reads its weights' nibble bytes
+// straight from memory, also a stage ahead (the stage loop is unrolled by
+// two, so the prefetched registers alternate instead of being copied). All
+// global addresses are a workgroup-uniform base plus a 32-bit lane offset.
+// Inside a block all MFMAs are issued before their results are used.
 // Split K (gridDim.y > 1): super-blocks [g0, g1) per split; the partial sums
 // go to part[split][t][r] and amdc_gemm_reduce adds them in split order.
 template <int NJ>
@@ -619,96 +628,85 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
                                            const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 Tp, u32 ys, u32 rs,
                                            float *__restrict__ part) {
   constexpr u32 NTH = 256u, MR = 64u, NTT = 32u * NJ;
-  constexpr u32 BSTR = 136u; // halves per token per stage: 4 blocks x 32 + 8 of padding
+  constexpr u32 BSTR = 72u; // halves per token per stage: 2 blocks x 32 + 8 of padding
   __shared__ __attribute__((aligned(16))) _Float16 sb[2][NTT * BSTR];
-  __shared__ __attribute__((aligned(16))) float sda[2][4][NTT];
+  __shared__ __attribute__((aligned(16))) float sda[2][2][NTT];
+  __shared__ __attribute__((aligned(16))) float sxa[2][8][NTT]; // d_a asum of a super-block's 8 blocks, by parity
   const u32 ng = nb >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6, wm = w & 1u, wn = w >> 1;
   const u32 i16 = lane & 15u, h = lane >> 4;
   const u32 ntt = (T + NTT - 1u) / NTT, tt = blockIdx.x % ntt, rt = blockIdx.x / ntt;
-  const u32 rbase = rt * MR + 32u * wm, tbase = tt * NTT, twave = 16u * NJ * wn;
+  const u32 tbase = tt * NTT, twave = 16u * NJ * wn;
   const u32 ks = blockIdx.y, nks = gridDim.y, g0 = ng * ks / nks, g1 = ng * (ks + 1u) / nks;
-  const u64 RB = amdc_row_bytes(nb), K = 32ull * nb;
-  const uint8_t *wr[2];
+  const u32 RB = (u32)amdc_row_bytes(nb), K2 = 64u * nb; // bytes per weight row, per activation row
+  // uniform bases (buffer resources), 32-bit lane offsets
+  const uint8_t *wbase = W + (u64)rt * MR * RB;
+  const __amdgpu_buffer_rsrc_t rw = rsrc(wbase, (u32)min((u64)(rows - rt * MR) * RB, (u64)0xFFFFFFF0u));
+  const __amdgpu_buffer_rsrc_t rx = rsrc((const uint8_t *)xh + (u64)tbase * K2, (u32)min((u64)(Tp - tbase) * K2, (u64)0xFFFFFFF0u));
+  const __amdgpu_buffer_rsrc_t rda = rsrc(DA, (u32)min((u64)nb * Tp * 4u, (u64)0xFFFFFFF0u));
+  const __amdgpu_buffer_rsrc_t rxa = rsrc(XA, (u32)min((u64)nb * Tp * 4u, (u64)0xFFFFFFF0u));
+  // lane offsets: the A rows of this lane (clamped), the B chunks of this thread
+  u32 wo[2];
 #pragma unroll
   for (u32 i = 0; i < 2u; i++) {
-    const u32 r = rbase + 16u * i + i16;
-    wr[i] = W + (u64)(r < rows ? r : rows - 1u) * RB;
+    const u32 rl = 32u * wm + 16u * i + i16, r = rt * MR + rl;
+    wo[i] = (r < rows ? rl : rows - 1u - rt * MR) * RB;
   }
+  constexpr u32 NCH = NTT * 8u / NTH; // 16-byte chunks of activations per thread and stage (128 bytes per token)
+  u32 xo[NCH];
+#pragma unroll
+  for (u32 c = 0; c < NCH; c++) {
+    const u32 ch = tid + c * NTH;
+    xo[c] = (ch >> 3) * K2 + 16u * (ch & 7u);
+  }
+  const u32 dao = ((tid / NTT) * Tp + tbase + tid % NTT) * 4u; // d_a of (block 2s + tid / NTT, token tid % NTT)
   v4f acc[2][NJ], tmp[2][NJ];
 #pragma unroll
   for (u32 i = 0; i < 2u; i++)
 #pragma unroll
     for (u32 j = 0; j < NJ; j++) acc[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f}, tmp[i][j] = acc[i][j];
 
-  // stage s = blocks 4s .. 4s+3 (super-block s / 2, its half s % 2)
-  constexpr u32 NCH = NTT * 16u / NTH; // 16-byte chunks of activations per thread (256 bytes per token)
-  constexpr u32 NDA = 4u * NTT / NTH;  // d_a values per thread
   u32x4 rb[NCH];
-  float rd[NDA];
-  auto fetch = [&](u32 s) {
+  float rd = 0.0f, rxv = 0.0f; // d_a, d_a asum: threads < 2 NTT, one (block, token) each
+  auto fetch = [&](u32 s) { // stage s = blocks 2s, 2s+1
 #pragma unroll
-    for (u32 c = 0; c < NCH; c++) {
-      const u32 ch = tid + c * NTH, tk = ch >> 4, p16 = ch & 15u;
-      rb[c] = *(const u32x4 *)(xh + (u64)(tbase + tk) * K + 128u * s + 8u * p16);
-    }
-#pragma unroll
-    for (u32 c = 0; c < NDA; c++) {
-      const u32 e = tid + c * NTH;
-      rd[c] = DA[(u64)(4u * s + e / NTT) * Tp + tbase + e % NTT];
+    for (u32 c = 0; c < NCH; c++) rb[c] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo[c], 128u * s, 0);
+    if (tid < 2u * NTT) {
+      rd = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rda, dao, 8u * s * Tp, 0));
+      rxv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxa, dao, 8u * s * Tp, 0));
     }
   };
-  auto store = [&](u32 bf) {
+  auto store = [&](u32 bf, u32 s) {
 #pragma unroll
     for (u32 c = 0; c < NCH; c++) {
-      const u32 ch = tid + c * NTH, tk = ch >> 4, p16 = ch & 15u;
-      *(u32x4 *)(&sb[bf][tk * BSTR + 8u * p16]) = rb[c];
+      const u32 ch = tid + c * NTH;
+      *(u32x4 *)(&sb[bf][(ch >> 3) * BSTR + 8u * (ch & 7u)]) = rb[c];
     }
-#pragma unroll
-    for (u32 c = 0; c < NDA; c++) {
-      const u32 e = tid + c * NTH;
-      sda[bf][e / NTT][e % NTT] = rd[c];
+    if (tid < 2u * NTT) {
+      sda[bf][tid / NTT][tid % NTT] = rd;
+      sxa[(s >> 2) & 1u][2u * (s & 3u) + tid / NTT][tid % NTT] = rxv; // the next super-block writes the other half
     }
   };
-  // the lane's 8 nibble bytes of the stage's 4 blocks, 2 row tiles
-  auto load_w = [&](u32 s, u32 (&wv)[4][2][2]) {
-    const u32 g = s >> 1, kb = 4u * (s & 1u);
+  auto load_w = [&](u32 s, u32 (&wv)[2][2][2]) { // the lane's 8 nibble bytes, 2 blocks x 2 row tiles
+    const u32 g = s >> 2, kb = 2u * (s & 3u);
 #pragma unroll
-    for (u32 bb = 0; bb < 4u; bb++)
+    for (u32 bb = 0; bb < 2u; bb++) {
+      const u32 so = (u32)amdc_nib_off(ng, g, kb + bb);
 #pragma unroll
       for (u32 i = 0; i < 2u; i++) {
-        const uint64_t v = *(const uint64_t *)(wr[i] + amdc_nib_off(ng, g, kb + bb) + 8u * (h & 1u));
-        wv[bb][i][0] = (u32)v, wv[bb][i][1] = (u32)(v >> 32);
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rw, wo[i] + 8u * (h & 1u), so, 0);
+        wv[bb][i][0] = v.x, wv[bb][i][1] = v.y;
       }
+    }
   };
-  auto load_g = [&](u32 g, u32x4 (&hd)[2], float (&xa)[2][NJ]) {
+  u32x4 hd[2];
+  auto load_h = [&](u32 g) {
 #pragma unroll
-    for (u32 i = 0; i < 2u; i++) hd[i] = *(const u32x4 *)(wr[i] + amdc_header_off(g));
-#pragma unroll
-    for (u32 q = 0; q < 2u; q++)
-#pragma unroll
-      for (u32 j = 0; j < NJ; j++) xa[q][j] = XA[(u64)(8u * g + 4u * q + h) * Tp + tbase + twave + 16u * j + i16];
+    for (u32 i = 0; i < 2u; i++) hd[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo[i], 16u * g, 0);
   };
 
-  const u32 s0 = 2u * g0, s1 = 2u * g1;
-  u32 wv[4][2][2], wvn[4][2][2];
-  u32x4 hd[2], hdn[2];
-  float xa[2][NJ], xan[2][NJ];
-  if (s0 < s1) { // a split may own no super-block (then its partial sums are 0)
-    fetch(s0);
-    store(0);
-    load_w(s0, wv);
-    load_g(g0, hd, xa);
-  }
-  __syncthreads();
-  u32 bf = 0;
-  for (u32 s = s0; s < s1; s++) {
-    const u32 kb = 4u * (s & 1u);
-    const bool more = s + 1u < s1, opens = ((s + 1u) & 1u) == 0u;
-    if (more) { // the next stage's global data, in flight during this stage
-      fetch(s + 1u);
-      load_w(s + 1u, wvn);
-      if (opens) load_g((s + 1u) >> 1, hdn, xan);
-    }
+  // one stage: the MFMAs and fmas of blocks kb, kb + 1 of the super-block (kb
+  // a constant) from LDS buffer bf and the nibbles wv
+  auto compute = [&](u32 kb, u32 bf, const u32(&wv)[2][2][2]) {
     const _Float16 *lb = &sb[bf][(twave + i16) * BSTR + 8u * h];
     h8 bq[NJ];
 #pragma unroll
@@ -717,66 +715,81 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
 #pragma unroll
     for (u32 i = 0; i < 2u; i++) af[i] = a_frag(wv[0][i][0], wv[0][i][1], h, (_Float16)(float)q4k_sc(hd[i], kb));
 #pragma unroll
-    for (u32 bb = 0; bb < 4u; bb++) {
-      v4f x[2][NJ];
-#pragma unroll
-      for (u32 j = 0; j < NJ; j++)
-#pragma unroll
-        for (u32 i = 0; i < 2u; i++) x[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bq[j], (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    for (u32 bb = 0; bb < 2u; bb++) {
       float dj[NJ];
 #pragma unroll
       for (u32 j = 0; j < NJ; j++) dj[j] = sda[bf][bb][twave + 16u * j + i16];
-      if (bb + 1u < 4u) { // the next block's operands while the MFMAs run
 #pragma unroll
-        for (u32 j = 0; j < NJ; j++) bq[j] = *(const h8 *)(lb + 16u * j * BSTR + 32u * (bb + 1u));
+      for (u32 i = 0; i < 2u; i++) { // a row tile at a time: NJ MFMAs in flight, then their fmas
+        v4f x[NJ];
 #pragma unroll
-        for (u32 i = 0; i < 2u; i++)
-          af[i] = a_frag(wv[bb + 1u][i][0], wv[bb + 1u][i][1], h, (_Float16)(float)q4k_sc(hd[i], kb + bb + 1u));
-      }
+        for (u32 j = 0; j < NJ; j++) x[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bq[j], (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        if (bb == 0u && i == 1u) { // the second block's operands while the MFMAs run
 #pragma unroll
-      for (u32 j = 0; j < NJ; j++)
+          for (u32 j = 0; j < NJ; j++) bq[j] = *(const h8 *)(lb + 16u * j * BSTR + 32u);
 #pragma unroll
-        for (u32 i = 0; i < 2u; i++)
-#pragma unroll
-          for (u32 v = 0; v < 4u; v++) tmp[i][j][v] = __builtin_fmaf(dj[j], x[i][j][v], tmp[i][j][v]);
-    }
-    if (s & 1u) { // the super-block is done: d, and the min term
-#pragma unroll
-      for (u32 i = 0; i < 2u; i++) {
-        const float dmine = h2f(hd[i].x), dmn = h2f(hd[i].x >> 16);
-        float dv[4];
-#pragma unroll
-        for (u32 v = 0; v < 4u; v++) dv[v] = __shfl(dmine, (int)(4u * h + v));
-        float am[2];
-#pragma unroll
-        for (u32 q = 0; q < 2u; q++) am[q] = -(dmn * (float)q4k_mn(hd[i], 4u * q + h));
-#pragma unroll
-        for (u32 j = 0; j < NJ; j++) {
-#pragma unroll
-          for (u32 v = 0; v < 4u; v++) acc[i][j][v] = __builtin_fmaf(dv[v], tmp[i][j][v], acc[i][j][v]);
-          tmp[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-          for (u32 q = 0; q < 2u; q++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(am[q], xa[q][j], acc[i][j], 0, 0, 0);
+          for (u32 i2 = 0; i2 < 2u; i2++) af[i2] = a_frag(wv[1][i2][0], wv[1][i2][1], h, (_Float16)(float)q4k_sc(hd[i2], kb + 1u));
         }
+#pragma unroll
+        for (u32 j = 0; j < NJ; j++)
+#pragma unroll
+          for (u32 v = 0; v < 4u; v++) tmp[i][j][v] = __builtin_fmaf(dj[j], x[j][v], tmp[i][j][v]);
       }
     }
-    if (more) {
-      store(bf ^ 1u); // that buffer was last read in the previous stage, before its barrier
-      __syncthreads();
-      bf ^= 1u;
+  };
+  // the end of a super-block: d, and the min term from the 8 blocks' d_a asum
+  auto close_group = [&](u32 gp) {
 #pragma unroll
-      for (u32 bb = 0; bb < 4u; bb++)
+    for (u32 i = 0; i < 2u; i++) {
+      const float dmine = h2f(hd[i].x), dmn = h2f(hd[i].x >> 16);
+      float dv[4];
 #pragma unroll
-        for (u32 i = 0; i < 2u; i++) wv[bb][i][0] = wvn[bb][i][0], wv[bb][i][1] = wvn[bb][i][1];
-      if (opens) {
+      for (u32 v = 0; v < 4u; v++) dv[v] = __shfl(dmine, (int)(4u * h + v));
+      float am[2];
 #pragma unroll
-        for (u32 i = 0; i < 2u; i++) hd[i] = hdn[i];
+      for (u32 q = 0; q < 2u; q++) am[q] = -(dmn * (float)q4k_mn(hd[i], 4u * q + h));
+#pragma unroll
+      for (u32 j = 0; j < NJ; j++) {
+#pragma unroll
+        for (u32 v = 0; v < 4u; v++) acc[i][j][v] = __builtin_fmaf(dv[v], tmp[i][j][v], acc[i][j][v]);
+        tmp[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (u32 q = 0; q < 2u; q++)
-#pragma unroll
-          for (u32 j = 0; j < NJ; j++) xa[q][j] = xan[q][j];
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(am[q], sxa[gp][4u * q + h][twave + 16u * j + i16], acc[i][j], 0, 0, 0);
       }
     }
+  };
+
+  // stages in pairs: s (LDS buffer 0, nibbles wa), s + 1 (buffer 1, nibbles
+  // wb); the activations and the nibbles of the next stage are in flight
+  // during a stage
+  const u32 s0 = 4u * g0, s1 = 4u * g1;
+  u32 wa[2][2][2], wb[2][2][2];
+  if (s0 < s1) { // a split may own no super-block (then its partial sums are 0)
+    fetch(s0);
+    store(0, s0);
+    load_w(s0, wa);
+    load_h(g0);
+  }
+  __syncthreads();
+  for (u32 s = s0; s < s1; s += 2u) {
+    fetch(s + 1u);
+    load_w(s + 1u, wb);
+    compute(2u * (s & 3u), 0, wa);
+    store(1, s + 1u);
+    __syncthreads();
+    const bool more = s + 2u < s1;
+    if (more) {
+      fetch(s + 2u);
+      load_w(s + 2u, wa);
+    }
+    compute(2u * ((s + 1u) & 3u), 1, wb);
+    if (((s + 1u) & 3u) == 3u) {
+      close_group((s >> 2) & 1u);
+      if (more) load_h((s + 2u) >> 2);
+    }
+    if (more) store(0, s + 2u);
+    __syncthreads();
   }
 #pragma unroll
   for (u32 i = 0; i < 2u; i++)
@@ -786,7 +799,7 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
       if (tk >= T) continue;
 #pragma unroll
       for (u32 v = 0; v < 4u; v++) {
-        const u32 r = rbase + 16u * i + 4u * h + v;
+        const u32 r = rt * MR + 32u * wm + 16u * i + 4u * h + v;
         if (r >= rows) continue;
         if (part) {
           part[((u64)ks * T + tk) * rows + r] = acc[i][j][v];

@@ -242,3 +242,24 @@ def test_graph_replay_matches_eager(dev, orc):
         for b, w in zip((c.Q, Y1, YT, YG), want):
             assert np.array_equal(b.download(np.uint32), w), rep
     assert rel_err(Y1.download(np.float32), c.y_oracle(0), c.mag(0)) < TOL
+
+
+@pytest.mark.parametrize("kern,ks", [(0, 0), (1, 0), (3, 2), (4, 4)])
+def test_gemm_deterministic(dev, orc, kern, ks):
+    """Repeated GEMMs give the same bits: the kernels have a fixed summation order, so any
+    difference between runs would be a race between waves."""
+    rows, nb, T = 300, 544, 96
+    c = Case(dev, orc, 3, rows, nb, T, seed=11)
+    c.quant()
+    dev.set_tuning(gemm_kernel=kern, gemm_ksplit=ks)
+    first = None
+    for _ in range(6):
+        c.Y.fill(0)
+        dev.gemm_q4k(c.W, c.Q, c.Y, rows, nb, T, c.xs, rows)
+        got = c.Y.download(np.uint32)
+        if first is None:
+            first = got
+        assert np.array_equal(got, first)
+    y = first.view(np.float32).reshape(T, rows)
+    for t in (0, T - 1):
+        assert rel_err(y[t], c.y_oracle(t), c.mag(t)) < TOL
