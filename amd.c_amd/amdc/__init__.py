@@ -53,6 +53,8 @@ ABI = {
     "amdc_quant_q8": (C.c_int, [_P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_gemv_q4": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
     "amdc_gemv_q4k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
+    "amdc_gemv_q4_x": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P, _P]),
+    "amdc_gemv_q4k_x": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P, _P]),
     "amdc_gemv_q4_t": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_gemv_q4k_t": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_gemm_q4k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
@@ -273,6 +275,12 @@ def gemv_q4k(w, xq, y, rows, nb, bias=None, res=None, stream=None):
 
 def gemv(kind, w, xq, y, rows, nb, bias=None, res=None, stream=None):
     (gemv_q4k if kind == KIND_Q4_K else gemv_q4)(w, xq, y, rows, nb, bias, res, stream)
+
+
+def gemv_x(kind, w, x, y, rows, nb, bias=None, res=None, q8=None, stream=None):
+    """Decode GEMV on the f32 vector x, quantized in the kernel (q8: optional Q8 output)."""
+    f = lib().amdc_gemv_q4k_x if kind == KIND_Q4_K else lib().amdc_gemv_q4_x
+    _check(f(_p(w), _p(x), _p(y), rows, nb, _p(bias), _p(res), _p(q8), stream))
 
 
 def gemv_q4_t(w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stream=None):

@@ -176,6 +176,10 @@ enum {
   K_GEMMH_M64_N128,
   K_GEMMH_M64_N64,
   K_GEMM_REDUCE,
+  K_GEMV_Q4_V8,
+  K_GEMV_Q4K_V8,
+  K_GEMV_Q4_X1,
+  K_GEMV_Q4K_X1,
   K_N
 };
 static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1",  "amdc_gemv_q4_k_t1",  "amdc_gemv_q4_0_t1u1",
@@ -183,7 +187,8 @@ static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1
                                        "amdc_gemv_q4_k_t16",  "amdc_dots_q4_0",     "amdc_dots_q4_k",     "amdc_gemm_q4_k_n128",
                                        "amdc_gemm_q4_k_n64",  "amdc_gemv_q4_0_p1",  "amdc_gemv_q4_k_p1",  "amdc_probe_read",
                                        "amdc_probe_copy",     "amdc_q8_prep",       "amdc_gemmh_m64_n128", "amdc_gemmh_m64_n64",
-                                       "amdc_gemm_reduce"};
+                                       "amdc_gemm_reduce",    "amdc_gemv_q4_0_v8",  "amdc_gemv_q4_k_v8",
+                                       "amdc_gemv_q4_0_x1",   "amdc_gemv_q4_k_x1"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -443,8 +448,34 @@ static u32 gemv_lanes(u32 ng) {
 #define GEMV_LDS_T1 (150u * 1024u)
 #define GEMV_LDS_TN (64u * 1024u)
 
+static int ws_reserve(size_t n);
+
+/* The verify GEMV on int8 MFMA (T <= 8): 64 rows per workgroup, K split
+ * over tiles of 64 blocks until the workgroups fill the CUs twice. */
+static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
+                        const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  const u32 nt = (amdc_ngroups(nb) + 7u) / 8u, wgs = (rows + 63u) / 64u, cus = g_cus > 0 ? (u32)g_cus : 256u;
+  u32 ks = 1;
+  while (ks < 8u && (u64)wgs * ks < 2u * cus && nt >= 2u * ks) ks <<= 1;
+  float *part = NULL;
+  if (ks > 1u) {
+    int rc = ws_reserve((size_t)ks * T * rows * 4u);
+    if (rc) return rc;
+    part = g_ws;
+  }
+  void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs, &part};
+  HIPCALL(H.ModuleLaunchKernel(g_k[kind ? K_GEMV_Q4K_V8 : K_GEMV_Q4_V8], wgs, ks, 1, 256, 1, 1, 0, stream, args, NULL));
+  if (ks > 1u) {
+    const u64 n = (u64)rows * T;
+    void *ra[] = {&part, &ks, &y, &rows, &T, &bias, &res, &ys, &rs};
+    return launch(K_GEMM_REDUCE, (unsigned)((n + 255u) / 256u), 1, 0, stream, ra);
+  }
+  return AMDC_OK;
+}
+
 static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                        const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  if (T > 1u && T <= 8u && t_unroll <= 0) return gemv8_launch(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
   const u32 ng = amdc_ngroups(nb), L = gemv_lanes(ng), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
   const u32 TT = T == 1u ? 1u : T <= 8u ? 8u : 16u;
   u32 GC = (TT == 1u ? GEMV_LDS_T1 : GEMV_LDS_TN) / (320u * TT);
@@ -498,6 +529,30 @@ static int gemv_t(int kind, const char *op, const void *w, const uint8_t *xq, fl
   return rc;
 }
 
+/* The decode GEMV with the Q8 quantization of its f32 input fused into the
+ * prologue (OP_QUANT + OP_GEMV_Q4 / OP_GEMV_Q4K in one launch). */
+static int gemv_x(int kind, const char *op, const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias,
+                  const float *res, uint8_t *q8, void *stream) {
+  NEED_OPEN();
+  int rc = check_mat(op, kind, w, (const uint8_t *)x, y, rows, nb);
+  if (rc) return rc;
+  const u32 ng = amdc_ngroups(nb), L = gemv_lanes(ng), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
+  if (320u * ng > GEMV_LDS_T1) return fail(AMDC_EINVAL, "%s: nb %u too large for the fused kernel", op, nb);
+  const unsigned grid = t_wgs > 0 && (u32)t_wgs < nrg ? (unsigned)t_wgs : nrg;
+  void *args[] = {&w, &x, &y, &rows, &nb, &bias, &res, (void *)&L, &q8};
+  return launch(kind ? K_GEMV_Q4K_X1 : K_GEMV_Q4_X1, grid, 1, 320u * ng, stream, args);
+}
+
+int amdc_gemv_q4_x(const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res, uint8_t *q8,
+                   void *stream) {
+  return gemv_x(AMDC_KIND_Q4_0, "gemv_q4_x", w, x, y, rows, nb, bias, res, q8, stream);
+}
+
+int amdc_gemv_q4k_x(const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res, uint8_t *q8,
+                    void *stream) {
+  return gemv_x(AMDC_KIND_Q4_K, "gemv_q4k_x", w, x, y, rows, nb, bias, res, q8, stream);
+}
+
 int amdc_gemv_q4_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                    uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
   return gemv_t(AMDC_KIND_Q4_0, "gemv_q4_t", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
@@ -539,26 +594,16 @@ int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uin
     void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs};
     return launch(n == 128u ? K_GEMM_N128 : K_GEMM_N64, (unsigned)grid, 1, 0, stream, args);
   }
-  /* the f16-MFMA kernel: pick the tile and the K split that fill the CUs best */
+  /* the f16-MFMA kernel: 128 tokens per workgroup when there are that many;
+   * the K split doubles until the workgroups number three per CU (measured
+   * best on the c4 shapes: 17408 x 5120 split 2, 5120 x 17408 split 8) */
   const u32 ng = nb / 8u, cus = g_cus > 0 ? (u32)g_cus : 256u;
-  int v = t_gemm >= 3 ? t_gemm - 3 : -1;
+  const int v = t_gemm >= 3 ? t_gemm - 3 : (T > 64u ? 0 : 1);
   u32 ks = t_ksplit > 0 ? (u32)t_ksplit : 0u;
-  if (v < 0 || !ks) {
-    double best = -1.0;
-    for (int c = 0; c < 2; c++) {
-      if (v >= 0 && c != v) continue;
-      for (u32 k = 1; k <= 4u; k <<= 1) {
-        if (ks && k != ks) continue;
-        if (k > 1u && ng < 8u * k) continue;
-        const u64 tiles = (u64)((rows + gh[c].mr - 1u) / gh[c].mr) * ((T + gh[c].nt - 1u) / gh[c].nt) * k;
-        const u64 slots = (u64)cus * 2u; /* workgroups resident at once */
-        const double rounds = (double)((tiles + slots - 1u) / slots), fill = (double)tiles / (rounds * (double)slots);
-        /* useful work per round slot, larger tiles reuse more; each split costs a reduction pass */
-        const double score = fill * (gh[c].nt >= 128u ? 1.0 : 0.85) /
-                             (1.0 + 0.04 * (double)(k - 1u));
-        if (score > best) best = score, v = c, ks = k;
-      }
-    }
+  if (!ks) {
+    const u64 tiles = (u64)((rows + gh[v].mr - 1u) / gh[v].mr) * ((T + gh[v].nt - 1u) / gh[v].nt);
+    ks = 1;
+    while (ks < 16u && tiles * ks < 3u * cus && ng >= 4u * ks) ks <<= 1;
   }
   if (ks > ng) ks = ng;
   const u32 Tp = (T + 127u) / 128u * 128u, K = 32u * nb;

@@ -289,9 +289,10 @@ __device__ __forceinline__ float item_dot(const Item &it, u32 gl, u32 GC, const 
   return acc;
 }
 
-template <int KIND>
+template <int KIND, bool FQ>
 __device__ __forceinline__ void gemv1_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
-                                           u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 L) {
+                                           u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 L,
+                                           const float *__restrict__ xf = nullptr, uint8_t *__restrict__ q8out = nullptr) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const u32 ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
   const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw;
@@ -310,18 +311,40 @@ __device__ __forceinline__ void gemv1_body(const uint8_t *__restrict__ W, const 
   };
   Item cur, nxt;
   load_item<KIND>(cur, rowp(rg), ng, l, l < ng);
-  for (u32 j = tid; j < nblk; j += NT) { // stage the whole Q8 vector (permuted)
-    const u32 p = (j & 7u) * ng + (j >> 3);
-    u32x4 lo = (u32x4)(0u), hi = (u32x4)(0u);
-    float d = 0.0f;
-    u32 as = 0;
-    if (j < nb) {
-      lo = *(const u32x4 *)(xq + 32u * j);
-      hi = *(const u32x4 *)(xq + 32u * j + 16u);
-      d = ((const float *)(xq + 32u * nb))[j];
-      as = ((const u32 *)(xq + 36u * nb))[j];
+  if (FQ) { // quantize the f32 vector here, half a wave per block (the arithmetic of amdc_quant_q8)
+    const u32 j = tid & 31u;
+    for (u32 b0 = 0; b0 < nblk; b0 += 8u) {
+      const u32 b = b0 + (tid >> 5), p = (b & 7u) * ng + (b >> 3);
+      const float v = b < nb ? xf[32u * b + j] : 0.0f;
+      float a = __builtin_fabsf(v);
+#pragma unroll
+      for (u32 o = 1; o < 32u; o <<= 1) a = __builtin_fmaxf(a, __shfl_xor(a, (int)o));
+      const float d = a / 127.0f;
+      const int qi = d != 0.0f ? (int)__builtin_roundf(v / d) : 0;
+      u32 sum = (u32)qi;
+#pragma unroll
+      for (u32 o = 1; o < 32u; o <<= 1) sum += (u32)__shfl_xor((int)sum, (int)o);
+      ((uint8_t *)(j < 16u ? &s_lo[p] : &s_hi[p]))[j & 15u] = (uint8_t)qi;
+      if (j == 0u) s_d[p] = d, s_as[p] = sum;
+      if (q8out && blockIdx.x == 0u && b < nb) { // the Q8 buffer, for other consumers
+        ((int8_t *)q8out)[32u * b + j] = (int8_t)qi;
+        if (j == 0u) ((float *)(q8out + 32u * nb))[b] = d, ((u32 *)(q8out + 36u * nb))[b] = sum;
+      }
     }
-    s_lo[p] = lo, s_hi[p] = hi, s_d[p] = d, s_as[p] = as;
+  } else {
+    for (u32 j = tid; j < nblk; j += NT) { // stage the whole Q8 vector (permuted)
+      const u32 p = (j & 7u) * ng + (j >> 3);
+      u32x4 lo = (u32x4)(0u), hi = (u32x4)(0u);
+      float d = 0.0f;
+      u32 as = 0;
+      if (j < nb) {
+        lo = *(const u32x4 *)(xq + 32u * j);
+        hi = *(const u32x4 *)(xq + 32u * j + 16u);
+        d = ((const float *)(xq + 32u * nb))[j];
+        as = ((const u32 *)(xq + 36u * nb))[j];
+      }
+      s_lo[p] = lo, s_hi[p] = hi, s_d[p] = d, s_as[p] = as;
+    }
   }
   __syncthreads();
   float acc = 0.0f;
@@ -350,11 +373,21 @@ __device__ __forceinline__ void gemv1_body(const uint8_t *__restrict__ W, const 
 
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_0_p1(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 L) {
-  gemv1_body<AMDC_Q4_0>(W, xq, y, rows, nb, bias, res, L);
+  gemv1_body<AMDC_Q4_0, false>(W, xq, y, rows, nb, bias, res, L);
 }
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_p1(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 L) {
-  gemv1_body<AMDC_Q4_K>(W, xq, y, rows, nb, bias, res, L);
+  gemv1_body<AMDC_Q4_K, false>(W, xq, y, rows, nb, bias, res, L);
+}
+// The same, quantizing the f32 vector x in the prologue (fused OP_QUANT);
+// workgroup 0 writes the Q8 buffer to q8 when q8 is not NULL.
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_0_x1(const uint8_t *W, const float *x, float *y, u32 rows, u32 nb,
+                                                                   const float *bias, const float *res, u32 L, uint8_t *q8) {
+  gemv1_body<AMDC_Q4_0, true>(W, nullptr, y, rows, nb, bias, res, L, x, q8);
+}
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_x1(const uint8_t *W, const float *x, float *y, u32 rows, u32 nb,
+                                                                   const float *bias, const float *res, u32 L, uint8_t *q8) {
+  gemv1_body<AMDC_Q4_K, true>(W, nullptr, y, rows, nb, bias, res, L, x, q8);
 }
 
 // ------------------------------------------------------------------ bandwidth probes
@@ -835,4 +868,210 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *
   if (bias) o = o + bias[r];
   if (res) o = res[(u64)t * rs + r] + o;
   y[(u64)t * ys + r] = o;
+}
+
+// ------------------------------------------------------------------ verify GEMV on int8 MFMA (T <= 8)
+
+// y_t = W x_t for T <= 8 Q8 vectors, the weights read once: per pair of
+// sub-blocks (g, k), (g + 1, k) of one plane, v_mfma_i32_16x16x64_i8 with
+//   A (16 rows x 64): lane (row i, h) = the nibbles of block (g + h / 2, k),
+//     low (h even) or high (h odd) half: weights 16 (h & 1) .. + 15
+//   B (64 x 16 columns n = t + 8 pp): the 32 activations of token t, block
+//     (g + pp, k), in K half pp, zeros in the other half
+// so that C[r][t + 8 pp] is the exact integer dot of block (g + pp, k) with
+// vector t (Q4_K: sum q a; Q4_0: sum q a, then - 8 asum). Per element the
+// reference's block arithmetic (src/cpu.c:81, 111-112):
+//   Q4_0: acc += (d_w d_a) (dq - 8 asum)
+//   Q4_K: acc = fma(s dq, d_a, acc), s = d sc; the min term - sum (dmin mn)
+//         (d_a asum) of every block on v_mfma_f32_16x16x4_f32 (column pp = 0).
+// The columns pp = 0 and 1 of a token hold the sums of alternate blocks; a
+// DPP add joins them at the end.
+// Workgroup: 4 waves, wave w: rows 16 w .. 16 w + 15 of a 64-row tile; K in
+// tiles of 8 super-groups (64 blocks): the tile's activations are staged in
+// LDS, B-ready (the zero halves written once), with d_a, d_a asum (or asum)
+// per (block, token); each wave builds its rows' scale table (and Q4_K min
+// table) from the headers; the weights come straight from memory, plane k of
+// the tile is 4 loads of 32 contiguous bytes per row, one plane ahead.
+// Split K over gridDim.y (tiles [t0, t1) per split, partial sums to part).
+template <int KIND>
+__device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
+                                           u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 xs, u32 ys,
+                                           u32 rs, float *__restrict__ part) {
+  __shared__ __attribute__((aligned(16))) u32x4 sB[32][4][16]; // [pair p + 4 k][K quarter][column]: a quarter's columns contiguous
+  __shared__ __attribute__((aligned(16))) float sda[64][8];    // d_a [block of tile][token]
+  __shared__ __attribute__((aligned(16))) float sxa[64][8];    // Q4_K: d_a asum; Q4_0: asum (as int bits)
+  __shared__ __attribute__((aligned(16))) float ssc[4][64][16]; // per wave: s (Q4_K d sc, Q4_0 d) [block][row]
+  __shared__ __attribute__((aligned(16))) float smn[4][64][16]; // per wave, Q4_K: -(dmin mn) [block][row]
+  const u32 ng = amdc_ngroups(nb), nt = (ng + 7u) >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
+  const u32 i16 = lane & 15u, h = lane >> 4, n = i16, tk = n & 7u, pp = n >> 3;
+  const u32 RB = (u32)amdc_row_bytes(nb);
+  const u32 rt0 = blockIdx.x * 64u, r0 = rt0 + 16u * w, ra = r0 + i16 < rows ? r0 + i16 : rows - 1u; // A row of this lane
+  // a workgroup-uniform resource over the tile's rows; the lane's row in the 32-bit offset
+  const __amdgpu_buffer_rsrc_t rw = rsrc(W + (u64)rt0 * RB, (u32)min((u64)(rows - rt0) * RB, (u64)0xFFFFFFF0u));
+  const u32 wo = (ra - rt0) * RB;
+  const u32 xn = (u32)min((u64)T * xs, (u64)0xFFFFFFF0u);
+  const __amdgpu_buffer_rsrc_t rxq = rsrc(xq, xn); // the T Q8 rows
+  constexpr u32 OOB = 0xFFFFFFF0u;                 // an offset past every resource: the load returns zeros
+  const u32 ks = blockIdx.y, nks = gridDim.y, t0 = nt * ks / nks, t1 = nt * (ks + 1u) / nks;
+  // the zero halves of B (never written again)
+  for (u32 i = tid; i < 32u * 16u * 4u; i += NT) {
+    const u32 col = i & 15u, q = (i >> 4) & 3u;
+    if ((q >> 1) != (col >> 3)) (&sB[0][0][0])[i] = (u32x4)(0u);
+  }
+  auto gtile = [&](u32 t) { return ng - 8u * t < 8u ? ng - 8u * t : 8u; };
+  // the weights of plane k of tile t: this lane's 16 bytes of the 4 pairs
+  // (every load unconditional: out-of-range ones read as zeros, so the
+  // compiler can count the loads in flight instead of draining them)
+  auto load_plane = [&](u32 t, u32 k, u32x4 (&wq)[4]) {
+    const u32 gt = gtile(t);
+#pragma unroll
+    for (u32 p = 0; p < 4u; p++) {
+      const u32 gl = 2u * p + (h >> 1);
+      wq[p] = __builtin_amdgcn_raw_buffer_load_b128(rw, gl < gt ? wo + (u32)amdc_nib_off(ng, 8u * t + gl, k) : OOB, 0, 0);
+    }
+  };
+  // activations of tile t in registers (thread: 2 of the 16-byte halves, 2 of the (block, token) scale pairs)
+  u32x4 ra4[4];
+  float rd[2];
+  u32 rx[2]; // asum as loaded: d_a asum is formed at the LDS store, so that the fetch does not wait for its loads
+  u32x4 rh[2];
+  auto fetch_tile = [&](u32 t) {
+    const u32 gt = gtile(t);
+#pragma unroll
+    for (u32 c = 0; c < 4u; c++) {
+      const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, gl = bl >> 3, k = bl & 7u, b = 64u * t + 8u * gl + k;
+      const bool ok = tok < T && gl < gt && b < nb;
+      ra4[c] = __builtin_amdgcn_raw_buffer_load_b128(rxq, ok ? tok * xs + 32u * b + 16u * half : OOB, 0, 0);
+    }
+#pragma unroll
+    for (u32 c = 0; c < 2u; c++) {
+      const u32 i = tid + c * NT, tok = i & 7u, bl = i >> 3, b = 64u * t + bl;
+      const bool ok = tok < T && (bl >> 3) < gt && b < nb;
+      rd[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxq, ok ? tok * xs + 32u * nb + 4u * b : OOB, 0, 0));
+      rx[c] = __builtin_amdgcn_raw_buffer_load_b32(rxq, ok ? tok * xs + 36u * nb + 4u * b : OOB, 0, 0);
+    }
+#pragma unroll
+    for (u32 q = 0; q < 2u; q++) {
+      const u32 gl = h + 4u * q;
+      rh[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, gl < gt ? wo + 16u * (8u * t + gl) : OOB, 0, 0);
+    }
+  };
+  auto stage_tile = [&]() {
+#pragma unroll
+    for (u32 c = 0; c < 4u; c++) {
+      const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, gl = bl >> 3, k = bl & 7u;
+      sB[(gl >> 1) + 4u * k][2u * (gl & 1u) + half][tok + 8u * (gl & 1u)] = ra4[c];
+    }
+#pragma unroll
+    for (u32 c = 0; c < 2u; c++) {
+      const u32 i = tid + c * NT, tok = i & 7u, bl = i >> 3;
+      sda[bl][tok] = rd[c];
+      sxa[bl][tok] = KIND == AMDC_Q4_K ? rd[c] * (float)(int)rx[c] : __builtin_bit_cast(float, rx[c]);
+    }
+#pragma unroll
+    for (u32 q = 0; q < 2u; q++) { // this wave's scale tables: row i16, groups h, h + 4
+      const u32 gl = h + 4u * q;
+      const u32x4 hd = rh[q];
+#pragma unroll
+      for (u32 k = 0; k < 8u; k++) {
+        if (KIND == AMDC_Q4_0) {
+          ssc[w][8u * gl + k][i16] = h2f(hword(hd, k >> 1) >> (16u * (k & 1u)));
+        } else {
+          ssc[w][8u * gl + k][i16] = h2f(hd.x) * (float)q4k_sc(hd, k);
+          smn[w][8u * gl + k][i16] = -(h2f(hd.x >> 16) * (float)q4k_mn(hd, k));
+        }
+      }
+    }
+  };
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  // the MFMAs of plane k (pairs of the tile) with its weights wq
+  auto plane = [&](u32 k, u32 npair, const u32x4 (&wq)[4]) {
+    v4i c[4];
+#pragma unroll
+    for (u32 p = 0; p < 4u; p++) { // the MFMAs of the plane first
+      if (p < npair) {
+        const u32x4 a = (wq[p] >> (4u * (h & 1u))) & 0x0F0F0F0Fu;
+        const u32x4 bq = sB[p + 4u * k][h][n];
+        c[p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, bq), (v4i){0, 0, 0, 0}, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (u32 p = 0; p < 4u; p++) {
+      if (p >= npair) break;
+      const u32 bl = 8u * (2u * p + pp) + k; // this lane's block (column pp)
+      const v4f s4 = *(const v4f *)&ssc[w][bl][4u * h];
+      const float da = sda[bl][tk];
+      if (KIND == AMDC_Q4_0) {
+        const u32 as = __builtin_bit_cast(u32, sxa[bl][tk]);
+#pragma unroll
+        for (u32 v = 0; v < 4u; v++) acc[v] += (s4[v] * da) * (float)(int)((u32)c[p][v] - 8u * as);
+      } else {
+#pragma unroll
+        for (u32 v = 0; v < 4u; v++) acc[v] = __builtin_fmaf(s4[v] * (float)c[p][v], da, acc[v]);
+      }
+    }
+  };
+
+  // software pipeline over (tile, plane): plane k uses ring slot k & 3 and,
+  // once used, the slot is reloaded with plane k + 4 (of this tile or the next)
+  u32x4 wq[4][4];
+  if (t0 < t1) {
+    fetch_tile(t0);
+#pragma unroll
+    for (u32 k = 0; k < 4u; k++) load_plane(t0, k, wq[k]);
+  }
+  for (u32 t = t0; t < t1; t++) {
+    const bool more = t + 1u < t1;
+    const u32 npair = (gtile(t) + 1u) >> 1;
+    __syncthreads(); // the previous tile's readers are done
+    stage_tile();
+    __syncthreads();
+    if (more) fetch_tile(t + 1u); // in flight during this tile
+#pragma unroll
+    for (u32 k = 0; k < 8u; k++) {
+      plane(k, npair, wq[k & 3u]);
+      if (k < 4u) load_plane(t, k + 4u, wq[k & 3u]);
+      else if (more) load_plane(t + 1u, k - 4u, wq[k & 3u]);
+    }
+    if (KIND == AMDC_Q4_K) { // the min term of the tile's blocks, into the pp = 0 columns
+      v4f m = {acc[0], acc[1], acc[2], acc[3]};
+#pragma unroll
+      for (u32 q = 0; q < 16u; q++) {
+        const u32 bl = 4u * q + h; // K index = block of the tile
+        const float am = smn[w][bl][i16];
+        const float bx = pp == 0u ? sxa[bl][tk] : 0.0f;
+        m = __builtin_amdgcn_mfma_f32_16x16x4f32(am, bx, m, 0, 0, 0);
+      }
+      acc[0] = m[0], acc[1] = m[1], acc[2] = m[2], acc[3] = m[3];
+    }
+  }
+  // join the two block parities of each token (columns n and n + 8) and store
+#pragma unroll
+  for (u32 v = 0; v < 4u; v++) acc[v] += dpp<0x128>(acc[v]); // row_ror:8
+  if (pp == 0u && tk < T) {
+#pragma unroll
+    for (u32 v = 0; v < 4u; v++) {
+      const u32 r = r0 + 4u * h + v;
+      if (r >= rows) continue;
+      if (part) {
+        part[((u64)ks * T + tk) * rows + r] = acc[v];
+      } else {
+        float o = acc[v];
+        if (bias) o = o + bias[r];
+        if (res) o = res[(u64)tk * rs + r] + o;
+        y[(u64)tk * ys + r] = o;
+      }
+    }
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_0_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+                                                                   const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
+                                                                   float *part) {
+  gemv8_body<AMDC_Q4_0>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+}
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+                                                                   const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
+                                                                   float *part) {
+  gemv8_body<AMDC_Q4_K>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
 }

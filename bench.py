@@ -3,7 +3,9 @@
 One "step" = one pass of the hot path over one batch-1 input through the
 configuration's GEMV set: for c1 (the headline, Llama-7B layer shapes, Q4_0)
 x -> Q8 -> q, k, v; Q8 -> o; Q8 -> gate, up; Q8 -> down; Q8 -> lm_head (5
-quantizations, 8 GEMVs), with weight copies rotated so that the weights
+quantizations, 8 GEMVs; the form with each quantization fused into the
+prologue of the first GEMV of its input is timed too: it is slower, every
+workgroup quantizes the vector), with weight copies rotated so that the weights
 streamed per step come from HBM (the copies total >= 2 GB, far above the 256
 MB Infinity Cache). value = weight bytes of the step (the reference's
 rows * nb * 18, src/hip.c:1831) / step time, inputs resident in HBM.
@@ -117,8 +119,19 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
                 amdc.quant_q8(X, Q, c // 32, stream=s)
             amdc.gemv(kind, M.dev[ci][i], Q, Y, r, c // 32, stream=s)
 
+    def step_fused(ci, s):  # the quantization fused into the first GEMV of each input (it writes the Q8 for the rest)
+        for i, (name, r, c) in enumerate(shapes):
+            if name not in share:
+                nxt = shapes[i + 1][0] if i + 1 < len(shapes) else None
+                amdc.gemv_x(kind, M.dev[ci][i], X, Y, r, c // 32, q8=Q if nxt in share else None, stream=s)
+            else:
+                amdc.gemv(kind, M.dev[ci][i], Q, Y, r, c // 32, stream=s)
+
     graphs = [timer.graph(lambda s, ci=ci: step_ops(ci, s)) for ci in range(M.copies)]
     ms = timer.replay_ms(graphs, steps, warmup)
+    del graphs
+    graphs = [timer.graph(lambda s, ci=ci: step_fused(ci, s)) for ci in range(M.copies)]
+    ms_fused = timer.replay_ms(graphs, steps, warmup)
     del graphs
     # each GEMV alone: one graph of back-to-back launches over the weight copies
     per, tot = {}, 0.0
@@ -133,7 +146,7 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
     set_bytes = sum(wbytes(r, c) for _, r, c in shapes)
     copies = M.copies
     del M
-    return {"set_bytes": set_bytes, "ms_per_step": ms, "per_shape": per, "kernel_GBps": set_bytes / tot / 1e6,
+    return {"set_bytes": set_bytes, "ms_per_step": ms, "ms_per_step_fused_quant": ms_fused, "per_shape": per, "kernel_GBps": set_bytes / tot / 1e6,
             "kernel_us_total": tot * 1e3, "weight_copies": copies}
 
 
@@ -150,6 +163,7 @@ def verify_set(steps, seed, timer):
         Q = amdc.DevBuf(T * xs)
         Y = amdc.DevBuf(4 * T * r)
         amdc.quant_q8(X, Q, nb, T, 4 * c, xs)
+        amdc.gemv_t(kind, M.dev[0][0], Q, Y, r, nb, T, xs, r)  # sizes the library's workspace before the capture
         t = timer.per_launch_ms(lambda j, s: amdc.gemv_t(kind, M.dev[j % M.copies][0], Q, Y, r, nb, T, xs, r, stream=s), M.copies)
         b = wbytes(r, c)
         out[name] = {"rows": r, "cols": c, "T": T, "us": round(t * 1e3, 3), "GB/s": round(b / t / 1e6, 1),
@@ -293,7 +307,7 @@ def main():
                    "weight_bytes_per_step": c1["set_bytes"], "rotation_copies_bytes": ROTATE_BYTES, "batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-                     "kernel": "amdc_gemv_q4_0_t1", "bytes_per_launch_avg": c1["set_bytes"] / len(c1["per_shape"])},
+                     "kernel": "amdc_gemv_q4_0_p1", "bytes_per_launch_avg": c1["set_bytes"] / len(c1["per_shape"])},
         "cpu_baseline": cpu,
         "detail": detail,
     }

@@ -106,9 +106,25 @@ int amdc_gemv_q4(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint
 int amdc_gemv_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                   void *stream);
 
+/* The decode GEMV fused with the Q8 quantization of its input: x is the f32
+ * vector (32 nb floats, 16-byte aligned); every workgroup quantizes it in its
+ * prologue, bit for bit as amdc_quant_q8, and when q8 is not NULL one of
+ * them also writes the Q8 buffer there (for other GEMVs of the same input).
+ * Replaces the pair OP_QUANT + OP_GEMV_Q4 / OP_GEMV_Q4K (src/hip.c:922-933,
+ * 1023-1024) with one launch; nb <= 480. No reference counterpart as one
+ * kernel (the reference fuses the quantization into the producer instead,
+ * kernels/ie_kernels.c:203-265). */
+int amdc_gemv_q4_x(const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res, uint8_t *q8,
+                   void *stream);
+int amdc_gemv_q4k_x(const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res, uint8_t *q8,
+                    void *stream);
+
 /* y_t = W x_t for T Q8 vectors (MTP verify, any T >= 1; the weights are
- * read once per 16 vectors): x_t at xq + t * xs bytes, y_t at y + t * ys
- * floats, res_t at res + t * rs floats. Replaces the multi-token branch of
+ * read once per 16 vectors, T <= 8 on int8 MFMA, the exact integer dots of
+ * ie_q4q8_block / ie_q4k_dot): x_t at xq + t * xs bytes, y_t at y + t * ys
+ * floats, res_t at res + t * rs floats. A library workspace holds split-K
+ * partial sums (allocated on the first call of a size: call once outside
+ * graph capture before capturing). Replaces the multi-token branch of
  * OP_GEMV_Q4K (ie_gemv_q4kq8_ts2 / _tr8 / _tr, src/hip.c:1004-1020); the
  * Q4_0 form has no reference kernel (the reference runs OP_GEMV_Q4 per
  * token, src/hip.c:1583-1588) and gives the same values as T calls of

@@ -149,9 +149,13 @@ def test_gemv_epilogue_bias_res(dev, orc, kind):
 
 # ---------------------------------------------------------------- multi-vector GEMV (verify)
 
+@pytest.mark.parametrize("path", [0, 1])  # 0: int8-MFMA verify kernel for T <= 8; 1: the dot4 kernels
 @pytest.mark.parametrize("T", [2, 5, 8, 9, 16, 19])
-@pytest.mark.parametrize("kind,rows,nb", [(0, 40, 128), (3, 33, 160), (3, 21, 544)])
-def test_gemv_multi(dev, orc, kind, rows, nb, T):
+@pytest.mark.parametrize("kind,rows,nb", [(0, 40, 128), (0, 130, 43), (3, 33, 160), (3, 21, 544), (3, 200, 72)])
+def test_gemv_multi(dev, orc, kind, rows, nb, T, path):
+    if path and T > 8:
+        pytest.skip("T > 8 uses the dot4 kernel in both paths")
+    dev.set_tuning(unroll=path)
     c = Case(dev, orc, kind, rows, nb, T, seed=T * 13 + nb)
     assert np.array_equal(c.quant(), c.xq)
     res = np.random.default_rng(T).standard_normal((T, rows)).astype(np.float32)
@@ -263,3 +267,24 @@ def test_gemm_deterministic(dev, orc, kern, ks):
     y = first.view(np.float32).reshape(T, rows)
     for t in (0, T - 1):
         assert rel_err(y[t], c.y_oracle(t), c.mag(t)) < TOL
+
+
+@pytest.mark.parametrize("kind,rows,nb", [(0, 70, 13), (0, 300, 128), (0, 64, 344), (3, 45, 160), (3, 20, 544)])
+def test_gemv_fused_quant(dev, orc, kind, rows, nb):
+    """The decode GEMV that quantizes its f32 input itself: its Q8 output equals cpu_quant_q8 bit for
+    bit, and y equals the separate quantize + GEMV launches bit for bit."""
+    c = Case(dev, orc, kind, rows, nb, seed=rows + nb, xscale=2.0)
+    g = np.random.default_rng(nb)
+    bias, res = g.standard_normal(rows).astype(np.float32), g.standard_normal(rows).astype(np.float32)
+    B, R = dev.DevBuf.of(bias), dev.DevBuf.of(res)
+    Q2, Y2 = dev.DevBuf(c.xs), dev.DevBuf(rows * 4)
+    Q2.fill(0)
+    dev.gemv_x(kind, c.W, c.X, Y2, rows, nb, bias=B, res=R, q8=Q2)
+    assert np.array_equal(Q2.download(np.uint8)[:40 * nb], c.xq[0])
+    c.quant()
+    dev.gemv(kind, c.W, c.Q, c.Y, rows, nb, bias=B, res=R)
+    assert np.array_equal(Y2.download(np.uint32), c.Y.download(np.uint32))
+    want = orc.epilogue(c.y_oracle(0), bias, res)
+    assert rel_err(Y2.download(np.float32), want, c.mag(0) + np.abs(bias) + np.abs(res)) < TOL
+    dev.gemv_x(kind, c.W, c.X, Y2, rows, nb)  # without the Q8 output
+    assert rel_err(Y2.download(np.float32), c.y_oracle(0), c.mag(0)) < TOL
