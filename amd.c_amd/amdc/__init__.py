@@ -46,6 +46,7 @@ ABI = {
     "amdc_stream_create": (C.c_int, [C.POINTER(_P)]),
     "amdc_stream_destroy": (C.c_int, [_P]),
     "amdc_stream_sync": (C.c_int, [_P]),
+    "amdc_stream_wait_event": (C.c_int, [_P, _P]),
     "amdc_graph_begin": (C.c_int, [_P]),
     "amdc_graph_end": (C.c_int, [_P, C.POINTER(_P)]),
     "amdc_graph_launch": (C.c_int, [_P, _P]),
@@ -199,6 +200,10 @@ class Stream:
 
     def sync(self):
         _check(lib().amdc_stream_sync(self.s))
+
+    def wait(self, event):
+        """Later work on this stream waits for `event` (an Event recorded on another stream)."""
+        _check(lib().amdc_stream_wait_event(self.s, event.ev))
 
     def __del__(self):
         try:

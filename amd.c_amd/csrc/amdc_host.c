@@ -145,6 +145,7 @@ static struct {
   hipError_t (*StreamCreate)(hipStream_t *);
   hipError_t (*StreamDestroy)(hipStream_t);
   hipError_t (*StreamSynchronize)(hipStream_t);
+  hipError_t (*StreamWaitEvent)(hipStream_t, hipEvent_t, unsigned);
   hipError_t (*StreamBeginCapture)(hipStream_t, int);
   hipError_t (*StreamEndCapture)(hipStream_t, hipGraph_t *);
   hipError_t (*GraphInstantiate)(hipGraphExec_t *, hipGraph_t, void *, char *, size_t);
@@ -244,6 +245,7 @@ static int hip_load(void) {
   SYM(StreamCreate, "hipStreamCreate");
   SYM(StreamDestroy, "hipStreamDestroy");
   SYM(StreamSynchronize, "hipStreamSynchronize");
+  SYM(StreamWaitEvent, "hipStreamWaitEvent");
   SYM(StreamBeginCapture, "hipStreamBeginCapture");
   SYM(StreamEndCapture, "hipStreamEndCapture");
   SYM(GraphInstantiate, "hipGraphInstantiate");
@@ -379,6 +381,11 @@ int amdc_stream_destroy(void *s) {
 int amdc_stream_sync(void *s) {
   NEED_OPEN();
   HIPCALL(H.StreamSynchronize(s));
+  return AMDC_OK;
+}
+int amdc_stream_wait_event(void *stream, void *ev) {
+  NEED_OPEN();
+  HIPCALL(H.StreamWaitEvent(stream, ev, 0));
   return AMDC_OK;
 }
 int amdc_graph_begin(void *stream) {

@@ -130,9 +130,11 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
     graphs = [timer.graph(lambda s, ci=ci: step_ops(ci, s)) for ci in range(M.copies)]
     ms = timer.replay_ms(graphs, steps, warmup)
     del graphs
-    graphs = [timer.graph(lambda s, ci=ci: step_fused(ci, s)) for ci in range(M.copies)]
-    ms_fused = timer.replay_ms(graphs, steps, warmup)
-    del graphs
+    ms_fused = None
+    if cfg_name == "c1":
+        graphs = [timer.graph(lambda s, ci=ci: step_fused(ci, s)) for ci in range(M.copies)]
+        ms_fused = timer.replay_ms(graphs, steps, warmup)
+        del graphs
     # each GEMV alone: one graph of back-to-back launches over the weight copies
     per, tot = {}, 0.0
     for i, (name, r, c) in enumerate(shapes):

@@ -82,6 +82,9 @@ int amdc_event_elapsed_ms(float *ms, void *start, void *stop);
 int amdc_stream_create(void **stream);
 int amdc_stream_destroy(void *stream);
 int amdc_stream_sync(void *stream);
+/* Later work on stream waits for event ev (recorded on another stream): the
+ * fork/join of independent operators, also inside a graph capture. */
+int amdc_stream_wait_event(void *stream, void *ev);
 int amdc_graph_begin(void *stream);
 int amdc_graph_end(void *stream, void **exec);
 int amdc_graph_launch(void *exec, void *stream);
