@@ -33,6 +33,7 @@ typedef u32 u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, u32 n) { return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)n, 0x00020000); }
 
 #define NT 256u
+#define QCH 17u // passes of 32 blocks whose activation loads are in flight together (fused quantization)
 
 // ------------------------------------------------------------------ helpers
 
@@ -258,13 +259,16 @@ struct Item {
   u32x4 h, n[8];
 };
 
+// The loads are unconditional (a lane past the last super-group reads the
+// row's first one again, inside the same wave's lines, and ignores it): no
+// branch joins them, so that a wait for an earlier load does not become a
+// wait for these.
 template <int KIND>
 __device__ __forceinline__ void load_item(Item &it, const uint8_t *wr, u32 ng, u32 g, bool ok) {
-  if (ok) {
-    it.h = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_header_off(g)));
+  g = ok ? g : 0u;
+  it.h = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_header_off(g)));
 #pragma unroll
-    for (u32 k = 0; k < 8u; k++) it.n[k] = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_nib_off(ng, g, k)));
-  }
+  for (u32 k = 0; k < 8u; k++) it.n[k] = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_nib_off(ng, g, k)));
 }
 
 template <int KIND>
@@ -309,27 +313,65 @@ __device__ __forceinline__ void gemv1_body(const uint8_t *__restrict__ W, const 
     const u32 r_ = g_ * rpg + wv * rpw + q;
     return W + (u64)(r_ < rows ? r_ : rows - 1u) * RB;
   };
-  Item cur, nxt;
-  load_item<KIND>(cur, rowp(rg), ng, l, l < ng);
-  if (FQ) { // quantize the f32 vector here, half a wave per block (the arithmetic of amdc_quant_q8)
-    const u32 j = tid & 31u;
-    for (u32 b0 = 0; b0 < nblk; b0 += 8u) {
-      const u32 b = b0 + (tid >> 5), p = (b & 7u) * ng + (b >> 3);
-      const float v = b < nb ? xf[32u * b + j] : 0.0f;
-      float a = __builtin_fabsf(v);
+  // Fused quantization (the arithmetic of amdc_quant_q8): 8 lanes per block,
+  // 4 values per lane, 32 blocks per pass of the workgroup. The activation
+  // loads of up to QCH passes are issued before the first weight item's, so
+  // that the quantization runs while the weights are in flight (loads count
+  // down in issue order); they are unconditional (a block past nb reads the
+  // last block again and takes zeros), so that no branch joins them. The max
+  // and the sum of a block's 8 lanes go by DPP (xor 1, xor 2, then the
+  // half-row mirror).
+  const u32 e = tid & 7u;
+  v4f xv[QCH];
+  auto xload = [&](u32 b0) {
 #pragma unroll
-      for (u32 o = 1; o < 32u; o <<= 1) a = __builtin_fmaxf(a, __shfl_xor(a, (int)o));
+    for (u32 c = 0; c < QCH; c++) {
+      const u32 b = b0 + 32u * c + (tid >> 3);
+      const v4f v = *(const v4f *)(xf + 32u * (b < nb ? b : nb - 1u) + 4u * e);
+      xv[c] = b < nb ? v : (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  };
+  auto xquant = [&](u32 b0) {
+#pragma unroll
+    for (u32 c = 0; c < QCH; c++) {
+      if (b0 + 32u * c >= nblk) break;
+      const u32 b = b0 + 32u * c + (tid >> 3);
+      float a = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(xv[c].x), __builtin_fabsf(xv[c].y)),
+                                __builtin_fmaxf(__builtin_fabsf(xv[c].z), __builtin_fabsf(xv[c].w)));
+      a = __builtin_fmaxf(a, dpp<0xB1>(a));
+      a = __builtin_fmaxf(a, dpp<0x4E>(a));
+      a = __builtin_fmaxf(a, dpp<0x141>(a));
       const float d = a / 127.0f;
-      const int qi = d != 0.0f ? (int)__builtin_roundf(v / d) : 0;
-      u32 sum = (u32)qi;
+      int qi[4];
 #pragma unroll
-      for (u32 o = 1; o < 32u; o <<= 1) sum += (u32)__shfl_xor((int)sum, (int)o);
-      ((uint8_t *)(j < 16u ? &s_lo[p] : &s_hi[p]))[j & 15u] = (uint8_t)qi;
-      if (j == 0u) s_d[p] = d, s_as[p] = sum;
-      if (q8out && blockIdx.x == 0u && b < nb) { // the Q8 buffer, for other consumers
-        ((int8_t *)q8out)[32u * b + j] = (int8_t)qi;
-        if (j == 0u) ((float *)(q8out + 32u * nb))[b] = d, ((u32 *)(q8out + 36u * nb))[b] = sum;
+      for (int m = 0; m < 4; m++) qi[m] = d != 0.0f ? (int)__builtin_roundf(xv[c][m] / d) : 0;
+      const u32 word = (u32)(qi[0] & 255) | (u32)(qi[1] & 255) << 8 | (u32)(qi[2] & 255) << 16 | (u32)qi[3] << 24;
+      u32 sum = (u32)qi[0] + (u32)qi[1] + (u32)qi[2] + (u32)qi[3];
+      sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0xB1, 0xF, 0xF, false);
+      sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0x4E, 0xF, 0xF, false);
+      sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0x141, 0xF, 0xF, false);
+      if (b < nblk) {
+        const u32 p = (b & 7u) * ng + (b >> 3);
+        ((u32 *)(e < 4u ? &s_lo[p] : &s_hi[p]))[e & 3u] = word;
+        if (e == 0u) s_d[p] = d, s_as[p] = sum;
       }
+      if (q8out && blockIdx.x == 0u && b < nb) { // the Q8 buffer, for other consumers
+        ((u32 *)(q8out + 32u * b))[e] = word;
+        if (e == 0u) ((float *)(q8out + 32u * nb))[b] = d, ((u32 *)(q8out + 36u * nb))[b] = sum;
+      }
+    }
+  };
+  Item cur, nxt;
+  if (FQ) {
+    xload(0);
+    __asm__ volatile("" ::: "memory"); // keep the activation loads ahead of the weight loads
+  }
+  load_item<KIND>(cur, rowp(rg), ng, l, l < ng);
+  if (FQ) {
+    xquant(0);
+    for (u32 b0 = 32u * QCH; b0 < nblk; b0 += 32u * QCH) {
+      xload(b0);
+      xquant(b0);
     }
   } else {
     for (u32 j = tid; j < nblk; j += NT) { // stage the whole Q8 vector (permuted)

@@ -1,19 +1,23 @@
 """Benchmark of the quantized GEMV/GEMM hot path on one MI355X.
 
 One "step" = one pass of the hot path over one batch-1 input through the
-configuration's GEMV set: for c1 (the headline, Llama-7B layer shapes, Q4_0)
-x -> Q8 -> q, k, v; Q8 -> o; Q8 -> gate, up; Q8 -> down; Q8 -> lm_head (5
-quantizations, 8 GEMVs; the form with each quantization fused into the
-prologue of the first GEMV of its input is timed too: it is slower, every
-workgroup quantizes the vector), with weight copies rotated so that the weights
-streamed per step come from HBM (the copies total >= 2 GB, far above the 256
-MB Infinity Cache). value = weight bytes of the step (the reference's
+configuration's GEMV set, dispatched as the reference engine runs it: for c1
+(the headline, Llama-7B layer shapes, Q4_0) the matrices that share an input
+are loaded as one matrix (wqkv = [wq; wk; wv], wgu = [wgate; wup], as
+src/model.c:696, 955 concat_mats), so a step is x -> qkv, o, gate_up, down,
+lm_head: 5 GEMVs, each on an f32 vector quantized to Q8 first (inside the
+GEMV's own launch where nb <= 128, else by a separate amdc_quant_q8 launch:
+7 launches). The same set as 8 separate GEMVs with 5 separate quantizations
+is timed too (ms_per_step_unmerged). Weight copies are rotated so that the
+weights streamed per step come from HBM (the copies total >= 2 GB, far above
+the 256 MB Infinity Cache). value = weight bytes of the step (the reference's
 rows * nb * 18, src/hip.c:1831) / step time, inputs resident in HBM.
 
 The step is captured once per weight copy as a HIP graph and the graphs are
 replayed back to back (no host launch per kernel), timed by HIP events on
 their stream; each GEMV's own duration comes from a graph of that GEMV
-launched back to back over the weight copies (the roofline's "achieved"). Also measured, in "detail": c0 (one 4096x4096 Q4_0 GEMV), c2 (Q4_K 27B
+launched back to back over the weight copies (the roofline's "achieved").
+Also measured, in "detail": c0 (one 4096x4096 Q4_0 GEMV), c2 (Q4_K 27B
 shapes), c3 (T = 8 verify GEMV, weights counted once) and c4 (the T = 256
 prefill GEMM, TOPS = 2 T rows cols / time), each from HIP events around every
 launch on the stream the kernels run on (graphs of back-to-back launches over
@@ -61,6 +65,7 @@ class Mats:
         self.set_bytes = sum(wbytes(r, c) for _, r, c in shapes)
         self.copies = max(1, -(-min_bytes // self.set_bytes))
         host = [amdc.repack(kind, synth.gguf(kind, r, c, seed + i), r, c) for i, (_, r, c) in enumerate(shapes)]
+        self.host = host
         self.dev = []
         for _ in range(self.copies):
             self.dev.append([amdc.DevBuf.of(h) for h in host])
@@ -100,42 +105,49 @@ class Timer:
 
 # ---------------------------------------------------------------- c1 (headline) and c0 / c2 sets
 
+# matrices that read the previous one's input; the reference engine loads each run of them as one
+# matrix (wqkv = [wq; wk; wv], wgu = [wgate; wup]: src/model.c:696, 955 concat_mats)
+SHARE = {"k", "v", "up", "ffn_up"}
+
+
+def merged_groups(shapes):
+    """[(name, rows, cols, [shape indices])]: runs of shapes with one input, concatenated by rows."""
+    out = []
+    for i, (name, r, c) in enumerate(shapes):
+        if name in SHARE and out:
+            n0, r0, c0, idx = out[-1]
+            out[-1] = (n0 + "+" + name, r0 + r, c0, idx + [i])
+        else:
+            out.append((name, r, c, [i]))
+    return out
+
+
 def gemv_set(cfg_name, steps, warmup, seed, timer):
-    """A batch-1 GEMV set (c0, c1, c2): the step as HIP graphs (one per weight copy), replayed;
-    and each GEMV alone, back to back over the weight copies in one graph."""
+    """A batch-1 GEMV set (c0, c1, c2). The step, as HIP graphs (one per weight copy) replayed:
+    - dispatched as the reference engine runs it: the matrices of one input concatenated (wqkv, wgu),
+      each GEMV on the f32 vector through amdc_gemv_q4_x / _q4k_x (the quantization fused into the
+      GEMV for nb <= 128, else a separate launch) -- ms_per_step;
+    - one GEMV per matrix, each input quantized by its own launch -- ms_per_step_unmerged.
+    Each GEMV kernel alone: a graph of that GEMV launched back to back over the weight copies."""
     cfg = synth.CONFIGS[cfg_name]
     kind, shapes = cfg["kind"], cfg["shapes"]
     M = Mats(kind, shapes, seed)
+    groups = merged_groups(shapes)
     cols_max = max(c for _, _, c in shapes)
+    rows_max = max(r for _, r, _, _ in groups)
     X = amdc.DevBuf.of(synth.activations(1, cols_max, seed + 99)[0])
     Q = amdc.DevBuf(q8_stride(cols_max // 32))
-    Y = amdc.DevBuf(4 * max(r for _, r, _ in shapes))
-    # a new Q8 vector before a matrix whose input differs from the previous one's (q/k/v, gate/up share)
-    share = {"k", "v", "up", "ffn_up"}
+    Y = amdc.DevBuf(4 * rows_max)
 
-    def step_ops(ci, s):
+    def step_unmerged(ci, s):
         for i, (name, r, c) in enumerate(shapes):
-            if name not in share:
+            if name not in SHARE:
                 amdc.quant_q8(X, Q, c // 32, stream=s)
             amdc.gemv(kind, M.dev[ci][i], Q, Y, r, c // 32, stream=s)
 
-    def step_fused(ci, s):  # the quantization fused into the first GEMV of each input (it writes the Q8 for the rest)
-        for i, (name, r, c) in enumerate(shapes):
-            if name not in share:
-                nxt = shapes[i + 1][0] if i + 1 < len(shapes) else None
-                amdc.gemv_x(kind, M.dev[ci][i], X, Y, r, c // 32, q8=Q if nxt in share else None, stream=s)
-            else:
-                amdc.gemv(kind, M.dev[ci][i], Q, Y, r, c // 32, stream=s)
-
-    graphs = [timer.graph(lambda s, ci=ci: step_ops(ci, s)) for ci in range(M.copies)]
-    ms = timer.replay_ms(graphs, steps, warmup)
+    graphs = [timer.graph(lambda s, ci=ci: step_unmerged(ci, s)) for ci in range(M.copies)]
+    ms_unmerged = timer.replay_ms(graphs, steps, warmup)
     del graphs
-    ms_fused = None
-    if cfg_name == "c1":
-        graphs = [timer.graph(lambda s, ci=ci: step_fused(ci, s)) for ci in range(M.copies)]
-        ms_fused = timer.replay_ms(graphs, steps, warmup)
-        del graphs
-    # each GEMV alone: one graph of back-to-back launches over the weight copies
     per, tot = {}, 0.0
     for i, (name, r, c) in enumerate(shapes):
         amdc.quant_q8(X, Q, c // 32)
@@ -145,11 +157,41 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
         per[name] = {"rows": r, "cols": c, "us": round(t * 1e3, 3), "GB/s": round(b / t / 1e6, 1),
                      "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4)}
         tot += t
-    set_bytes = sum(wbytes(r, c) for _, r, c in shapes)
-    copies = M.copies
+    host = M.host
     del M
-    return {"set_bytes": set_bytes, "ms_per_step": ms, "ms_per_step_fused_quant": ms_fused, "per_shape": per, "kernel_GBps": set_bytes / tot / 1e6,
-            "kernel_us_total": tot * 1e3, "weight_copies": copies}
+    # the merged matrices (row concatenation of the repacked matrices: the layout is row-major)
+    G = Mats.__new__(Mats)
+    G.set_bytes = sum(wbytes(r, c) for _, r, c, _ in groups)
+    G.copies = max(1, -(-ROTATE_BYTES // G.set_bytes))
+    hg = [np.concatenate([host[i] for i in idx]) for _, _, _, idx in groups]
+    G.dev = [[amdc.DevBuf.of(h) for h in hg] for _ in range(G.copies)]
+    del host, hg
+    for gi, (name, r, c, _) in enumerate(groups):  # first use sizes the library's workspace, before any capture
+        amdc.gemv_x(kind, G.dev[0][gi], X, Y, r, c // 32)
+
+    def step(ci, s):
+        for gi, (name, r, c, _) in enumerate(groups):
+            amdc.gemv_x(kind, G.dev[ci][gi], X, Y, r, c // 32, stream=s)
+
+    graphs = [timer.graph(lambda s, ci=ci: step(ci, s)) for ci in range(G.copies)]
+    ms = timer.replay_ms(graphs, steps, warmup)
+    del graphs
+    per_m, tot_m = {}, 0.0
+    for gi, (name, r, c, _) in enumerate(groups):
+        amdc.quant_q8(X, Q, c // 32)
+        t = timer.per_launch_ms(lambda j, s, gi=gi, r=r, c=c: amdc.gemv(kind, G.dev[j % G.copies][gi], Q, Y, r, c // 32, stream=s),
+                                G.copies, reps=max(2, steps // 4))
+        b = wbytes(r, c)
+        per_m[name] = {"rows": r, "cols": c, "us": round(t * 1e3, 3), "GB/s": round(b / t / 1e6, 1),
+                       "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4)}
+        tot_m += t
+    set_bytes = G.set_bytes
+    del G
+    return {"set_bytes": set_bytes, "ms_per_step": ms, "ms_per_step_unmerged": ms_unmerged,
+            "launches_per_step": sum(1 if (c // 32) <= 128 else 2 for _, _, c, _ in groups),
+            "per_shape": per, "per_merged_shape": per_m,
+            "kernel_GBps": set_bytes / tot_m / 1e6, "kernel_us_total": tot_m * 1e3,
+            "kernel_GBps_unmerged": set_bytes / tot / 1e6, "weight_copies": -(-ROTATE_BYTES // set_bytes)}
 
 
 def verify_set(steps, seed, timer):
@@ -305,11 +347,13 @@ def main():
         "dtype": "int8",
         "data": "synthetic (seeded: uniform nibbles, f16 |N(0,1)|*0.02 scales, N(0,1) activations)",
         "config": {"workload": "c1: Llama-7B layer GEMV set, Q4_0 x Q8, batch 1 (q,k,v,o 4096x4096; gate,up 11008x4096; "
-                               "down 4096x11008; lm_head 32000x4096) + 5 Q8 quantizations per step",
+                               "down 4096x11008; lm_head 32000x4096), f32 inputs quantized to Q8 in the step; q,k,v and "
+                               "gate,up run as the concatenated wqkv 12288x4096 and wgu 22016x4096 (src/model.c:696,955)",
+                   "launches_per_step": c1["launches_per_step"], "ms_per_step_unmerged": round(c1["ms_per_step_unmerged"], 4),
                    "weight_bytes_per_step": c1["set_bytes"], "rotation_copies_bytes": ROTATE_BYTES, "batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-                     "kernel": "amdc_gemv_q4_0_p1", "bytes_per_launch_avg": c1["set_bytes"] / len(c1["per_shape"])},
+                     "kernel": "amdc_gemv_q4_0_p1", "bytes_per_launch_avg": c1["set_bytes"] / len(c1["per_merged_shape"])},
         "cpu_baseline": cpu,
         "detail": detail,
     }

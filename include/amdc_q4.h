@@ -109,14 +109,16 @@ int amdc_gemv_q4(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint
 int amdc_gemv_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                   void *stream);
 
-/* The decode GEMV fused with the Q8 quantization of its input: x is the f32
- * vector (32 nb floats, 16-byte aligned); every workgroup quantizes it in its
- * prologue, bit for bit as amdc_quant_q8, and when q8 is not NULL one of
- * them also writes the Q8 buffer there (for other GEMVs of the same input).
- * Replaces the pair OP_QUANT + OP_GEMV_Q4 / OP_GEMV_Q4K (src/hip.c:922-933,
- * 1023-1024) with one launch; nb <= 480. No reference counterpart as one
- * kernel (the reference fuses the quantization into the producer instead,
- * kernels/ie_kernels.c:203-265). */
+/* The decode GEMV of an f32 input x (32 nb floats, 16-byte aligned): the
+ * pair OP_QUANT + OP_GEMV_Q4 / OP_GEMV_Q4K (src/hip.c:922-933, 1023-1024).
+ * For nb <= 128 (AMDC_GEMVX_FUSE_NB) one launch: every workgroup quantizes x
+ * in its prologue, bit for bit as amdc_quant_q8, and when q8 is not NULL one
+ * of them also writes the Q8 buffer there (for other GEMVs of the same
+ * input). For larger nb, amdc_quant_q8 into q8 and the GEMV (two launches);
+ * with q8 NULL the Q8 vector goes to the library's workspace, which grows on
+ * first use (make one call before a graph capture). y is the same either way.
+ * No reference counterpart as one kernel (the reference fuses the
+ * quantization into the producer instead, kernels/ie_kernels.c:203-265). */
 int amdc_gemv_q4_x(const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res, uint8_t *q8,
                    void *stream);
 int amdc_gemv_q4k_x(const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res, uint8_t *q8,

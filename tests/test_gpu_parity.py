@@ -288,3 +288,31 @@ def test_gemv_fused_quant(dev, orc, kind, rows, nb):
     assert rel_err(Y2.download(np.float32), want, c.mag(0) + np.abs(bias) + np.abs(res)) < TOL
     dev.gemv_x(kind, c.W, c.X, Y2, rows, nb)  # without the Q8 output
     assert rel_err(Y2.download(np.float32), c.y_oracle(0), c.mag(0)) < TOL
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind,nb", [(0, 120), (3, 120), (0, 136), (3, 136)])
+def test_gemv_fused_quant_special_blocks(dev, orc, kind, nb):
+    """The fused quantization on blocks that stress rounding: an all-zero block (d = 0), a block of
+    exact .5 ties of x / d, a single non-zero value, and denormal-sized values; its Q8 output equals
+    cpu_quant_q8 bit for bit."""
+    rows = 96
+    c = Case(dev, orc, kind, rows, nb, seed=7)
+    x = c.x.copy()
+    x[0, 0:32] = 0.0
+    x[0, 32:64] = np.arange(32, dtype=np.float32) - 15.5  # d = 1 below: every x / d a tie
+    x[0, 63] = 127.0
+    x[0, 64:96] = 0.0
+    x[0, 70] = -3.0
+    x[0, 96:128] = np.float32(1e-42) * np.arange(1, 33, dtype=np.float32)
+    x[0, 32 * (nb - 1):] *= 1e6
+    want_q = orc.quant_q8(x)[0]
+    X, Q2, Y2 = dev.DevBuf.of(x), dev.DevBuf(c.xs), dev.DevBuf(rows * 4)
+    Q2.fill(0)
+    dev.gemv_x(kind, c.W, X, Y2, rows, nb, q8=Q2)
+    assert np.array_equal(Q2.download(np.uint8)[:40 * nb], want_q)
+    Q1, Y1 = dev.DevBuf(c.xs), dev.DevBuf(rows * 4)
+    dev.quant_q8(X, Q1, nb)
+    assert np.array_equal(Q1.download(np.uint8)[:40 * nb], want_q)
+    dev.gemv(kind, c.W, Q1, Y1, rows, nb)
+    assert np.array_equal(Y2.download(np.uint32), Y1.download(np.uint32))
