@@ -61,7 +61,7 @@ ABI = {
     "amdc_gemm_q4k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_op_gemv": (C.c_int, [C.c_int, _P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_block_dots": (C.c_int, [C.c_int, _P, _P, _P, _U32, _U32, _P]),
-    "amdc_set_tuning": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "amdc_set_tuning": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "amdc_probe_read": (C.c_int, [_P, C.c_size_t, _P, _U32, _P]),
     "amdc_probe_copy": (C.c_int, [_P, _P, C.c_size_t, _U32, _P]),
 }
@@ -108,8 +108,8 @@ def cu_count():
     return lib().amdc_cu_count()
 
 
-def set_tuning(lanes=0, unroll=0, wgs=0, gemm_kernel=0, gemm_ksplit=0):
-    _check(lib().amdc_set_tuning(lanes, unroll, wgs, gemm_kernel, gemm_ksplit))
+def set_tuning(lanes=0, unroll=0, wgs=0, gemm_kernel=0, gemm_ksplit=0, form=0):
+    _check(lib().amdc_set_tuning(lanes, unroll, wgs, gemm_kernel, gemm_ksplit, form))
 
 
 def sync():

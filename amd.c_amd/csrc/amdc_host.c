@@ -181,6 +181,8 @@ enum {
   K_GEMV_Q4K_V8,
   K_GEMV_Q4_X1,
   K_GEMV_Q4K_X1,
+  K_GEMV_Q4_P2,
+  K_GEMV_Q4K_P2,
   K_N
 };
 static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1",  "amdc_gemv_q4_k_t1",  "amdc_gemv_q4_0_t1u1",
@@ -189,13 +191,14 @@ static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1
                                        "amdc_gemm_q4_k_n64",  "amdc_gemv_q4_0_p1",  "amdc_gemv_q4_k_p1",  "amdc_probe_read",
                                        "amdc_probe_copy",     "amdc_q8_prep",       "amdc_gemmh_m64_n128", "amdc_gemmh_m64_n64",
                                        "amdc_gemm_reduce",    "amdc_gemv_q4_0_v8",  "amdc_gemv_q4_k_v8",
-                                       "amdc_gemv_q4_0_x1",   "amdc_gemv_q4_k_x1"};
+                                       "amdc_gemv_q4_0_x1",   "amdc_gemv_q4_k_x1",  "amdc_gemv_q4_0_p2",  "amdc_gemv_q4_k_p2"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
 static int g_open, g_cus;
 static int t_lanes = -1, t_unroll = -1, t_wgs = -1, t_gemm = -1, t_gemm_min = -1, t_ksplit = -1;
-static u32 x_fuse_nb = 128; /* amdc_gemv_q4_x / _q4k_x: the largest nb quantized inside the GEMV */
+static u32 x_fuse_nb = 128;
+static int t_form = 0; /* decode GEMV: 1 = amdc_gemv_*_p1, 2 = amdc_gemv_*_p2, 0 = by shape */ /* amdc_gemv_q4_x / _q4k_x: the largest nb quantized inside the GEMV */
 /* The GEMM's device workspace (prepared activations, split-K partial sums): grown on demand. */
 static void *g_ws;
 static size_t g_ws_bytes;
@@ -285,6 +288,7 @@ int amdc_open(const char *hsaco) {
   if (t_ksplit < 0) t_ksplit = envi("AMDC_GEMM_KSPLIT", 0);
   if (t_gemm_min < 0) t_gemm_min = envi("IE_GEMM_MIN", 17);
   x_fuse_nb = (u32)envi("AMDC_GEMVX_FUSE_NB", 128);
+  t_form = envi("AMDC_GEMV_FORM", 0);
   g_open = 1;
   return AMDC_OK;
 }
@@ -299,14 +303,15 @@ void amdc_close(void) {
 
 int amdc_cu_count(void) { return g_open ? g_cus : 0; }
 
-int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kernel, int gemm_ksplit) {
+int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kernel, int gemm_ksplit, int gemv_form) {
   if (gemv_lanes && (gemv_lanes < 4 || gemv_lanes > 64 || (gemv_lanes & (gemv_lanes - 1))))
     return fail(AMDC_EINVAL, "gemv lanes %d: 4..64, a power of two", gemv_lanes);
   if (gemv_unroll < 0 || gemv_unroll > 2) return fail(AMDC_EINVAL, "gemv unroll %d: 0, 1 or 2", gemv_unroll);
   if (gemm_kernel < 0 || gemm_kernel > 4) return fail(AMDC_EINVAL, "gemm kernel %d: 0..4", gemm_kernel);
   if (gemm_ksplit < 0 || gemm_ksplit > 16) return fail(AMDC_EINVAL, "gemm ksplit %d: 0..16", gemm_ksplit);
   if (gemv_wgs < 0) return fail(AMDC_EINVAL, "gemv workgroups %d", gemv_wgs);
-  t_lanes = gemv_lanes, t_unroll = gemv_unroll, t_wgs = gemv_wgs, t_gemm = gemm_kernel, t_ksplit = gemm_ksplit;
+  if (gemv_form < 0 || gemv_form > 2) return fail(AMDC_EINVAL, "gemv form %d: 0, 1 or 2", gemv_form);
+  t_lanes = gemv_lanes, t_unroll = gemv_unroll, t_wgs = gemv_wgs, t_gemm = gemm_kernel, t_ksplit = gemm_ksplit, t_form = gemv_form;
   return AMDC_OK;
 }
 
@@ -491,6 +496,23 @@ static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uin
   if (GC > ng) GC = ng;
   const u32 lds = 320u * TT * GC;
   const unsigned grid = t_wgs > 0 && (u32)t_wgs < nrg ? (unsigned)t_wgs : nrg;
+  const int form = t_form > 0 ? t_form : ng > 32u ? 2 : 1;
+  if (TT == 1u && t_unroll <= 0 && form == 2 && (u64)rows * 144u * ng + 144u * ng < (1ull << 32)) {
+    /* the decode kernel with buffer loads, for long rows: up to 3 super-groups per lane (it keeps
+       the next one in flight), at most 2 workgroups per CU; LDS for the vector and the
+       workgroup's results. Measured on MI355X: 4096 x 11008 Q4_0 8.6 us (9.5 with the
+       amdc_gemv_*_p1 split), 5120 x 17408 Q4_K 14.7 (15.8). */
+    u32 L2 = 4u;
+    while (L2 < 64u && 3u * L2 < ng) L2 <<= 1;
+    if (t_lanes > 0) L2 = (u32)t_lanes;
+    const u32 rpg2 = 4u * (64u / L2), nrg2 = (rows + rpg2 - 1u) / rpg2, cap = 2u * (g_cus > 0 ? (u32)g_cus : 256u);
+    const unsigned g2 = t_wgs > 0 && (u32)t_wgs < nrg2 ? (unsigned)t_wgs : nrg2 < cap ? nrg2 : cap;
+    const u32 lds2 = 320u * ng + 4u * rpg2 * ((nrg2 + g2 - 1u) / g2);
+    if (lds2 <= GEMV_LDS_T1) {
+      void *a2[] = {&w, &xq, &y, &rows, &nb, &bias, &res, (void *)&L2};
+      return launch(kind ? K_GEMV_Q4K_P2 : K_GEMV_Q4_P2, g2, 1, lds2, stream, a2);
+    }
+  }
   if (TT == 1u && t_unroll <= 0 && 320u * ng <= GEMV_LDS_T1) { /* the pipelined decode kernel */
     const unsigned g1 = t_wgs > 0 && (u32)t_wgs < nrg ? (unsigned)t_wgs : nrg;
     void *a1[] = {&w, &xq, &y, &rows, &nb, &bias, &res, (void *)&L};

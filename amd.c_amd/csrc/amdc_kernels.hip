@@ -33,6 +33,7 @@ typedef u32 u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, u32 n) { return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)n, 0x00020000); }
 
 #define NT 256u
+#define SCH 3u  // Q8 blocks per thread whose staging loads are in flight together (decode GEMV)
 #define QCH 17u // passes of 32 blocks whose activation loads are in flight together (fused quantization)
 
 // ------------------------------------------------------------------ helpers
@@ -430,6 +431,142 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_0_x1(const uint8_
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_x1(const uint8_t *W, const float *x, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 L, uint8_t *q8) {
   gemv1_body<AMDC_Q4_K, true>(W, nullptr, y, rows, nb, bias, res, L, x, q8);
+}
+
+// The decode GEMV, second form: the same lane split, LDS layout and
+// per-block arithmetic as gemv1_body, with the weights read through a buffer
+// resource (32-bit offsets; the host checks rows * row bytes + row bytes <
+// 2^32) so that an item past the end -- a lane past the last super-group, a
+// row past the last, the prefetch after the workgroup's last item -- is a
+// load out of range, which returns zeros and touches no memory. No load is
+// then under a branch, and the loop over a workgroup's items (row groups
+// blockIdx.x, + gridDim.x, ...; ceil(ng / L) items per lane each) keeps one
+// item in flight while it computes the previous one: two item buffers
+// alternate (a 2-way unrolled loop: no register copy, which would wait for
+// the loads). The bias and residual values of an item's row come with it
+// (loads out of range when absent).
+struct Item2 {
+  Item w;
+  float b, r;
+};
+
+template <int KIND>
+__device__ __forceinline__ void gemv2_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
+                                           u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 L) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const u32 ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw;
+  const u32 nrg = (rows + rpg - 1u) / rpg, ni = (ng + L - 1u) / L;
+  if (blockIdx.x >= nrg) return; // the whole workgroup
+  const u32 RB = 144u * ng, NR = rows * RB; // the host checks NR + RB < 2^32
+  const u32 nblk = 8u * ng;
+  u32x4 *s_lo = (u32x4 *)smem;
+  u32x4 *s_hi = s_lo + nblk;
+  float *s_d = (float *)(s_hi + nblk);
+  u32 *s_as = (u32 *)(s_d + nblk);
+  const __amdgpu_buffer_rsrc_t rw = rsrc(W, NR), rb = rsrc(bias, bias ? 4u * rows : 0u), rr = rsrc(res, res ? 4u * rows : 0u);
+  const u32 n = ((nrg - blockIdx.x + gridDim.x - 1u) / gridDim.x) * ni; // items per lane
+  const u32 rbase = wv * rpw + q;
+
+  // an item's loads: position (j, i) = row group blockIdx.x + j gridDim.x, super-group l + L i
+  auto load = [&](Item2 &it, u32 f, u32 j, u32 i) {
+    const u32 r = (blockIdx.x + j * gridDim.x) * rpg + rbase, g = l + L * i;
+    const bool ok = f < n && g < ng && r < rows;
+    const u32 t = g >> 3, gt = ng - 8u * t < 8u ? ng - 8u * t : 8u;
+    const u32 base = ok ? r * RB : NR;
+    it.w.h = __builtin_amdgcn_raw_buffer_load_b128(rw, base + 16u * g, 0, 0);
+    const u32 o0 = base + 16u * ng + 1024u * t + 16u * (g & 7u);
+#pragma unroll
+    for (u32 k = 0; k < 8u; k++) it.w.n[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, o0 + 16u * gt * k, 0, 0);
+    const u32 ro = f < n && r < rows ? 4u * r : 0xFFFFFFF0u;
+    it.b = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, ro, 0, 0));
+    it.r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, ro, 0, 0));
+  };
+
+  // stage the Q8 vector: the loads of the first SCH blocks per thread go out
+  // ahead of the first item's
+  u32x4 slo[SCH], shi[SCH];
+  float sd[SCH];
+  u32 sa[SCH];
+  auto sload = [&](u32 i, u32 c) { // slot i <- block tid + NT c
+    const u32 jb = tid + NT * c, jj = jb < nb ? jb : nb - 1u;
+    slo[i] = *(const u32x4 *)(xq + 32u * jj);
+    shi[i] = *(const u32x4 *)(xq + 32u * jj + 16u);
+    sd[i] = ((const float *)(xq + 32u * nb))[jj];
+    sa[i] = ((const u32 *)(xq + 36u * nb))[jj];
+  };
+  auto sstore = [&](u32 i, u32 c) {
+    const u32 jb = tid + NT * c;
+    if (jb < nblk) {
+      const u32 p = (jb & 7u) * ng + (jb >> 3);
+      const bool in = jb < nb;
+      s_lo[p] = in ? slo[i] : (u32x4)(0u), s_hi[p] = in ? shi[i] : (u32x4)(0u);
+      s_d[p] = in ? sd[i] : 0.0f, s_as[p] = in ? sa[i] : 0u;
+    }
+  };
+  for (u32 c = SCH; NT * c < nblk; c++) { // past SCH blocks per thread (more than 24576 columns)
+    sload(0, c);
+    sstore(0, c);
+  }
+#pragma unroll
+  for (u32 c = 0; c < SCH; c++) sload(c, c);
+  __asm__ volatile("" ::: "memory"); // the activation loads ahead of the weight loads
+  Item2 A, B;
+  load(A, 0u, 0u, 0u);
+#pragma unroll
+  for (u32 c = 0; c < SCH; c++) sstore(c, c);
+  __syncthreads();
+
+  // the results of the workgroup's rows collect in LDS (after the staged
+  // vector) and go out after the loop: a store inside the loop would make the
+  // reuse of its registers wait for every load in flight
+  float *s_y = (float *)(s_as + nblk);
+  float acc = 0.0f;
+  auto comp = [&](const Item2 &it, u32 j, u32 i) {
+    const u32 g = l + L * i;
+    const float a2 = item_dot<KIND>(it.w, g < ng ? g : 0u, ng, s_lo, s_hi, s_d, s_as, acc);
+    acc = g < ng ? a2 : acc;
+    if (i == ni - 1u) { // the row group is done
+      const float v = seg_sum(acc, L);
+      float o = bias ? v + it.b : v;
+      o = res ? it.r + o : o;
+      if (l == 0u) s_y[j * rpg + rbase] = o;
+      acc = 0.0f;
+    }
+  };
+  u32 cj = 0, ci = 0, lj = 0, li = 0; // compute / load positions
+  auto adv = [&](u32 &j, u32 &i) {
+    if (++i == ni) i = 0, j++;
+  };
+  adv(lj, li);
+  for (u32 f = 0; f < n; f += 2u) {
+    load(B, f + 1u, lj, li);
+    adv(lj, li);
+    __asm__ volatile("" ::: "memory"); // the next item's loads go out before this item's arithmetic
+    comp(A, cj, ci);
+    adv(cj, ci);
+    if (f + 1u >= n) break;
+    load(A, f + 2u, lj, li);
+    adv(lj, li);
+    __asm__ volatile("" ::: "memory");
+    comp(B, cj, ci);
+    adv(cj, ci);
+  }
+  __syncthreads();
+  const u32 ny = (n / ni) * rpg;
+  for (u32 k = tid; k < ny; k += NT) {
+    const u32 r = (blockIdx.x + (k / rpg) * gridDim.x) * rpg + k % rpg;
+    if (r < rows) y[r] = s_y[k];
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_0_p2(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+                                                                   const float *bias, const float *res, u32 L) {
+  gemv2_body<AMDC_Q4_0>(W, xq, y, rows, nb, bias, res, L);
+}
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_p2(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+                                                                   const float *bias, const float *res, u32 L) {
+  gemv2_body<AMDC_Q4_K>(W, xq, y, rows, nb, bias, res, L);
 }
 
 // ------------------------------------------------------------------ bandwidth probes

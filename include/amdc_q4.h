@@ -167,9 +167,13 @@ int amdc_block_dots(int kind, const void *w, const uint8_t *xq, int32_t *out, ui
  * kernel with 1 or 2 super-groups of loads per step); workgroups of a GEMV
  * launch; the GEMM kernel (1, 2: int8 MFMA with 64 or 128 tokens per
  * workgroup; 3, 4: f16 MFMA, rows x tokens 64x128, 64x64);
- * the GEMM's K split (1..16). Also read once from the environment:
- * AMDC_GEMV_L, AMDC_GEMV_U, AMDC_GEMV_WG, AMDC_GEMM_KERNEL, AMDC_GEMM_KSPLIT. */
-int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kernel, int gemm_ksplit);
+ * the GEMM's K split (1..16); the decode kernel's form when gemv_unroll is 0
+ * (1: the split across whole rows, 2: the buffer-load form that keeps the
+ * next super-group in flight; 0: form 2 for rows of more than 32
+ * super-groups). Also read once from the environment: AMDC_GEMV_L,
+ * AMDC_GEMV_U, AMDC_GEMV_WG, AMDC_GEMM_KERNEL, AMDC_GEMM_KSPLIT,
+ * AMDC_GEMV_FORM. */
+int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kernel, int gemm_ksplit, int gemv_form);
 
 /* Bandwidth yardsticks (no reference counterpart): stream nbytes (a multiple
  * of 16) through a plain read kernel (one u32 per workgroup may be written to

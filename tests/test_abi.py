@@ -40,7 +40,7 @@ def test_dynamic_symbols():
 def test_kernel_names_in_code_object():
     host = open(os.path.join(ROOT, "amd.c_amd", "csrc", "amdc_host.c")).read()
     names = re.findall(r'"(amdc_(?:quant|gemv|gemm|dots|probe|q8)\w*)"', host)
-    assert len(names) == 25
+    assert len(names) == 27
     blob = open(amdc.HSACO_PATH, "rb").read()
     for n in names:
         assert n.encode() in blob, n
@@ -59,9 +59,10 @@ def test_bad_arguments_rejected_before_launch():
     # kind / shape checks run on the host after the open check; without a GPU they report not-open
     rc = L.amdc_op_gemv(7, None, None, None, 1, 1, None, None, 1, 0, 0, 0, None)
     assert rc != 0
-    assert L.amdc_set_tuning(3, 0, 0, 0, 0) == 1 and b"power of two" in L.amdc_last_error()
-    assert L.amdc_set_tuning(0, 0, 0, 9, 0) == 1
-    assert L.amdc_set_tuning(0, 0, 0, 0, 0) == 0
+    assert L.amdc_set_tuning(3, 0, 0, 0, 0, 0) == 1 and b"power of two" in L.amdc_last_error()
+    assert L.amdc_set_tuning(0, 0, 0, 9, 0, 0) == 1
+    assert L.amdc_set_tuning(0, 0, 0, 0, 0, 3) == 1
+    assert L.amdc_set_tuning(0, 0, 0, 0, 0, 0) == 0
 
 
 def test_open_without_gpu_fails_cleanly():

@@ -119,22 +119,25 @@ def test_gemv_t1(dev, orc, kind, rows, nb):
 
 
 @pytest.mark.parametrize("lanes", [4, 8, 16, 32, 64])
-@pytest.mark.parametrize("unroll", [0, 1, 2])
-@pytest.mark.parametrize("kind,rows,nb", [(0, 70, 344), (3, 45, 160), (3, 6, 544)])
-def test_gemv_t1_tunings(dev, orc, kind, rows, nb, lanes, unroll):
-    c = Case(dev, orc, kind, rows, nb, seed=lanes + unroll)
+@pytest.mark.parametrize("unroll,form", [(0, 1), (0, 2), (1, 0), (2, 0)])
+@pytest.mark.parametrize("wgs", [0, 3])  # 3 workgroups: each loops over several row groups
+@pytest.mark.parametrize("kind,rows,nb", [(0, 70, 344), (0, 33, 300), (3, 45, 160), (3, 6, 544)])
+def test_gemv_t1_tunings(dev, orc, kind, rows, nb, lanes, unroll, form, wgs):
+    c = Case(dev, orc, kind, rows, nb, seed=lanes + unroll + form)
     c.quant()
-    dev.set_tuning(lanes, unroll, 3)  # 3 workgroups: each loops over several row groups
+    dev.set_tuning(lanes, unroll, wgs, form=form)
     dev.gemv(kind, c.W, c.Q, c.Y, rows, nb)
     err = rel_err(c.y_gpu()[0], c.y_oracle(0), c.mag(0))
     assert err < TOL, err
 
 
 @pytest.mark.parametrize("kind", [0, 3])
-def test_gemv_epilogue_bias_res(dev, orc, kind):
+@pytest.mark.parametrize("form", [1, 2])
+def test_gemv_epilogue_bias_res(dev, orc, kind, form):
     rows, nb = 50, 64
     c = Case(dev, orc, kind, rows, nb, seed=77)
     c.quant()
+    dev.set_tuning(form=form)
     g = np.random.default_rng(5)
     bias, res = g.standard_normal(rows).astype(np.float32), g.standard_normal(rows).astype(np.float32)
     B, R = dev.DevBuf.of(bias), dev.DevBuf.of(res)
@@ -144,6 +147,9 @@ def test_gemv_epilogue_bias_res(dev, orc, kind):
     assert err < TOL, err
     dev.gemv(kind, c.W, c.Q, c.Y, rows, nb, res=R)
     err = rel_err(c.y_gpu()[0], orc.epilogue(c.y_oracle(0), None, res), c.mag(0) + np.abs(res))
+    assert err < TOL, err
+    dev.gemv(kind, c.W, c.Q, c.Y, rows, nb, bias=B)
+    err = rel_err(c.y_gpu()[0], orc.epilogue(c.y_oracle(0), bias, None), c.mag(0) + np.abs(bias))
     assert err < TOL, err
 
 
