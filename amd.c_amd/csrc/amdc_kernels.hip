@@ -1035,15 +1035,21 @@ GEMMH_KERNEL(amdc_gemmh_m64_n128, 4)
 GEMMH_KERNEL(amdc_gemmh_m64_n64, 2)
 
 // The split-K sums: y[t][r] = part[0][t][r] + part[1][t][r] + ... (in split
-// order), then the epilogue.
+// order), then the epilogue. All nks (<= 16) loads are issued before the
+// first add (a split past nks reads split 0 again and is not added).
 extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *__restrict__ part, u32 nks, float *__restrict__ y, u32 rows,
                                                                    u32 T, const float *__restrict__ bias, const float *__restrict__ res,
                                                                    u32 ys, u32 rs) {
   const u64 i = (u64)blockIdx.x * NT + threadIdx.x;
   if (i >= (u64)rows * T) return;
   const u32 t = (u32)(i / rows), r = (u32)(i - (u64)t * rows);
-  float o = part[i];
-  for (u32 k = 1; k < nks; k++) o += part[(u64)k * rows * T + i];
+  const u64 step = (u64)rows * T;
+  float v[16];
+#pragma unroll
+  for (u32 k = 0; k < 16u; k++) v[k] = part[(k < nks ? k : 0u) * step + i];
+  float o = v[0];
+#pragma unroll
+  for (u32 k = 1; k < 16u; k++) o = k < nks ? o + v[k] : o;
   if (bias) o = o + bias[r];
   if (res) o = res[(u64)t * rs + r] + o;
   y[(u64)t * ys + r] = o;

@@ -322,3 +322,31 @@ def test_gemv_fused_quant_special_blocks(dev, orc, kind, nb):
     assert np.array_equal(Q1.download(np.uint8)[:40 * nb], want_q)
     dev.gemv(kind, c.W, Q1, Y1, rows, nb)
     assert np.array_equal(Y2.download(np.uint32), Y1.download(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", [0, 3])
+def test_verify_splitk(dev, orc, kind):
+    """The T <= 8 verify kernel with K split over workgroups (partial sums added in split order by the reduce
+    kernel): calls in a row with different splits, bias and residual all match the oracle, and a repeated
+    split gives the same bits."""
+    rows, nb, T = 200, 544, 8
+    c = Case(dev, orc, kind, rows, nb, T, seed=21)
+    c.quant()
+    g = np.random.default_rng(3)
+    bias = g.standard_normal(rows).astype(np.float32)
+    res = g.standard_normal((T, rows)).astype(np.float32)
+    B, R = dev.DevBuf.of(bias), dev.DevBuf.of(res)
+    bits = {}
+    for ks in (1, 9, 4, 9, 2, 4):
+        dev.set_tuning(gemm_ksplit=ks)
+        c.Y.fill(0)
+        dev.gemv_t(kind, c.W, c.Q, c.Y, rows, nb, T, c.xs, rows, rs=rows, bias=B, res=R)
+        y = c.y_gpu()
+        for t in range(T):
+            want = orc.epilogue(c.y_oracle(t), bias, res[t])
+            assert rel_err(y[t], want, c.mag(t) + np.abs(bias) + np.abs(res[t])) < TOL, (ks, t)
+        u = y.view(np.uint32).copy()
+        if ks in bits:
+            assert np.array_equal(u, bits[ks]), ks
+        bits[ks] = u
