@@ -64,7 +64,19 @@ ABI = {
     "amdc_set_tuning": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "amdc_probe_read": (C.c_int, [_P, C.c_size_t, _P, _U32, _P]),
     "amdc_probe_copy": (C.c_int, [_P, _P, C.c_size_t, _U32, _P]),
+    "amdc_chain_create": (C.c_int, [_P, _U32, C.POINTER(_P)]),
+    "amdc_chain_launch": (C.c_int, [_P, _P]),
+    "amdc_chain_check": (C.c_int, [_P]),
+    "amdc_chain_destroy": (C.c_int, [_P]),
 }
+
+CHAIN_QUANT, CHAIN_GEMV = 0, 1
+
+
+class ChainOp(C.Structure):
+    """amdc_chain_op of include/amdc_q4.h."""
+    _fields_ = [("type", C.c_int), ("kind", C.c_int), ("sync", C.c_int), ("rows", _U32), ("nb", _U32),
+                ("w", _P), ("x", _P), ("q", _P), ("xq", _P), ("y", _P), ("bias", _P), ("res", _P)]
 
 
 class AmdcError(RuntimeError):
@@ -319,3 +331,34 @@ def probe_read(src, nbytes, scratch, grid, stream=None):
 
 def probe_copy(dst, src, nbytes, grid, stream=None):
     _check(lib().amdc_probe_copy(_p(dst), _p(src), nbytes, grid, stream))
+
+
+def chain_quant(x, q, nb, sync=True):
+    """A quantize operation of a GEMV chain: x (f32) -> q (Q8)."""
+    return ChainOp(CHAIN_QUANT, 0, int(sync), 0, nb, None, _p(x), _p(q), None, None, None, None)
+
+
+def chain_gemv(kind, w, xq, y, rows, nb, bias=None, res=None, sync=True):
+    """A decode-GEMV operation of a GEMV chain: w, xq (Q8) -> y."""
+    return ChainOp(CHAIN_GEMV, kind, int(sync), rows, nb, _p(w), None, None, _p(xq), _p(y), _p(bias), _p(res))
+
+
+class Chain:
+    """amdc_chain_create / _launch / _check / _destroy: a list of ChainOp run by one launch."""
+
+    def __init__(self, ops):
+        arr = (ChainOp * len(ops))(*ops)
+        h = _P()
+        _check(lib().amdc_chain_create(C.cast(arr, _P), len(ops), C.byref(h)))
+        self.h = h
+
+    def launch(self, stream=None):
+        _check(lib().amdc_chain_launch(self.h, stream))
+
+    def check(self):
+        _check(lib().amdc_chain_check(self.h))
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            lib().amdc_chain_destroy(self.h)
+            self.h = None

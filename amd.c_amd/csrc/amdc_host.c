@@ -152,6 +152,7 @@ static struct {
   hipError_t (*GraphDestroy)(hipGraph_t);
   hipError_t (*GraphLaunch)(hipGraphExec_t, hipStream_t);
   hipError_t (*GraphExecDestroy)(hipGraphExec_t);
+  hipError_t (*OccupancyMaxActiveBlocks)(int *, hipFunction_t, int, size_t);
 } H;
 
 /* The kernels of amdc_kernels.hip. */
@@ -183,6 +184,7 @@ enum {
   K_GEMV_Q4K_X1,
   K_GEMV_Q4_P2,
   K_GEMV_Q4K_P2,
+  K_CHAIN,
   K_N
 };
 static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1",  "amdc_gemv_q4_k_t1",  "amdc_gemv_q4_0_t1u1",
@@ -191,7 +193,8 @@ static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1
                                        "amdc_gemm_q4_k_n64",  "amdc_gemv_q4_0_p1",  "amdc_gemv_q4_k_p1",  "amdc_probe_read",
                                        "amdc_probe_copy",     "amdc_q8_prep",       "amdc_gemmh_m64_n128", "amdc_gemmh_m64_n64",
                                        "amdc_gemm_reduce",    "amdc_gemv_q4_0_v8",  "amdc_gemv_q4_k_v8",
-                                       "amdc_gemv_q4_0_x1",   "amdc_gemv_q4_k_x1",  "amdc_gemv_q4_0_p2",  "amdc_gemv_q4_k_p2"};
+                                       "amdc_gemv_q4_0_x1",   "amdc_gemv_q4_k_x1",  "amdc_gemv_q4_0_p2",  "amdc_gemv_q4_k_p2",
+                                       "amdc_chain"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -256,6 +259,7 @@ static int hip_load(void) {
   SYM(GraphDestroy, "hipGraphDestroy");
   SYM(GraphLaunch, "hipGraphLaunch");
   SYM(GraphExecDestroy, "hipGraphExecDestroy");
+  SYM(OccupancyMaxActiveBlocks, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
 #undef SYM
   return AMDC_OK;
 }
@@ -712,4 +716,126 @@ int amdc_probe_copy(void *dst, const void *src, size_t nbytes, uint32_t grid, vo
   u64 n = nbytes / 16u;
   void *args[] = {&src, &dst, &n};
   return launch(K_PROBE_COPY, grid, 1, 0, stream, args);
+}
+
+/* ------------------------------------------------------------------ GEMV chain */
+
+/* The kernel's ChainOp (amdc_kernels.hip): 64 bytes. */
+typedef struct {
+  uint32_t type, sync, rows, nb, L, pad;
+  const void *a;
+  void *b;
+  float *y;
+  const float *bias, *res;
+} chain_dev_op;
+typedef char chain_dev_op_is_64_bytes[sizeof(chain_dev_op) == 64 ? 1 : -1];
+
+typedef struct {
+  chain_dev_op *ops; /* device: the list, then the barrier state (CHAIN_SYNC_BYTES) */
+  uint32_t *sync;
+  uint32_t n, grid, lds;
+} chain_t;
+
+#define CHAIN_SPIN_NS 200000000u
+#define CHAIN_SYNC_BYTES (35u * 128u) /* the kernel's NGRP + 3 lines */
+
+int amdc_chain_create(const amdc_chain_op *ops, uint32_t n, void **chain) {
+  NEED_OPEN();
+  if (!ops || !n || !chain) return fail(AMDC_EINVAL, "chain_create: null pointer or empty list");
+  chain_dev_op *d = (chain_dev_op *)calloc(n, sizeof(chain_dev_op));
+  if (!d) return fail(AMDC_EINVAL, "chain_create: out of host memory");
+  u32 lds = 0, seg0 = 0;
+  int rc = AMDC_OK;
+  for (u32 k = 0; k < n && !rc; k++) {
+    const amdc_chain_op *o = &ops[k];
+    chain_dev_op *e = &d[k];
+    e->sync = o->sync ? 1u : 0u, e->nb = o->nb;
+    if (o->type == AMDC_CHAIN_QUANT) {
+      if (!o->x || !o->q || !o->nb) rc = fail(AMDC_EINVAL, "chain op %u: quantize needs x, q and nb", k);
+      else if (!aligned16(o->x)) rc = fail(AMDC_EINVAL, "chain op %u: x must be 16-byte aligned", k);
+      e->type = 0, e->a = o->x, e->b = o->q;
+    } else if (o->type == AMDC_CHAIN_GEMV) {
+      rc = check_mat("chain gemv", o->kind, o->w, o->xq, o->y, o->rows, o->nb);
+      if (!rc && 320u * amdc_ngroups(o->nb) > GEMV_LDS_T1) rc = fail(AMDC_EINVAL, "chain op %u: nb %u too large", k, o->nb);
+      e->type = o->kind == AMDC_KIND_Q4_K ? 2u : 1u, e->rows = o->rows, e->L = gemv_lanes(amdc_ngroups(o->nb));
+      e->a = o->w, e->b = (void *)o->xq, e->y = o->y, e->bias = o->bias, e->res = o->res;
+      if (!rc && 320u * amdc_ngroups(o->nb) > lds) lds = 320u * amdc_ngroups(o->nb);
+    } else {
+      rc = fail(AMDC_EINVAL, "chain op %u: type %d", k, o->type);
+    }
+    /* a read of a buffer written earlier in the same segment (no sync between) */
+    for (u32 j = seg0; j < k && !rc; j++) {
+      const void *wj = d[j].type == 0u ? d[j].b : (const void *)d[j].y;
+      const void *r1 = e->type == 0u ? e->a : e->b;
+      if (wj == r1 || (e->type && (wj == (const void *)e->bias || wj == (const void *)e->res)))
+        rc = fail(AMDC_EINVAL, "chain op %u reads what op %u writes without a sync between them", k, j);
+    }
+    if (o->sync) seg0 = k + 1u;
+  }
+  if (rc) {
+    free(d);
+    return rc;
+  }
+  int occ = 0;
+  if (H.OccupancyMaxActiveBlocks(&occ, g_k[K_CHAIN], 256, lds) != 0 || occ < 1) {
+    free(d);
+    return fail(AMDC_EHIP, "chain_create: the chain kernel does not fit on a CU (LDS %u)", lds);
+  }
+  chain_t *c = (chain_t *)calloc(1, sizeof(chain_t));
+  if (!c) {
+    free(d);
+    return fail(AMDC_EINVAL, "chain_create: out of host memory");
+  }
+  c->n = n, c->lds = lds, c->grid = (u32)(g_cus > 0 ? g_cus : 256) * (u32)(occ < 2 ? occ : 2);
+  const size_t bytes = (size_t)n * sizeof(chain_dev_op) + CHAIN_SYNC_BYTES;
+  if (H.Malloc((void **)&c->ops, bytes) != 0) rc = fail(AMDC_EHIP, "chain_create: device allocation of %zu bytes", bytes);
+  if (!rc) {
+    c->sync = (uint32_t *)(c->ops + n);
+    if (H.Memcpy(c->ops, d, (size_t)n * sizeof(chain_dev_op), hipMemcpyHostToDevice) != 0 ||
+        H.Memset(c->sync, 0, CHAIN_SYNC_BYTES) != 0)
+      rc = fail(AMDC_EHIP, "chain_create: upload");
+  }
+  free(d);
+  if (rc) {
+    if (c->ops) H.Free(c->ops);
+    free(c);
+    return rc;
+  }
+  *chain = c;
+  return AMDC_OK;
+}
+
+int amdc_chain_launch(void *chain, void *stream) {
+  NEED_OPEN();
+  chain_t *c = (chain_t *)chain;
+  if (!c) return fail(AMDC_EINVAL, "chain_launch: null chain");
+  u32 spin = CHAIN_SPIN_NS;
+  void *args[] = {&c->ops, &c->n, &c->sync, &spin};
+  return launch(K_CHAIN, c->grid, 1, c->lds, stream, args);
+}
+
+int amdc_chain_check(void *chain) {
+  NEED_OPEN();
+  chain_t *c = (chain_t *)chain;
+  if (!c) return fail(AMDC_EINVAL, "chain_check: null chain");
+  HIPCALL(H.DeviceSynchronize());
+  uint32_t st[CHAIN_SYNC_BYTES / 4u];
+  HIPCALL(H.Memcpy(st, c->sync, CHAIN_SYNC_BYTES, hipMemcpyDeviceToHost));
+  int dirty = 0;
+  for (u32 i = 0; i < CHAIN_SYNC_BYTES / 4u; i++) dirty |= st[i] != 0u;
+  if (dirty) {
+    HIPCALL(H.Memset(c->sync, 0, CHAIN_SYNC_BYTES));
+    return fail(AMDC_EHIP, "chain: a launch aborted at a grid barrier (abort flag %u, released barrier %u): not all %u workgroups were resident",
+                st[34u * 32u], st[33u * 32u], c->grid);
+  }
+  return AMDC_OK;
+}
+
+int amdc_chain_destroy(void *chain) {
+  NEED_OPEN();
+  chain_t *c = (chain_t *)chain;
+  if (!c) return AMDC_OK;
+  HIPCALL(H.Free(c->ops));
+  free(c);
+  return AMDC_OK;
 }

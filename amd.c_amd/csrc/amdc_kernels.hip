@@ -569,6 +569,226 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_p2(const uint8_
   gemv2_body<AMDC_Q4_K>(W, xq, y, rows, nb, bias, res, L);
 }
 
+// ------------------------------------------------------------------ GEMV chain (one launch)
+
+// A list of quantize and decode-GEMV operations run by one persistent launch
+// (the reference's megakernel command list, kernels/ie_mk.c, and its GEMV
+// chain probe ie_mk_gemv_chain, kernels/ie_kernels.c:464-478): every
+// workgroup walks the list; an operation's work is split over the grid
+// (row groups blockIdx.x, + gridDim.x, ... of a GEMV; blocks of a
+// quantization), and a grid barrier follows an operation marked `sync`.
+// While a workgroup waits at a barrier, the weight loads of its first item of
+// the next GEMV are already in flight (weights do not depend on earlier
+// operations), so the HBM stream does not stop at operation boundaries.
+//
+// Data passed between workgroups (the Q8 vectors, the GEMV outputs) is
+// written and read with agent-scope coherent accesses (sc1: the L2 of each
+// XCD is not coherent with the others'), so no L2 flush is needed; a barrier
+// first waits for the wave's own stores (vmcnt 0), then counts the
+// workgroup's arrival with an agent-scope atomic add. The wait is bounded
+// (spin_ns of the 100 MHz real-time counter): past it, the workgroup raises
+// the abort flag, every workgroup leaves, and the host reports the error.
+// The last workgroup to finish sets the counters back to zero.
+struct ChainOp { // the host's amdc_chain_op, resolved (amdc_host.c): 64 bytes
+  u32 type;      // 0: quantize a -> b (nb blocks); 1, 2: GEMV Q4_0 / Q4_K, W a, Q8 vector b -> y
+  u32 sync;      // grid barrier after this operation
+  u32 rows, nb, L, pad;
+  const void *a;
+  void *b;
+  float *y;
+  const float *bias, *res;
+};
+#define CPOL_SC1 16 // cache policy of agent-coherent buffer accesses (gfx94x / gfx950 SC1)
+
+// The grid barrier. Arrivals are counted per group of workgroups
+// (blockIdx.x mod NGRP, one counter per 128-byte line: few atomics on any one
+// address); the last arrival of a group counts the group, the last group
+// publishes the barrier's number on a line of its own, which the waiting
+// workgroups poll (with a short sleep). The end of the launch is one more
+// arrival, without the wait: the last one sets the counters back to zero.
+// Layout of sync (u32, 128-byte lines): line g < NGRP: group g's arrivals;
+// line NGRP: groups arrived; NGRP + 1: released barrier number; NGRP + 2:
+// abort flag.
+#define SYNC_LINE 32u
+#define NGRP 32u
+__device__ __forceinline__ bool chain_arrive(u32 *sync, u32 nbar) {
+  const u32 grp = blockIdx.x % NGRP, gs = (gridDim.x - grp + NGRP - 1u) / NGRP, ngrp = gridDim.x < NGRP ? gridDim.x : NGRP;
+  return __hip_atomic_fetch_add(sync + SYNC_LINE * grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nbar * gs - 1u &&
+         __hip_atomic_fetch_add(sync + SYNC_LINE * NGRP, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nbar * ngrp - 1u;
+}
+
+__device__ __forceinline__ bool chain_barrier(u32 *sync, u32 nbar, u32 spin_ns) {
+  __shared__ u32 s_ok;
+  __builtin_amdgcn_s_waitcnt(0); // this wave's coherent stores are complete
+  __syncthreads();
+  if (threadIdx.x == 0u) {
+    if (chain_arrive(sync, nbar)) __hip_atomic_store(sync + SYNC_LINE * (NGRP + 1u), nbar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const u64 t0 = __builtin_amdgcn_s_memrealtime(), lim = spin_ns / 10u;
+    u32 ok = 0;
+    for (u32 it = 0;; it++) {
+      if ((int)(__hip_atomic_load(sync + SYNC_LINE * (NGRP + 1u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - nbar) >= 0) {
+        ok = 1;
+        break;
+      }
+      if ((it & 15u) == 15u) {
+        if (__hip_atomic_load(sync + SYNC_LINE * (NGRP + 2u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+        if (__builtin_amdgcn_s_memrealtime() - t0 > lim) {
+          __hip_atomic_store(sync + SYNC_LINE * (NGRP + 2u), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    s_ok = ok;
+  }
+  __syncthreads();
+  return s_ok != 0u;
+}
+
+// One decode GEMV of the chain: the same lane split, LDS layout and block
+// arithmetic as amdc_gemv_*_p1 (bit-equal results). A workgroup's items
+// (row groups blockIdx.x, + gridDim.x, ..., ceil(ng / L) super-groups per
+// lane each) go in batches of CHI: all loads of a batch first (a slot past
+// the last item reads row 0's first super-group again and is not used), then
+// the arithmetic; it[0] of the first batch may already be loaded (pre).
+#define CHI 2u
+template <int KIND>
+__device__ __forceinline__ void chain_gemv(const ChainOp &op, Item (&it)[CHI], bool pre, uint8_t *smem) {
+  const uint8_t *W = (const uint8_t *)op.a, *xq = (const uint8_t *)op.b;
+  const u32 rows = op.rows, nb = op.nb, L = op.L, ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw;
+  const u32 nrg = (rows + rpg - 1u) / rpg, ni = (ng + L - 1u) / L, nblk = 8u * ng;
+  const u32 mine = blockIdx.x < nrg ? (nrg - blockIdx.x + gridDim.x - 1u) / gridDim.x : 0u, nit = mine * ni;
+  const u64 RB = amdc_row_bytes(nb);
+  u32x4 *s_lo = (u32x4 *)smem;
+  u32x4 *s_hi = s_lo + nblk;
+  float *s_d = (float *)(s_hi + nblk);
+  u32 *s_as = (u32 *)(s_d + nblk);
+  auto rowp = [&](u32 g_) {
+    const u32 r_ = g_ * rpg + wv * rpw + q;
+    return W + (u64)(r_ < rows ? r_ : rows - 1u) * RB;
+  };
+  auto load_batch = [&](u32 f0, u32 u0) {
+#pragma unroll
+    for (u32 u = 0; u < CHI; u++) {
+      if (u < u0) continue;
+      const u32 f = f0 + u, j = f / ni, i = f - j * ni;
+      const bool ok = f < nit;
+      load_item<KIND>(it[u], ok ? rowp(blockIdx.x + j * gridDim.x) : W, ng, l + L * i, ok && l + L * i < ng);
+    }
+  };
+  if (nit) load_batch(0u, pre ? 1u : 0u);
+  __asm__ volatile("" ::: "memory"); // the weight loads ahead of the activation loads
+  const __amdgpu_buffer_rsrc_t rq = rsrc(xq, 40u * nb);
+  for (u32 j = tid; j < nblk; j += NT) { // the Q8 vector, written by other workgroups: coherent loads
+    const u32 p = (j & 7u) * ng + (j >> 3);
+    u32x4 lo = (u32x4)(0u), hi = (u32x4)(0u);
+    float d = 0.0f;
+    u32 as = 0;
+    if (j < nb) {
+      lo = __builtin_amdgcn_raw_buffer_load_b128(rq, 32u * j, 0, CPOL_SC1);
+      hi = __builtin_amdgcn_raw_buffer_load_b128(rq, 32u * j + 16u, 0, CPOL_SC1);
+      d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, 32u * nb + 4u * j, 0, CPOL_SC1));
+      as = __builtin_amdgcn_raw_buffer_load_b32(rq, 36u * nb + 4u * j, 0, CPOL_SC1);
+    }
+    s_lo[p] = lo, s_hi[p] = hi, s_d[p] = d, s_as[p] = as;
+  }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t ry = rsrc(op.y, 4u * rows), rb = rsrc(op.bias, 4u * rows), rr = rsrc(op.res, 4u * rows);
+  float acc = 0.0f;
+  for (u32 f0 = 0; f0 < nit; f0 += CHI) {
+    if (f0) load_batch(f0, 0u);
+#pragma unroll
+    for (u32 u = 0; u < CHI; u++) {
+      const u32 f = f0 + u, j = f / ni, i = f - j * ni, g = l + L * i;
+      if (f >= nit) break;
+      if (g < ng) acc = item_dot<KIND>(it[u], g, ng, s_lo, s_hi, s_d, s_as, acc);
+      if (i == ni - 1u) {
+        const float v = seg_sum(acc, L);
+        const u32 r = (blockIdx.x + j * gridDim.x) * rpg + wv * rpw + q;
+        if (l == 0u && r < rows) {
+          float o = v;
+          if (op.bias) o = o + __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, 4u * r, 0, CPOL_SC1));
+          if (op.res) o = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, 4u * r, 0, CPOL_SC1)) + o;
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(u32, o), ry, 4u * r, 0, CPOL_SC1);
+        }
+        acc = 0.0f;
+      }
+    }
+  }
+  __syncthreads(); // the LDS vector is free for the next operation
+}
+
+// the quantization of op.a (nb blocks of 32 floats) into the Q8 buffer op.b,
+// blocks 32 p .. 32 p + 31 by workgroup p, + 32 gridDim.x, ... (8 lanes per
+// block, 4 values per lane; the arithmetic of amdc_quant_q8)
+__device__ __forceinline__ void chain_quant(const ChainOp &op) {
+  const u32 nb = op.nb, tid = threadIdx.x, e = tid & 7u;
+  const __amdgpu_buffer_rsrc_t rx = rsrc(op.a, 128u * nb), rq = rsrc(op.b, 40u * nb);
+  for (u32 b0 = 32u * blockIdx.x; b0 < nb; b0 += 32u * gridDim.x) {
+    const u32 b = b0 + (tid >> 3);
+    const v4f v = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rx, b < nb ? 128u * b + 16u * e : 0xFFFFFFF0u, 0, CPOL_SC1));
+    float a = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)), __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
+    a = __builtin_fmaxf(a, dpp<0xB1>(a));
+    a = __builtin_fmaxf(a, dpp<0x4E>(a));
+    a = __builtin_fmaxf(a, dpp<0x141>(a));
+    const float d = a / 127.0f;
+    int qi[4];
+#pragma unroll
+    for (int m = 0; m < 4; m++) qi[m] = d != 0.0f ? (int)__builtin_roundf(v[m] / d) : 0;
+    const u32 word = (u32)(qi[0] & 255) | (u32)(qi[1] & 255) << 8 | (u32)(qi[2] & 255) << 16 | (u32)qi[3] << 24;
+    u32 sum = (u32)qi[0] + (u32)qi[1] + (u32)qi[2] + (u32)qi[3];
+    sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0xB1, 0xF, 0xF, false);
+    sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0x4E, 0xF, 0xF, false);
+    sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0x141, 0xF, 0xF, false);
+    if (b < nb) {
+      __builtin_amdgcn_raw_buffer_store_b32(word, rq, 32u * b + 4u * e, 0, CPOL_SC1);
+      if (e == 0u) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(u32, d), rq, 32u * nb + 4u * b, 0, CPOL_SC1);
+        __builtin_amdgcn_raw_buffer_store_b32(sum, rq, 36u * nb + 4u * b, 0, CPOL_SC1);
+      }
+    }
+  }
+}
+
+// the first item of op (a GEMV) for this workgroup, loaded ahead (false if it has none)
+__device__ __forceinline__ bool chain_preload(const ChainOp &op, Item &cur) {
+  const u32 L = op.L, ng = amdc_ngroups(op.nb), lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
+  const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw, nrg = (op.rows + rpg - 1u) / rpg;
+  if (blockIdx.x >= nrg) return false;
+  const u32 r = blockIdx.x * rpg + wv * rpw + q;
+  const uint8_t *wr = (const uint8_t *)op.a + (u64)(r < op.rows ? r : op.rows - 1u) * amdc_row_bytes(op.nb);
+  if (op.type == 1u) load_item<AMDC_Q4_0>(cur, wr, ng, l, l < ng);
+  else load_item<AMDC_Q4_K>(cur, wr, ng, l, l < ng);
+  return true;
+}
+
+extern "C" __global__ __launch_bounds__(256) void amdc_chain(const ChainOp *__restrict__ ops, u32 n, u32 *sync, u32 spin_ns) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  u32 nbar = 0, pre = 0xFFFFFFFFu; // pre: the operation whose first item it[0] holds
+  Item it[CHI];
+  for (u32 k = 0; k < n; k++) {
+    const ChainOp op = ops[k];
+    if (op.type == 0u) chain_quant(op);
+    else if (op.type == 1u) chain_gemv<AMDC_Q4_0>(op, it, pre == k, smem);
+    else chain_gemv<AMDC_Q4_K>(op, it, pre == k, smem);
+    if (op.sync && k + 1u < n) {
+      // the next GEMV's first weights go out before the wait (quantizations between do not touch it[])
+      u32 j = k + 1u;
+      while (j < n && ops[j].type == 0u) j++;
+      if (j < n && pre != j && chain_preload(ops[j], it[0])) pre = j;
+      nbar++;
+      if (!chain_barrier(sync, nbar, spin_ns)) break;
+    }
+  }
+  // the end: one more arrival; the last one sets the counters back to zero
+  // (not the abort flag: the host reads it)
+  __syncthreads();
+  if (threadIdx.x == 0u && chain_arrive(sync, nbar + 1u)) {
+    for (u32 g = 0; g < NGRP + 2u; g++) __hip_atomic_store(sync + SYNC_LINE * g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // ------------------------------------------------------------------ bandwidth probes
 
 // Plain streaming kernels of known traffic, the yardsticks of the GEMV: read

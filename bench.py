@@ -174,8 +174,24 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
             amdc.gemv_x(kind, G.dev[ci][gi], X, Y, r, c // 32, stream=s)
 
     graphs = [timer.graph(lambda s, ci=ci: step(ci, s)) for ci in range(G.copies)]
-    ms = timer.replay_ms(graphs, steps, warmup)
+    ms_launches = timer.replay_ms(graphs, steps, warmup)
     del graphs
+    # the same step as one GEMV chain launch per weight copy (quantize, barrier, GEMV, barrier, ...)
+    Qc = amdc.DevBuf(q8_stride(cols_max // 32))
+    chains = []
+    for ci in range(G.copies):
+        ops = []
+        for gi, (name, r, c, _) in enumerate(groups):
+            ops += [amdc.chain_quant(X, Qc, c // 32), amdc.chain_gemv(kind, G.dev[ci][gi], Qc, Y, r, c // 32)]
+        chains.append(amdc.Chain(ops))
+    chains[0].launch()
+    chains[0].check()
+    graphs = [timer.graph(lambda s, ch=ch: ch.launch(s)) for ch in chains]
+    ms_chain = timer.replay_ms(graphs, steps, warmup)
+    del graphs
+    chains[0].check()
+    del chains
+    ms = min(ms_launches, ms_chain)
     per_m, tot_m = {}, 0.0
     for gi, (name, r, c, _) in enumerate(groups):
         amdc.quant_q8(X, Q, c // 32)
@@ -188,6 +204,8 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
     set_bytes = G.set_bytes
     del G
     return {"set_bytes": set_bytes, "ms_per_step": ms, "ms_per_step_unmerged": ms_unmerged,
+            "ms_per_step_launches": ms_launches, "ms_per_step_chain": ms_chain,
+            "step_form": "chain" if ms_chain <= ms_launches else "launches",
             "launches_per_step": sum(1 if (c // 32) <= 128 else 2 for _, _, c, _ in groups),
             "per_shape": per, "per_merged_shape": per_m,
             "kernel_GBps": set_bytes / tot_m / 1e6, "kernel_us_total": tot_m * 1e3,

@@ -175,6 +175,43 @@ int amdc_block_dots(int kind, const void *w, const uint8_t *xq, int32_t *out, ui
  * AMDC_GEMV_FORM. */
 int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kernel, int gemm_ksplit, int gemv_form);
 
+/* A GEMV chain: a list of quantize and decode-GEMV operations run by ONE
+ * persistent launch, a grid barrier after every operation marked sync (the
+ * reference's megakernel command list, kernels/ie_mk.c with mk_put in
+ * src/hip.c:530, and its GEMV chain probe ie_mk_gemv_chain,
+ * kernels/ie_kernels.c:464-478). While a workgroup waits at a barrier the
+ * weight loads of the next GEMV are already in flight. Results equal the
+ * separate launches bit for bit (amdc_quant_q8; amdc_gemv_q4 / _q4k with
+ * the same lane split).
+ *   AMDC_CHAIN_QUANT: x (32 nb floats) -> q (Q8 buffer, 40 nb bytes)
+ *   AMDC_CHAIN_GEMV:  kind, w (rows x nb), xq (Q8) -> y (rows floats),
+ *                     optional bias / res (rows floats) as amdc_gemv_q4
+ * An operation that reads what an earlier one writes must come after a sync
+ * (the check compares buffer pointers). All workgroups must be resident at
+ * once: the grid is what the device holds (at most 2 per CU); nothing else
+ * should run on the device meanwhile. A barrier that waits longer than 200 ms
+ * aborts the launch (every workgroup leaves); amdc_chain_check reports it. */
+enum { AMDC_CHAIN_QUANT = 0, AMDC_CHAIN_GEMV = 1 };
+typedef struct {
+  int type, kind, sync;
+  uint32_t rows, nb;
+  const void *w;
+  const float *x;
+  uint8_t *q;
+  const uint8_t *xq;
+  float *y;
+  const float *bias, *res;
+} amdc_chain_op;
+/* Validate the list, upload it and the barrier counters (allocates: call
+ * before any graph capture); *chain receives the handle. */
+int amdc_chain_create(const amdc_chain_op *ops, uint32_t n, void **chain);
+/* One launch of the whole list on stream (no allocation: can be captured). */
+int amdc_chain_launch(void *chain, void *stream);
+/* Synchronizes the device; AMDC_EHIP if a launch of this chain aborted at a
+ * barrier (the counters are then reset). */
+int amdc_chain_check(void *chain);
+int amdc_chain_destroy(void *chain);
+
 /* Bandwidth yardsticks (no reference counterpart): stream nbytes (a multiple
  * of 16) through a plain read kernel (one u32 per workgroup may be written to
  * scratch) or a copy kernel, grid workgroups of 256 threads. They give the

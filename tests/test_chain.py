@@ -1,0 +1,98 @@
+"""The GEMV chain (amdc_chain_*): a list of quantize and decode-GEMV operations in one persistent launch
+with grid barriers. Every result equals the separate launches (amdc_quant_q8, then amdc_gemv_q4 / _q4k with
+the same lane split) bit for bit, across repeated launches and graph replays, and the GEMVs match the oracle
+to the GEMV tolerance."""
+import numpy as np
+import pytest
+
+from amdc import synth
+from test_gpu_parity import Case, rel_err, TOL, q8_stride
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _form1(dev):
+    dev.set_tuning(form=1)  # the separate launches with the chain's lane split (bitwise comparison)
+    yield
+    dev.set_tuning()
+
+
+def test_chain_equals_separate_launches(dev, orc):
+    """x0 -> Q8 -> GEMV A (Q4_0, nb 13: a partial super-group) -> y1 -> Q8 -> GEMV B (Q4_K, with bias and
+    residual) -> y2 -> Q8 -> GEMV C and D (Q4_0, one input, no barrier between them)."""
+    g = np.random.default_rng(0)
+    A = Case(dev, orc, 0, 256, 13, seed=1)  # 416 -> 256 (each output feeds the next stage's input)
+    B = Case(dev, orc, 3, 1024, 8, seed=2)  # 256 -> 1024
+    C_ = Case(dev, orc, 0, 77, 32, seed=3)  # 1024 -> 77
+    D = Case(dev, orc, 0, 300, 32, seed=4)  # 1024 -> 300
+    x0 = dev.DevBuf.of(A.x[0])
+    q0, q1, q2 = dev.DevBuf(q8_stride(13)), dev.DevBuf(q8_stride(8)), dev.DevBuf(q8_stride(32))
+    y1, y2, y3, y4 = (dev.DevBuf(4 * r) for r in (256, 1024, 77, 300))
+    bias = dev.DevBuf.of(g.standard_normal(1024).astype(np.float32))
+    res = dev.DevBuf.of(g.standard_normal(1024).astype(np.float32))
+    ops = [dev.chain_quant(x0, q0, 13),
+           dev.chain_gemv(0, A.W, q0, y1, 256, 13),
+           dev.chain_quant(y1, q1, 8),
+           dev.chain_gemv(3, B.W, q1, y2, 1024, 8, bias=bias, res=res),
+           dev.chain_quant(y2, q2, 32),
+           dev.chain_gemv(0, C_.W, q2, y3, 77, 32, sync=False),
+           dev.chain_gemv(0, D.W, q2, y4, 300, 32)]
+    ch = dev.Chain(ops)
+    # the separate launches
+    r0, r1, r2 = dev.DevBuf(q8_stride(13)), dev.DevBuf(q8_stride(8)), dev.DevBuf(q8_stride(32))
+    z1, z2, z3, z4 = (dev.DevBuf(4 * r) for r in (256, 1024, 77, 300))
+    dev.quant_q8(x0, r0, 13)
+    dev.gemv(0, A.W, r0, z1, 256, 13)
+    dev.quant_q8(z1, r1, 8)
+    dev.gemv(3, B.W, r1, z2, 1024, 8, bias=bias, res=res)
+    dev.quant_q8(z2, r2, 32)
+    dev.gemv(0, C_.W, r2, z3, 77, 32)
+    dev.gemv(0, D.W, r2, z4, 300, 32)
+    want = [b.download(np.uint32) for b in (r0, z1, r1, z2, r2, z3, z4)]
+    for rep in range(3):
+        for b in (q0, q1, q2, y1, y2, y3, y4):
+            b.fill(0)
+        ch.launch()
+        ch.check()
+        got = [b.download(np.uint32) for b in (q0, y1, q1, y2, q2, y3, y4)]
+        for i, (gt, wt) in enumerate(zip(got, want)):
+            n = 10 * (13, 8, 32)[i // 2] if i in (0, 2, 4) else gt.size  # Q8 buffers: their 40 nb bytes
+            assert np.array_equal(gt[:n], wt[:n]), (rep, i)
+    # the first GEMV against the oracle
+    yA = y1.download(np.float32)
+    assert rel_err(yA, A.y_oracle(0), A.mag(0)) < TOL
+
+
+def test_chain_graph_replay(dev, orc):
+    """A chain captured in a HIP graph and replayed, with eager work between replays, equals the eager chain."""
+    A = Case(dev, orc, 3, 3000, 160, seed=5)
+    x0 = dev.DevBuf.of(A.x[0])
+    q0, y = dev.DevBuf(q8_stride(160)), dev.DevBuf(4 * 3000)
+    ch = dev.Chain([dev.chain_quant(x0, q0, 160), dev.chain_gemv(3, A.W, q0, y, 3000, 160)])
+    ch.launch()
+    ch.check()
+    want = y.download(np.uint32)
+    assert rel_err(y.download(np.float32), A.y_oracle(0), A.mag(0)) < TOL
+    S = dev.Stream()
+    gph = dev.Graph(S, lambda s: ch.launch(s))
+    other = Case(dev, orc, 0, 64, 128, seed=9)
+    for rep in range(3):
+        y.fill(0)
+        other.quant()
+        dev.sync()
+        gph.launch()
+        S.sync()
+        assert np.array_equal(y.download(np.uint32), want), rep
+    ch.check()
+
+
+def test_chain_rejects_read_before_sync(dev, orc):
+    A = Case(dev, orc, 0, 64, 8, seed=6)
+    x0, q0, y = dev.DevBuf.of(A.x[0]), dev.DevBuf(q8_stride(8)), dev.DevBuf(4 * 64)
+    with pytest.raises(dev.AmdcError, match="without a sync"):
+        dev.Chain([dev.chain_quant(x0, q0, 8, sync=False), dev.chain_gemv(0, A.W, q0, y, 64, 8)])
+    with pytest.raises(dev.AmdcError, match="type"):
+        op = dev.chain_quant(x0, q0, 8)
+        op.type = 7
+        dev.Chain([op])
