@@ -371,7 +371,7 @@ def main():
                    "weight_bytes_per_step": c1["set_bytes"], "rotation_copies_bytes": ROTATE_BYTES, "batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-                     "kernel": "amdc_gemv_q4_0_p1", "bytes_per_launch_avg": c1["set_bytes"] / len(c1["per_merged_shape"])},
+                     "kernel": "amdc_gemv_q4_0_p1 (down: amdc_gemv_q4_0_p2)", "bytes_per_launch_avg": c1["set_bytes"] / len(c1["per_merged_shape"])},
         "cpu_baseline": cpu,
         "detail": detail,
     }
