@@ -64,6 +64,8 @@ ABI = {
     "amdc_set_tuning": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "amdc_probe_read": (C.c_int, [_P, C.c_size_t, _P, _U32, _P]),
     "amdc_probe_copy": (C.c_int, [_P, _P, C.c_size_t, _U32, _P]),
+    "amdc_rmsnorm_q8": (C.c_int, [_P, _P, _P, _U32, C.c_float, _P, _U32, _U32, _U32, _U32, _P]),
+    "amdc_swiglu_q8": (C.c_int, [_P, _P, _U32, _P, _U32, _U32, _U32, _P]),
     "amdc_chain_create": (C.c_int, [_P, _U32, C.POINTER(_P)]),
     "amdc_chain_launch": (C.c_int, [_P, _P]),
     "amdc_chain_check": (C.c_int, [_P]),
@@ -331,6 +333,16 @@ def probe_read(src, nbytes, scratch, grid, stream=None):
 
 def probe_copy(dst, src, nbytes, grid, stream=None):
     _check(lib().amdc_probe_copy(_p(dst), _p(src), nbytes, grid, stream))
+
+
+def rmsnorm_q8(x, w, y, n, eps, q=None, T=1, xs=0, ys=0, qs=0, stream=None):
+    """amdc_rmsnorm_q8: y = rmsnorm(x) w and, when q is given, its Q8 copy."""
+    _check(lib().amdc_rmsnorm_q8(_p(x), _p(w), _p(y), n, eps, _p(q), T, xs, ys, qs, stream))
+
+
+def swiglu_q8(a, b, n, q=None, T=1, as_=0, qs=0, stream=None):
+    """amdc_swiglu_q8: a = silu(a) b in place and, when q is given, its Q8 copy."""
+    _check(lib().amdc_swiglu_q8(_p(a), _p(b), n, _p(q), T, as_, qs, stream))
 
 
 def chain_quant(x, q, nb, sync=True):

@@ -185,6 +185,8 @@ enum {
   K_GEMV_Q4_P2,
   K_GEMV_Q4K_P2,
   K_CHAIN,
+  K_RMSNORM_Q8,
+  K_SWIGLU_Q8,
   K_N
 };
 static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1",  "amdc_gemv_q4_k_t1",  "amdc_gemv_q4_0_t1u1",
@@ -194,7 +196,7 @@ static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1
                                        "amdc_probe_copy",     "amdc_q8_prep",       "amdc_gemmh_m64_n128", "amdc_gemmh_m64_n64",
                                        "amdc_gemm_reduce",    "amdc_gemv_q4_0_v8",  "amdc_gemv_q4_k_v8",
                                        "amdc_gemv_q4_0_x1",   "amdc_gemv_q4_k_x1",  "amdc_gemv_q4_0_p2",  "amdc_gemv_q4_k_p2",
-                                       "amdc_chain"};
+                                       "amdc_chain",          "amdc_rmsnorm_q8",    "amdc_swiglu_q8"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -442,6 +444,29 @@ int amdc_quant_q8(const float *x, uint8_t *q, uint32_t nb, uint32_t T, uint32_t 
   if (T > 65535u) return fail(AMDC_EINVAL, "quant_q8: T %u > 65535", T);
   void *args[] = {&x, &q, &nb, &xs, &qs};
   return launch(K_QUANT, (nb + 7u) / 8u, T, 0, stream, args);
+}
+
+int amdc_rmsnorm_q8(const float *x, const float *w, float *y, uint32_t n, float eps, uint8_t *q, uint32_t T, uint32_t xs, uint32_t ys,
+                    uint32_t qs, void *stream) {
+  NEED_OPEN();
+  if (!x || !w || !y || !n || !T) return fail(AMDC_EINVAL, "rmsnorm_q8: null pointer or empty (n %u, T %u)", n, T);
+  if (n % 32u) return fail(AMDC_EINVAL, "rmsnorm_q8: n %u not a multiple of 32", n);
+  if (T > 1u && (xs % 4u || ys % 4u || xs < 4u * n || ys < 4u * n || (q && qs < 40u * (n / 32u))))
+    return fail(AMDC_EINVAL, "rmsnorm_q8: strides xs %u, ys %u, qs %u too small or unaligned for n %u", xs, ys, qs, n);
+  if (T > 65535u) return fail(AMDC_EINVAL, "rmsnorm_q8: T %u > 65535", T);
+  void *args[] = {&x, &w, &y, &n, &eps, &q, &xs, &ys, &qs};
+  return launch(K_RMSNORM_Q8, (n / 32u + 7u) / 8u, T, 0, stream, args);
+}
+
+int amdc_swiglu_q8(float *a, const float *b, uint32_t n, uint8_t *q, uint32_t T, uint32_t as, uint32_t qs, void *stream) {
+  NEED_OPEN();
+  if (!a || !b || !n || !T) return fail(AMDC_EINVAL, "swiglu_q8: null pointer or empty (n %u, T %u)", n, T);
+  if (n % 32u) return fail(AMDC_EINVAL, "swiglu_q8: n %u not a multiple of 32", n);
+  if (T > 1u && (as % 4u || as < 4u * n || (q && qs < 40u * (n / 32u))))
+    return fail(AMDC_EINVAL, "swiglu_q8: strides as %u, qs %u too small or unaligned for n %u", as, qs, n);
+  if (T > 65535u) return fail(AMDC_EINVAL, "swiglu_q8: T %u > 65535", T);
+  void *args[] = {&a, &b, &n, &q, &as, &qs};
+  return launch(K_SWIGLU_Q8, (n + 255u) / 256u, T, 0, stream, args);
 }
 
 static int check_mat(const char *op, int kind, const void *w, const uint8_t *xq, const float *y, uint32_t rows, uint32_t nb) {

@@ -113,6 +113,83 @@ extern "C" __global__ __launch_bounds__(256) void amdc_quant_q8(const float *__r
   }
 }
 
+// The Q8 producers of a decode step, fused as the reference fuses them
+// (kernels/ie_kernels.c:240-265 ie_rmsnorm, :2458 ie_swiglu): the float result
+// and its Q8 copy (the arithmetic of amdc_quant_q8 on that result) in one
+// launch. Grid (ceil(n / 256), T); token t at byte offsets t xs, t ys, t qs.
+
+// half a wave quantizes the block of 32 values v (one per lane) into q
+__device__ __forceinline__ void quant_half(float v, u32 b, uint8_t *__restrict__ q, u32 nb) {
+  const u32 j = threadIdx.x & 31u;
+  float a = __builtin_fabsf(v);
+#pragma unroll
+  for (u32 o = 1; o < 32u; o <<= 1) a = __builtin_fmaxf(a, __shfl_xor(a, (int)o));
+  const float d = a / 127.0f;
+  const int qi = d != 0.0f ? (int)__builtin_roundf(v / d) : 0;
+  ((int8_t *)q)[32u * b + j] = (int8_t)qi;
+  u32 s = (u32)qi;
+#pragma unroll
+  for (u32 o = 1; o < 32u; o <<= 1) s += (u32)__shfl_xor((int)s, (int)o);
+  if (j == 0u) {
+    ((float *)(q + 32u * nb))[b] = d;
+    ((u32 *)(q + 36u * nb))[b] = s;
+  }
+}
+
+// y = x s w, s = 1 / sqrt(sum x^2 / n + eps) (src/cpu.c:276-281), and its Q8
+// copy when q is not NULL. Every workgroup computes the whole sum of squares
+// with the same code (so the same s), 8 loads in flight per thread, then
+// normalizes its 8 blocks. n is a multiple of 32.
+extern "C" __global__ __launch_bounds__(256) void amdc_rmsnorm_q8(const float *__restrict__ x, const float *__restrict__ w, float *__restrict__ y,
+                                                                 u32 n, float eps, uint8_t *__restrict__ q, u32 xs, u32 ys, u32 qs) {
+  __shared__ float s_ss[4];
+  x = (const float *)((const uint8_t *)x + (u64)blockIdx.y * xs);
+  y = (float *)((uint8_t *)y + (u64)blockIdx.y * ys);
+  if (q) q += (u64)blockIdx.y * qs;
+  const u32 tid = threadIdx.x;
+  float ss = 0.0f;
+  u32 i0 = tid;
+  for (; i0 + 7u * NT < n; i0 += 8u * NT) {
+    float v[8];
+#pragma unroll
+    for (u32 k = 0; k < 8u; k++) v[k] = x[i0 + k * NT];
+#pragma unroll
+    for (u32 k = 0; k < 8u; k++) ss += v[k] * v[k];
+  }
+  for (; i0 < n; i0 += NT) ss += x[i0] * x[i0];
+  ss += dpp<0xB1>(ss);
+  ss += dpp<0x4E>(ss);
+  ss += dpp<0x141>(ss);
+  ss += dpp<0x140>(ss);
+  ss += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, ss), 0x401F));
+  ss += __shfl_xor(ss, 32);
+  if ((tid & 63u) == 0u) s_ss[tid >> 6] = ss;
+  __syncthreads();
+  ss = (s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]);
+  const float s = 1.0f / __builtin_sqrtf(ss / (float)n + eps);
+  const u32 nb = n >> 5, b = blockIdx.x * 8u + (tid >> 5);
+  if (b >= nb) return; // whole 32-lane halves leave together
+  const u32 i = 32u * b + (tid & 31u);
+  const float v = x[i] * s * w[i];
+  y[i] = v;
+  if (q) quant_half(v, b, q, nb);
+}
+
+// a = a / (1 + exp(-a)) b in place (src/cpu.c:580), and its Q8 copy when q
+// is not NULL. n is a multiple of 32.
+extern "C" __global__ __launch_bounds__(256) void amdc_swiglu_q8(float *__restrict__ a, const float *__restrict__ b, u32 n,
+                                                                uint8_t *__restrict__ q, u32 as, u32 qs) {
+  a = (float *)((uint8_t *)a + (u64)blockIdx.y * as);
+  b = (const float *)((const uint8_t *)b + (u64)blockIdx.y * as);
+  if (q) q += (u64)blockIdx.y * qs;
+  const u32 i = blockIdx.x * NT + threadIdx.x;
+  if (i >= n) return; // whole 32-lane halves leave together
+  const float g = a[i];
+  const float v = g / (1.0f + __builtin_expf(-g)) * b[i];
+  a[i] = v;
+  if (q) quant_half(v, i >> 5, q, n >> 5);
+}
+
 // ------------------------------------------------------------------ GEMV
 
 // y[t][r] = sum over blocks of W[r] . x_t for the T (<= TT) Q8 vectors x_t

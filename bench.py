@@ -258,6 +258,23 @@ def prefill_set(steps, seed, timer):
 
 # ---------------------------------------------------------------- CPU baseline
 
+def producers_set(timer):
+    """The fused Q8 producers at the c1/c2 sizes: us per launch (graphs of back-to-back launches)."""
+    out = {}
+    g = np.random.default_rng(7)
+    for name, n in (("rmsnorm_q8", 4096), ("rmsnorm_q8", 5120), ("swiglu_q8", 11008), ("swiglu_q8", 17408)):
+        nb = n // 32
+        X = amdc.DevBuf.of(g.standard_normal(n).astype(np.float32))
+        Wt = amdc.DevBuf.of(np.ones(n, np.float32))
+        Y, Q = amdc.DevBuf(4 * n), amdc.DevBuf(q8_stride(nb))
+        if name == "rmsnorm_q8":
+            t = timer.per_launch_ms(lambda j, s: amdc.rmsnorm_q8(X, Wt, Y, n, 1e-6, Q, stream=s), 64)
+        else:
+            t = timer.per_launch_ms(lambda j, s: amdc.swiglu_q8(X, Wt, n, Q, stream=s), 64)
+        out[f"{name}_{n}"] = {"us": round(t * 1e3, 3)}
+    return out
+
+
 def cpu_baseline(seed, budget_s=12.0):
     """The c1 step on one host core: reference cpu_gemv_q4 (oracle/_ref) or the restatement."""
     from oracle import GGML_Q4_0, Oracle, RefCPU
@@ -346,6 +363,8 @@ def main():
         print(f"bench: c3 {json.dumps(detail['c3'])}", file=sys.stderr, flush=True)
         detail["c4"] = prefill_set(a.steps, a.seed + 3000, timer)
         print(f"bench: c4 {json.dumps(detail['c4'])}", file=sys.stderr, flush=True)
+        detail["producers"] = producers_set(timer)
+        print(f"bench: producers {json.dumps(detail['producers'])}", file=sys.stderr, flush=True)
     cpu = None
     if not a.quick and not a.no_cpu:
         cpu = cpu_baseline(a.seed)

@@ -109,6 +109,19 @@ int amdc_gemv_q4(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint
 int amdc_gemv_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                   void *stream);
 
+/* The fused Q8 producers (the float op and the Q8 copy of its result, bit
+ * for bit amdc_quant_q8 of that result, in one launch), as the reference's
+ * OP_RMSNORM / OP_SWIGLU with a Q8 output (src/hip.c:915-921, 1266-1271;
+ * kernels/ie_kernels.c:240-265 ie_rmsnorm, :2458 ie_swiglu):
+ *   rmsnorm: y = x s w, s = 1 / sqrt(sum x^2 / n + eps) (src/cpu.c:276-281)
+ *   swiglu:  a = a / (1 + exp(-a)) b, in place (src/cpu.c:580)
+ * q may be NULL (no Q8 copy). n is a multiple of 32; T tokens at byte
+ * strides xs / ys / as (floats) and qs (Q8). The float results differ from
+ * the CPU's in summation order (rmsnorm) and exp rounding (swiglu) only. */
+int amdc_rmsnorm_q8(const float *x, const float *w, float *y, uint32_t n, float eps, uint8_t *q, uint32_t T, uint32_t xs, uint32_t ys,
+                    uint32_t qs, void *stream);
+int amdc_swiglu_q8(float *a, const float *b, uint32_t n, uint8_t *q, uint32_t T, uint32_t as, uint32_t qs, void *stream);
+
 /* The decode GEMV of an f32 input x (32 nb floats, 16-byte aligned): the
  * pair OP_QUANT + OP_GEMV_Q4 / OP_GEMV_Q4K (src/hip.c:922-933, 1023-1024).
  * For nb <= 128 (AMDC_GEMVX_FUSE_NB) one launch: every workgroup quantizes x

@@ -80,6 +80,20 @@ void or_quant_q8(const float *x, uint8_t *q, uint32_t nb) {
   }
 }
 
+/* src/cpu.c:276-281: the sum of squares in element order, one division, one
+ * square root, then (x s) w per element. */
+void or_rmsnorm(const float *x, const float *w, float *y, uint32_t n, float eps) {
+  float ss = 0.0f;
+  for (uint32_t i = 0; i < n; i++) ss += x[i] * x[i];
+  const float s = 1.0f / sqrtf(ss / (float)n + eps);
+  for (uint32_t i = 0; i < n; i++) y[i] = x[i] * s * w[i];
+}
+
+/* src/cpu.c:580 */
+void or_swiglu(float *a, const float *b, uint32_t n) {
+  for (uint32_t j = 0; j < n; j++) a[j] = a[j] / (1.0f + expf(-a[j])) * b[j];
+}
+
 /* ---------------------------------------------------------------- repack */
 
 /* GGUF Q4_0 (18-byte blocks: f16 d, 16 nibble bytes) -> MAT_Q4: word w of

@@ -30,6 +30,13 @@ uint16_t or_f32_to_f16(float f);
 /* Q8 activation quantization (src/cpu.c:36-53). q gets 40*nb bytes. */
 void or_quant_q8(const float *x, uint8_t *q, uint32_t nb);
 
+/* The producers of Q8 vectors in a decode step (the float part; the Q8 copy
+ * is or_quant_q8 of the result, as src/cpu.c:501-504, 579-581 do):
+ * RMSNorm y = x s w, s = 1 / sqrtf(sum x^2 / n + eps) (src/cpu.c:276-281);
+ * SwiGLU a = a / (1 + expf(-a)) b in place (src/cpu.c:580). */
+void or_rmsnorm(const float *x, const float *w, float *y, uint32_t n, float eps);
+void or_swiglu(float *a, const float *b, uint32_t n);
+
 /* GGUF -> the reference's MAT_Q4 / MAT_Q4K layouts (src/model.c:205-219,
  * 246-267). qw: rows*nb*4 words; qs: rows*nb (Q4) or rows*nb + rows*nb/4
  * (Q4K) u16 entries. */

@@ -50,6 +50,8 @@ class Oracle:
         L.or_gemv_f64.argtypes = [C.c_int, _P, _U32, _U32, _P, _P, _P]
         L.or_q4k_qs_n.restype = C.c_size_t
         L.or_q4k_qs_n.argtypes = [_U32, _U32]
+        L.or_rmsnorm.argtypes = [_P, _P, _P, _U32, C.c_float]
+        L.or_swiglu.argtypes = [_P, _P, _U32]
 
     # -- Q8
     def quant_q8(self, x):
@@ -63,6 +65,24 @@ class Oracle:
         for i in range(flat.shape[0]):
             self.lib.or_quant_q8(_ptr(flat[i]), _ptr(out[i]), nb)
         return out.reshape(x.shape[:-1] + (40 * nb,))
+
+    # -- the producers of Q8 vectors (float part; their Q8 copy is quant_q8 of the result)
+    def rmsnorm(self, x, w, eps):
+        """y = x s w per row of x (src/cpu.c:276-281)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        flat = x.reshape(-1, x.shape[-1])
+        out = np.empty_like(flat)
+        for i in range(flat.shape[0]):
+            self.lib.or_rmsnorm(_ptr(flat[i]), _ptr(w), _ptr(out[i]), flat.shape[1], C.c_float(eps))
+        return out.reshape(x.shape)
+
+    def swiglu(self, a, b):
+        """a / (1 + expf(-a)) * b per element (src/cpu.c:580)."""
+        a = np.array(a, dtype=np.float32, copy=True)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        self.lib.or_swiglu(_ptr(a), _ptr(b), a.size)
+        return a
 
     # -- repack to the reference layouts
     def repack(self, kind, src, rows, nb):
