@@ -9,7 +9,9 @@ Names follow the reference's operators (hanw/amd.c src/backend.h:61-64,
 src/hip.c:922-1026): ``quant_q8``, ``gemv_q4``, ``gemv_q4k``, the multi-vector
 ``gemv_q4_t`` / ``gemv_q4k_t``, the prefill ``gemm_q4k`` and the dispatcher
 ``op_gemv``; ``repack_q4`` / ``repack_q4k`` replace the load-time repack of
-src/model.c:205-267.
+src/model.c:205-267. The Q8_0 and Q6_K kinds (``gemv_q8`` / ``gemv_q6k``,
+``repack_q8`` / ``repack_q6k``) follow OP_GEMV_Q8 / OP_GEMV_Q6K
+(src/hip.c:934-962, 1027-1089) and src/model.c:221-292.
 """
 import ctypes as C
 import os
@@ -20,7 +22,8 @@ PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_DIR, "libamdc_q4.so")
 HSACO_PATH = os.path.join(PKG_DIR, "amdc_kernels.hsaco")
 
-KIND_Q4_0, KIND_Q4_K = 0, 3
+KIND_Q4_0, KIND_Q8_0, KIND_Q4_K, KIND_Q6_K = 0, 2, 3, 4
+_SUF = {KIND_Q4_0: "q4", KIND_Q8_0: "q8", KIND_Q4_K: "q4k", KIND_Q6_K: "q6k"}
 _P, _U32 = C.c_void_p, C.c_uint32
 
 # every function of include/amdc_q4.h: name -> (restype, argtypes)
@@ -29,6 +32,8 @@ ABI = {
     "amdc_mat_bytes": (C.c_size_t, [C.c_int, _U32, _U32]),
     "amdc_repack_q4": (C.c_int, [_P, _U32, _U32, _P]),
     "amdc_repack_q4k": (C.c_int, [_P, _U32, _U32, _P]),
+    "amdc_repack_q8": (C.c_int, [_P, _U32, _U32, _P]),
+    "amdc_repack_q6k": (C.c_int, [_P, _U32, _U32, _P]),
     "amdc_open": (C.c_int, [C.c_char_p]),
     "amdc_close": (None, []),
     "amdc_cu_count": (C.c_int, []),
@@ -54,6 +59,12 @@ ABI = {
     "amdc_quant_q8": (C.c_int, [_P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_gemv_q4": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
     "amdc_gemv_q4k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
+    "amdc_gemv_q8": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
+    "amdc_gemv_q6k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
+    "amdc_gemv_q8_x": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P, _P]),
+    "amdc_gemv_q6k_x": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P, _P]),
+    "amdc_gemv_q8_t": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
+    "amdc_gemv_q6k_t": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_gemv_q4_x": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P, _P]),
     "amdc_gemv_q4k_x": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P, _P]),
     "amdc_gemv_q4_t": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
@@ -265,7 +276,7 @@ def repack(kind, gguf, rows, cols):
     """GGUF bytes -> the CDNA4 layout (host numpy uint8)."""
     src = np.ascontiguousarray(gguf, dtype=np.uint8)
     dst = np.empty(mat_bytes(kind, rows, cols), dtype=np.uint8)
-    f = lib().amdc_repack_q4 if kind == KIND_Q4_0 else lib().amdc_repack_q4k
+    f = getattr(lib(), "amdc_repack_" + _SUF[kind])
     _check(f(src.ctypes.data_as(_P), rows, cols, dst.ctypes.data_as(_P)))
     return dst
 
@@ -276,6 +287,14 @@ def repack_q4(gguf, rows, cols):
 
 def repack_q4k(gguf, rows, cols):
     return repack(KIND_Q4_K, gguf, rows, cols)
+
+
+def repack_q8(gguf, rows, cols):
+    return repack(KIND_Q8_0, gguf, rows, cols)
+
+
+def repack_q6k(gguf, rows, cols):
+    return repack(KIND_Q6_K, gguf, rows, cols)
 
 
 # ---------------------------------------------------------------- operators (device pointers)
@@ -292,14 +311,23 @@ def gemv_q4k(w, xq, y, rows, nb, bias=None, res=None, stream=None):
     _check(lib().amdc_gemv_q4k(_p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), stream))
 
 
+def gemv_q8(w, xq, y, rows, nb, bias=None, res=None, stream=None):
+    _check(lib().amdc_gemv_q8(_p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), stream))
+
+
+def gemv_q6k(w, xq, y, rows, nb, bias=None, res=None, stream=None):
+    _check(lib().amdc_gemv_q6k(_p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), stream))
+
+
 def gemv(kind, w, xq, y, rows, nb, bias=None, res=None, stream=None):
-    (gemv_q4k if kind == KIND_Q4_K else gemv_q4)(w, xq, y, rows, nb, bias, res, stream)
+    f = getattr(lib(), "amdc_gemv_" + _SUF[kind])
+    _check(f(_p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), stream))
 
 
 def gemv_x(kind, w, x, y, rows, nb, bias=None, res=None, q8=None, stream=None):
     """Decode GEMV on the f32 vector x (quantized in the kernel for nb <= 128, else quantize + GEMV;
     q8: optional Q8 output)."""
-    f = lib().amdc_gemv_q4k_x if kind == KIND_Q4_K else lib().amdc_gemv_q4_x
+    f = getattr(lib(), f"amdc_gemv_{_SUF[kind]}_x")
     _check(f(_p(w), _p(x), _p(y), rows, nb, _p(bias), _p(res), _p(q8), stream))
 
 
@@ -312,7 +340,8 @@ def gemv_q4k_t(w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stream=
 
 
 def gemv_t(kind, w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stream=None):
-    (gemv_q4k_t if kind == KIND_Q4_K else gemv_q4_t)(w, xq, y, rows, nb, T, xs, ys, rs, bias, res, stream)
+    f = getattr(lib(), f"amdc_gemv_{_SUF[kind]}_t")
+    _check(f(_p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), T, xs, ys, rs, stream))
 
 
 def gemm_q4k(w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stream=None):

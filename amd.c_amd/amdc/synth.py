@@ -7,11 +7,19 @@ reference's ie_f32_to_f16 (hanw/amd.c src/common.c:48-67).
 GGUF Q4_0 block (18 bytes): f16 d, 16 nibble bytes (core/ie_core.h:66-68).
 GGUF Q4_K super-block (144 bytes): f16 d, f16 dmin, 12 bytes of 6-bit scales
 and mins, 128 nibble bytes (core/ie_core.h:247-251).
+GGUF Q8_0 block (34 bytes): f16 d, 32 int8 (core/ie_core.h:187-192): f16 d =
+|N(0,1)| * 0.004, uniform bytes (-128 included).
+GGUF Q6_K super-block (210 bytes): ql[128], qh[64], int8 scales[16], f16 d
+(core/ie_core.h:309-313): uniform bytes, uniform int8 scales, f16 d =
+|N(0,1)| * 0.0005.
 """
 import numpy as np
 
-KIND_Q4_0, KIND_Q4_K = 0, 3
-GGML = {KIND_Q4_0: 2, KIND_Q4_K: 12}
+KIND_Q4_0, KIND_Q8_0, KIND_Q4_K, KIND_Q6_K = 0, 2, 3, 4  # the reference's MAT_* (src/model.h:15)
+GGML = {KIND_Q4_0: 2, KIND_Q8_0: 8, KIND_Q4_K: 12, KIND_Q6_K: 14}
+# GGUF bytes per 32 weights, and the weights per GGUF block
+BYTES_PER_32 = {KIND_Q4_0: 18.0, KIND_Q8_0: 34.0, KIND_Q4_K: 18.0, KIND_Q6_K: 26.25}
+BLOCK_WEIGHTS = {KIND_Q4_0: 32, KIND_Q8_0: 32, KIND_Q4_K: 256, KIND_Q6_K: 256}
 
 
 def rng(seed):
@@ -42,8 +50,35 @@ def gguf_q4_k(rows, cols, seed, scale=0.01):
     return blk.reshape(-1)
 
 
+def gguf_q8_0(rows, cols, seed, scale=0.004):
+    """rows x cols Q8_0 weights as GGUF bytes (rows * cols / 32 * 34)."""
+    assert cols % 32 == 0
+    g = rng(seed)
+    n = rows * (cols // 32)
+    blk = np.empty((n, 34), dtype=np.uint8)
+    d = (np.abs(g.standard_normal(n, dtype=np.float32)) * np.float32(scale)).astype(np.float16)
+    blk[:, 0:2] = d.view(np.uint8).reshape(n, 2)
+    blk[:, 2:] = g.integers(0, 256, size=(n, 32), dtype=np.uint8)
+    return blk.reshape(-1)
+
+
+def gguf_q6_k(rows, cols, seed, scale=0.0005):
+    """rows x cols Q6_K weights as GGUF bytes (rows * cols / 256 * 210)."""
+    assert cols % 256 == 0
+    g = rng(seed)
+    n = rows * (cols // 256)
+    blk = np.empty((n, 210), dtype=np.uint8)
+    blk[:, 0:208] = g.integers(0, 256, size=(n, 208), dtype=np.uint8)
+    d = (np.abs(g.standard_normal(n, dtype=np.float32)) * np.float32(scale)).astype(np.float16)
+    blk[:, 208:210] = d.view(np.uint8).reshape(n, 2)
+    return blk.reshape(-1)
+
+
+_GEN = {KIND_Q4_0: gguf_q4_0, KIND_Q8_0: gguf_q8_0, KIND_Q4_K: gguf_q4_k, KIND_Q6_K: gguf_q6_k}
+
+
 def gguf(kind, rows, cols, seed):
-    return gguf_q4_k(rows, cols, seed) if kind == KIND_Q4_K else gguf_q4_0(rows, cols, seed)
+    return _GEN[kind](rows, cols, seed)
 
 
 def activations(T, cols, seed):
@@ -52,7 +87,7 @@ def activations(T, cols, seed):
 
 
 def gguf_bytes(kind, rows, cols):
-    return rows * cols // 32 * 18
+    return int(rows * cols // 32 * BYTES_PER_32[kind])
 
 
 # The configurations (rows x cols = N outputs x K inputs).

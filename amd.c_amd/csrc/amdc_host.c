@@ -37,9 +37,13 @@ const char *amdc_last_error(void) { return g_err; }
 
 /* ---------------------------------------------------------------- repack */
 
+static int kind_ok(int kind) {
+  return kind == AMDC_KIND_Q4_0 || kind == AMDC_KIND_Q4_K || kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K;
+}
+
 size_t amdc_mat_bytes(int kind, uint32_t rows, uint32_t cols) {
-  if (cols % 32u || (kind == AMDC_KIND_Q4_K && cols % 256u) || (kind != AMDC_KIND_Q4_0 && kind != AMDC_KIND_Q4_K)) return 0;
-  return (size_t)rows * amdc_row_bytes(cols / 32u);
+  if (cols % 32u || ((kind == AMDC_KIND_Q4_K || kind == AMDC_KIND_Q6_K) && cols % 256u) || !kind_ok(kind)) return 0;
+  return (size_t)rows * amdc_row_bytes_k(kind, cols / 32u);
 }
 
 /* GGUF Q4_0: block b of row r = 18 bytes at (r nb + b) 18: f16 d, then
@@ -106,6 +110,67 @@ int amdc_repack_q4k(const uint8_t *src, uint32_t rows, uint32_t cols, uint8_t *d
         for (u32 j = 0; j < 16; j++) {
           const u32 lo = (k & 1u) ? (u32)pair[j] >> 4 : pair[j] & 15u, hi = (k & 1u) ? (u32)pair[j + 16] >> 4 : pair[j + 16] & 15u;
           o[j] = (uint8_t)(lo | (hi << 4));
+        }
+      }
+    }
+  }
+  return AMDC_OK;
+}
+
+/* GGUF Q8_0: block b of row r = 34 bytes at (r nb + b) 34: f16 d, 32 int8.
+ * The int8 bytes go to planes 2k, 2k + 1 of the block's super-group, d to
+ * its header (src/model.c:221-237 keeps the same bytes as 8 words per block
+ * and a separate f16 array). */
+int amdc_repack_q8(const uint8_t *src, uint32_t rows, uint32_t cols, uint8_t *dst) {
+  if (!src || !dst || !rows || !cols || cols % 32u) return fail(AMDC_EINVAL, "repack_q8: %ux%u (cols must be a multiple of 32)", rows, cols);
+  const u32 nb = cols / 32u, ng = amdc_ngroups(nb);
+  const u64 rb = amdc_q8_row_bytes(nb);
+  memset(dst, 0, (size_t)rows * rb);
+  for (u32 r = 0; r < rows; r++) {
+    uint8_t *row = dst + (u64)r * rb;
+    for (u32 b = 0; b < nb; b++) {
+      const uint8_t *blk = src + ((u64)r * nb + b) * 34u;
+      const u32 g = b >> 3, k = b & 7u;
+      memcpy(row + amdc_header_off(g) + 2u * k, blk, 2);
+      memcpy(row + amdc_q8_off(ng, g, 2u * k), blk + 2, 16);
+      memcpy(row + amdc_q8_off(ng, g, 2u * k + 1u), blk + 18, 16);
+    }
+  }
+  return AMDC_OK;
+}
+
+/* GGUF Q6_K: super-block g of row r = 210 bytes: ql[128], qh[64], int8
+ * scales[16], f16 d. Weight e = 128 n + 32 m + l has the low 4 bits of
+ * ql[64 n + 32 (m & 1) + l] (low nibble for m < 2, else high) and the 2 bits
+ * (qh[32 n + l] >> 2 m) & 3 above them (core/ie_core.h:309-313, 338-341).
+ * Sub-block k (weights 32k..32k+31) becomes a Q4_0-order nibble block and two
+ * high-bit words, as MAT_Q6K (src/model.c:269-292); scales and d are copied. */
+int amdc_repack_q6k(const uint8_t *src, uint32_t rows, uint32_t cols, uint8_t *dst) {
+  if (!src || !dst || !rows || !cols || cols % 256u)
+    return fail(AMDC_EINVAL, "repack_q6k: %ux%u (cols must be a multiple of 256)", rows, cols);
+  const u32 nb = cols / 32u, ng = nb / 8u;
+  const u64 rb = amdc_q6k_row_bytes(nb);
+  for (u32 r = 0; r < rows; r++) {
+    uint8_t *row = dst + (u64)r * rb;
+    memset(row + 16u * ng, 0, amdc_q6k_dpad(ng));
+    for (u32 g = 0; g < ng; g++) {
+      const uint8_t *blk = src + ((u64)r * ng + g) * 210u;
+      memcpy(row + amdc_header_off(g), blk + 192, 16);
+      memcpy(row + amdc_q6k_d_off(ng, g), blk + 208, 2);
+      for (u32 k = 0; k < 8; k++) {
+        const u32 n = k / 4u, m = k % 4u;
+        u32 q[32];
+        for (u32 l = 0; l < 32; l++) {
+          const uint8_t lo = blk[64u * n + 32u * (m & 1u) + l];
+          q[l] = (m < 2u ? (lo & 15u) : (u32)(lo >> 4)) | ((((u32)blk[128u + 32u * n + l] >> (2u * m)) & 3u) << 4);
+        }
+        uint8_t *o = row + amdc_q6k_nib_off(ng, g, k);
+        for (u32 j = 0; j < 16; j++) o[j] = (uint8_t)((q[j] & 15u) | ((q[j + 16] & 15u) << 4));
+        uint8_t *hp = row + amdc_q6k_hi_off(ng, g, k >> 1) + 8u * (k & 1u);
+        for (u32 h = 0; h < 2; h++) {
+          u32 wd = 0;
+          for (u32 e = 0; e < 16; e++) wd |= (q[16u * h + e] >> 4) << (8u * (e % 4u) + 2u * (e / 4u));
+          memcpy(hp + 4u * h, &wd, 4);
         }
       }
     }
@@ -187,6 +252,10 @@ enum {
   K_CHAIN,
   K_RMSNORM_Q8,
   K_SWIGLU_Q8,
+  K_GEMV_Q8_P2,
+  K_GEMV_Q6K_P2,
+  K_DOTS_Q8,
+  K_DOTS_Q6K,
   K_N
 };
 static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1",  "amdc_gemv_q4_k_t1",  "amdc_gemv_q4_0_t1u1",
@@ -196,7 +265,8 @@ static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1
                                        "amdc_probe_copy",     "amdc_q8_prep",       "amdc_gemmh_m64_n128", "amdc_gemmh_m64_n64",
                                        "amdc_gemm_reduce",    "amdc_gemv_q4_0_v8",  "amdc_gemv_q4_k_v8",
                                        "amdc_gemv_q4_0_x1",   "amdc_gemv_q4_k_x1",  "amdc_gemv_q4_0_p2",  "amdc_gemv_q4_k_p2",
-                                       "amdc_chain",          "amdc_rmsnorm_q8",    "amdc_swiglu_q8"};
+                                       "amdc_chain",          "amdc_rmsnorm_q8",    "amdc_swiglu_q8",     "amdc_gemv_q8_0_p2",
+                                       "amdc_gemv_q6_k_p2",   "amdc_dots_q8_0",     "amdc_dots_q6_k"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -470,10 +540,11 @@ int amdc_swiglu_q8(float *a, const float *b, uint32_t n, uint8_t *q, uint32_t T,
 }
 
 static int check_mat(const char *op, int kind, const void *w, const uint8_t *xq, const float *y, uint32_t rows, uint32_t nb) {
-  if (kind != AMDC_KIND_Q4_0 && kind != AMDC_KIND_Q4_K) return fail(AMDC_EINVAL, "%s: kind %d", op, kind);
+  if (!kind_ok(kind)) return fail(AMDC_EINVAL, "%s: kind %d", op, kind);
   if (!w || !xq || !y) return fail(AMDC_EINVAL, "%s: null pointer", op);
   if (!rows || !nb || rows >= (1u << 24) || nb >= (1u << 16)) return fail(AMDC_EINVAL, "%s: size %u rows x %u blocks", op, rows, nb);
-  if (kind == AMDC_KIND_Q4_K && nb % 8u) return fail(AMDC_EINVAL, "%s: Q4_K needs nb %% 8 == 0 (nb %u)", op, nb);
+  if ((kind == AMDC_KIND_Q4_K || kind == AMDC_KIND_Q6_K) && nb % 8u)
+    return fail(AMDC_EINVAL, "%s: %s needs nb %% 8 == 0 (nb %u)", op, kind == AMDC_KIND_Q4_K ? "Q4_K" : "Q6_K", nb);
   if (!aligned16(w) || !aligned16(xq)) return fail(AMDC_EINVAL, "%s: w and xq must be 16-byte aligned", op);
   return AMDC_OK;
 }
@@ -511,7 +582,7 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
     part = g_ws;
   }
   void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs, &part};
-  HIPCALL(H.ModuleLaunchKernel(g_k[kind ? K_GEMV_Q4K_V8 : K_GEMV_Q4_V8], wgs, ks, 1, 256, 1, 1, 0, stream, args, NULL));
+  HIPCALL(H.ModuleLaunchKernel(g_k[kind == AMDC_KIND_Q4_K ? K_GEMV_Q4K_V8 : K_GEMV_Q4_V8], wgs, ks, 1, 256, 1, 1, 0, stream, args, NULL));
   if (ks > 1u) {
     const u64 n = (u64)rows * T;
     void *ra[] = {&part, &ks, &y, &rows, &T, &bias, &res, &ys, &rs};
@@ -520,8 +591,38 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
   return AMDC_OK;
 }
 
+/* The decode GEMV of the Q8_0 and Q6_K kinds (amdc_gemv_q8_0_p2 /
+ * amdc_gemv_q6_k_p2: the buffer-load kernel with the lane split of the Q4
+ * kinds), one launch per vector: L lanes per row with up to 3 super-groups
+ * each, at most 2 workgroups per CU; LDS for the vector (40 or 44 bytes per
+ * block) and the workgroup's results. */
+static int gemv_k8_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
+                          const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  const u32 ng = amdc_ngroups(nb), bpb = kind == AMDC_KIND_Q6_K ? 44u : 40u;
+  const u64 rb = amdc_row_bytes_k(kind, nb);
+  if ((u64)rows * rb + rb >= (1ull << 32))
+    return fail(AMDC_EINVAL, "gemv: %u rows of %llu bytes: the matrix must be under 4 GiB (split the rows)", rows, (unsigned long long)rb);
+  u32 L = 4u;
+  while (L < 64u && 3u * L < ng) L <<= 1;
+  if (t_lanes > 0) L = (u32)t_lanes;
+  const u32 rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg, cap = 2u * (g_cus > 0 ? (u32)g_cus : 256u);
+  const unsigned g = t_wgs > 0 && (u32)t_wgs < nrg ? (unsigned)t_wgs : nrg < cap ? nrg : cap;
+  const u32 lds = bpb * 8u * ng + 4u * rpg * ((nrg + g - 1u) / g);
+  if (lds > GEMV_LDS_T1) return fail(AMDC_EINVAL, "gemv: nb %u too large for the staged vector (%u bytes of LDS)", nb, lds);
+  for (u32 t = 0; t < T; t++) {
+    const uint8_t *xt = xq + (u64)t * xs;
+    float *yt = y + (u64)t * ys;
+    const float *rt = res ? res + (u64)t * rs : NULL;
+    void *a[] = {&w, &xt, &yt, &rows, &nb, &bias, &rt, (void *)&L};
+    int rc = launch(kind == AMDC_KIND_Q6_K ? K_GEMV_Q6K_P2 : K_GEMV_Q8_P2, g, 1, lds, stream, a);
+    if (rc) return rc;
+  }
+  return AMDC_OK;
+}
+
 static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                        const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  if (kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) return gemv_k8_launch(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
   if (T > 1u && T <= 8u && t_unroll <= 0) return gemv8_launch(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
   const u32 ng = amdc_ngroups(nb), L = gemv_lanes(ng), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
   const u32 TT = T == 1u ? 1u : T <= 8u ? 8u : 16u;
@@ -543,17 +644,18 @@ static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uin
     const u32 lds2 = 320u * ng + 4u * rpg2 * ((nrg2 + g2 - 1u) / g2);
     if (lds2 <= GEMV_LDS_T1) {
       void *a2[] = {&w, &xq, &y, &rows, &nb, &bias, &res, (void *)&L2};
-      return launch(kind ? K_GEMV_Q4K_P2 : K_GEMV_Q4_P2, g2, 1, lds2, stream, a2);
+      return launch(kind == AMDC_KIND_Q4_K ? K_GEMV_Q4K_P2 : K_GEMV_Q4_P2, g2, 1, lds2, stream, a2);
     }
   }
   if (TT == 1u && t_unroll <= 0 && 320u * ng <= GEMV_LDS_T1) { /* the pipelined decode kernel */
     const unsigned g1 = t_wgs > 0 && (u32)t_wgs < nrg ? (unsigned)t_wgs : nrg;
     void *a1[] = {&w, &xq, &y, &rows, &nb, &bias, &res, (void *)&L};
-    return launch(kind ? K_GEMV_Q4K_P1 : K_GEMV_Q4_P1, g1, 1, 320u * ng, stream, a1);
+    return launch(kind == AMDC_KIND_Q4_K ? K_GEMV_Q4K_P1 : K_GEMV_Q4_P1, g1, 1, 320u * ng, stream, a1);
   }
   int k;
-  if (TT == 1u) k = t_unroll == 1 ? (kind ? K_GEMV_Q4K_T1U1 : K_GEMV_Q4_T1U1) : (kind ? K_GEMV_Q4K_T1 : K_GEMV_Q4_T1);
-  else k = TT == 8u ? (kind ? K_GEMV_Q4K_T8 : K_GEMV_Q4_T8) : (kind ? K_GEMV_Q4K_T16 : K_GEMV_Q4_T16);
+  const int k4 = kind == AMDC_KIND_Q4_K;
+  if (TT == 1u) k = t_unroll == 1 ? (k4 ? K_GEMV_Q4K_T1U1 : K_GEMV_Q4_T1U1) : (k4 ? K_GEMV_Q4K_T1 : K_GEMV_Q4_T1);
+  else k = TT == 8u ? (k4 ? K_GEMV_Q4K_T8 : K_GEMV_Q4_T8) : (k4 ? K_GEMV_Q4K_T16 : K_GEMV_Q4_T16);
   void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs, (void *)&L, &GC};
   return launch(k, grid, 1, lds, stream, args);
 }
@@ -607,7 +709,7 @@ static int gemv_x(int kind, const char *op, const void *w, const float *x, float
   if (rc) return rc;
   if (q8 && !aligned16(q8)) return fail(AMDC_EINVAL, "%s: q8 must be 16-byte aligned", op);
   const u32 ng = amdc_ngroups(nb), L = gemv_lanes(ng), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
-  if (nb > x_fuse_nb || 320u * ng > GEMV_LDS_T1) {
+  if (nb > x_fuse_nb || 320u * ng > GEMV_LDS_T1 || kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) {
     if (!q8) {
       if ((rc = ws_reserve((size_t)40u * nb + 64u))) return rc;
       q8 = (uint8_t *)g_ws;
@@ -620,7 +722,7 @@ static int gemv_x(int kind, const char *op, const void *w, const float *x, float
   const u32 cap = 3u * (g_cus > 0 ? (u32)g_cus : 256u);
   const unsigned grid = t_wgs > 0 && (u32)t_wgs < nrg ? (unsigned)t_wgs : nrg < cap ? nrg : cap;
   void *args[] = {&w, &x, &y, &rows, &nb, &bias, &res, (void *)&L, &q8};
-  return launch(kind ? K_GEMV_Q4K_X1 : K_GEMV_Q4_X1, grid, 1, 320u * ng, stream, args);
+  return launch(kind == AMDC_KIND_Q4_K ? K_GEMV_Q4K_X1 : K_GEMV_Q4_X1, grid, 1, 320u * ng, stream, args);
 }
 
 int amdc_gemv_q4_x(const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res, uint8_t *q8,
@@ -641,6 +743,40 @@ int amdc_gemv_q4_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, ui
 int amdc_gemv_q4k_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                     uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
   return gemv_t(AMDC_KIND_Q4_K, "gemv_q4k_t", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+}
+
+int amdc_gemv_q8(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                 void *stream) {
+  NEED_OPEN();
+  int rc = check_mat("gemv_q8", AMDC_KIND_Q8_0, w, xq, y, rows, nb);
+  return rc ? rc : gemv_launch(AMDC_KIND_Q8_0, w, xq, y, rows, nb, bias, res, 1, 0, 0, 0, stream);
+}
+
+int amdc_gemv_q6k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                  void *stream) {
+  NEED_OPEN();
+  int rc = check_mat("gemv_q6k", AMDC_KIND_Q6_K, w, xq, y, rows, nb);
+  return rc ? rc : gemv_launch(AMDC_KIND_Q6_K, w, xq, y, rows, nb, bias, res, 1, 0, 0, 0, stream);
+}
+
+int amdc_gemv_q8_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                   uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  return gemv_t(AMDC_KIND_Q8_0, "gemv_q8_t", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+}
+
+int amdc_gemv_q6k_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                    uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  return gemv_t(AMDC_KIND_Q6_K, "gemv_q6k_t", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+}
+
+int amdc_gemv_q8_x(const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res, uint8_t *q8,
+                   void *stream) {
+  return gemv_x(AMDC_KIND_Q8_0, "gemv_q8_x", w, x, y, rows, nb, bias, res, q8, stream);
+}
+
+int amdc_gemv_q6k_x(const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res, uint8_t *q8,
+                    void *stream) {
+  return gemv_x(AMDC_KIND_Q6_K, "gemv_q6k_x", w, x, y, rows, nb, bias, res, q8, stream);
 }
 
 static int ws_reserve(size_t n) {
@@ -711,8 +847,10 @@ int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uin
 int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                  const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
   NEED_OPEN();
-  if (T == 1u)
-    return kind == AMDC_KIND_Q4_K ? amdc_gemv_q4k(w, xq, y, rows, nb, bias, res, stream) : amdc_gemv_q4(w, xq, y, rows, nb, bias, res, stream);
+  if (T == 1u) {
+    int rc = check_mat("op_gemv", kind, w, xq, y, rows, nb);
+    return rc ? rc : gemv_launch(kind, w, xq, y, rows, nb, bias, res, 1, 0, 0, 0, stream);
+  }
   if (kind == AMDC_KIND_Q4_K && (int)T >= t_gemm_min && nb % 8u == 0u) return amdc_gemm_q4k(w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
   return gemv_t(kind, "op_gemv", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
 }
@@ -724,7 +862,8 @@ int amdc_block_dots(int kind, const void *w, const uint8_t *xq, int32_t *out, ui
   const u64 n = (u64)rows * nb;
   if ((n + 255u) / 256u > 0x7FFFFFFFull) return fail(AMDC_EINVAL, "block_dots: too large");
   void *args[] = {&w, &xq, &out, &rows, &nb};
-  return launch(kind == AMDC_KIND_Q4_K ? K_DOTS_Q4K : K_DOTS_Q4, (unsigned)((n + 255u) / 256u), 1, 0, stream, args);
+  const int k = kind == AMDC_KIND_Q4_K ? K_DOTS_Q4K : kind == AMDC_KIND_Q8_0 ? K_DOTS_Q8 : kind == AMDC_KIND_Q6_K ? K_DOTS_Q6K : K_DOTS_Q4;
+  return launch(k, (unsigned)((n + 255u) / 256u), 1, 0, stream, args);
 }
 
 int amdc_probe_read(const void *src, size_t nbytes, void *scratch, uint32_t grid, void *stream) {
@@ -781,6 +920,8 @@ int amdc_chain_create(const amdc_chain_op *ops, uint32_t n, void **chain) {
       e->type = 0, e->a = o->x, e->b = o->q;
     } else if (o->type == AMDC_CHAIN_GEMV) {
       rc = check_mat("chain gemv", o->kind, o->w, o->xq, o->y, o->rows, o->nb);
+      if (!rc && o->kind != AMDC_KIND_Q4_0 && o->kind != AMDC_KIND_Q4_K)
+        rc = fail(AMDC_EINVAL, "chain op %u: kind %d (the chain runs Q4_0 and Q4_K GEMVs)", k, o->kind);
       if (!rc && 320u * amdc_ngroups(o->nb) > GEMV_LDS_T1) rc = fail(AMDC_EINVAL, "chain op %u: nb %u too large", k, o->nb);
       e->type = o->kind == AMDC_KIND_Q4_K ? 2u : 1u, e->rows = o->rows, e->L = gemv_lanes(amdc_ngroups(o->nb));
       e->a = o->w, e->b = (void *)o->xq, e->y = o->y, e->bias = o->bias, e->res = o->res;

@@ -80,6 +80,40 @@ __device__ __forceinline__ int nib_dot(u32x4 w, u32x4 alo, u32x4 ahi) {
   return s;
 }
 
+// Sum over j < 32 of w_j a_j for the 32 int8 weights of a Q8_0 block (w0:
+// bytes 0..15, w1: 16..31) and activations alo, ahi (ie_q8q8_block,
+// core/ie_core.h:222-233).
+__device__ __forceinline__ int q8_dot(u32x4 w0, u32x4 w1, u32x4 alo, u32x4 ahi) {
+  int s = sdot4(w0.x, alo.x, 0);
+  s = sdot4(w0.y, alo.y, s), s = sdot4(w0.z, alo.z, s), s = sdot4(w0.w, alo.w, s);
+  s = sdot4(w1.x, ahi.x, s), s = sdot4(w1.y, ahi.y, s), s = sdot4(w1.z, ahi.z, s), s = sdot4(w1.w, ahi.w, s);
+  return s;
+}
+
+// Sum over each half h of a Q6_K sub-block of q a (q = 0..63: the nibble of
+// word nw plus the high bits of word hh << 4; weight 16h + 4i + e at bits
+// 8e + 2i of hh, so word i of the half takes (hh >> 2i) & 0x03030303, here
+// as a shift and a mask of 0x30303030). The q - 32 of the reference
+// (ie_q6k_dots, core/ie_core.h:355-389) is sum q a - 32 (sum a), subtracted
+// by the caller.
+__device__ __forceinline__ void q6k_dots(u32x4 nw, u32 h0, u32 h1, u32x4 alo, u32x4 ahi, int &d0, int &d1) {
+  const u32 M = 0x0F0F0F0Fu, M2 = 0x30303030u;
+  d0 = sdot4((nw.x & M) | ((h0 << 4) & M2), alo.x, 0);
+  d0 = sdot4((nw.y & M) | ((h0 << 2) & M2), alo.y, d0);
+  d0 = sdot4((nw.z & M) | (h0 & M2), alo.z, d0);
+  d0 = sdot4((nw.w & M) | ((h0 >> 2) & M2), alo.w, d0);
+  d1 = sdot4(((nw.x >> 4) & M) | ((h1 << 4) & M2), ahi.x, 0);
+  d1 = sdot4(((nw.y >> 4) & M) | ((h1 << 2) & M2), ahi.y, d1);
+  d1 = sdot4(((nw.z >> 4) & M) | (h1 & M2), ahi.z, d1);
+  d1 = sdot4(((nw.w >> 4) & M) | ((h1 >> 2) & M2), ahi.w, d1);
+}
+
+// The sum of the 16 int8 activations of a word quad.
+__device__ __forceinline__ int hsum16(u32x4 a) {
+  const u32 one = 0x01010101u;
+  return sdot4(a.w, one, sdot4(a.z, one, sdot4(a.y, one, sdot4(a.x, one, 0))));
+}
+
 // The 6-bit scale and min of sub-block k of a Q4_K header (amdc_layout.h).
 __device__ __forceinline__ u32 q4k_sc(u32x4 h, u32 k) { return (u32)((((u64)h.z << 32) | h.y) >> (6u * k)) & 63u; }
 __device__ __forceinline__ u32 q4k_mn(u32x4 h, u32 k) { return (u32)((((u64)h.w << 32) | h.z) >> (16u + 6u * k)) & 63u; }
@@ -336,6 +370,17 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, const u
 struct Item {
   u32x4 h, n[8];
 };
+// The weights of one super-group of the other kinds (amdc_layout.h).
+struct ItemQ8 {
+  u32x4 h, n[16];
+};
+struct ItemQ6 {
+  u32x4 h, n[8], x[4];
+  u32 d;
+};
+template <int KIND> struct ItemOf { using type = Item; };
+template <> struct ItemOf<AMDC_Q8_0> { using type = ItemQ8; };
+template <> struct ItemOf<AMDC_Q6_K> { using type = ItemQ6; };
 
 // The loads are unconditional (a lane past the last super-group reads the
 // row's first one again, inside the same wave's lines, and ignores it): no
@@ -349,23 +394,43 @@ __device__ __forceinline__ void load_item(Item &it, const uint8_t *wr, u32 ng, u
   for (u32 k = 0; k < 8u; k++) it.n[k] = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_nib_off(ng, g, k)));
 }
 
+// One super-group's contribution to a row: for each of its 8 blocks k (LDS
+// slot p = k GC + gl of the staged vector), the integer block dot and the
+// reference's per-block float step (src/cpu.c:81, 112, 142, 168).
 template <int KIND>
-__device__ __forceinline__ float item_dot(const Item &it, u32 gl, u32 GC, const u32x4 *s_lo, const u32x4 *s_hi, const float *s_d,
-                                          const u32 *s_as, float acc) {
+__device__ __forceinline__ float item_dot(const typename ItemOf<KIND>::type &it, u32 gl, u32 GC, const u32x4 *s_lo, const u32x4 *s_hi,
+                                          const float *s_d, const u32 *s_as, float acc) {
   float dsc = 0.0f, dmn = 0.0f;
-  if (KIND == AMDC_Q4_K) dsc = h2f(it.h.x), dmn = h2f(it.h.x >> 16);
+  if constexpr (KIND == AMDC_Q4_K) dsc = h2f(it.h.x), dmn = h2f(it.h.x >> 16);
+  if constexpr (KIND == AMDC_Q6_K) dsc = h2f(it.d);
 #pragma unroll
   for (u32 k = 0; k < 8u; k++) {
     const u32 p = k * GC + gl;
-    const int dq = nib_dot(it.n[k], s_lo[p], s_hi[p]);
     const float da = s_d[p];
-    const u32 as = s_as[p];
-    if (KIND == AMDC_Q4_0) {
+    if constexpr (KIND == AMDC_Q8_0) {
+      const int dq = q8_dot(it.n[2u * k], it.n[2u * k + 1u], s_lo[p], s_hi[p]);
       const float sw = h2f(hword(it.h, k >> 1) >> (16u * (k & 1u)));
-      acc += (sw * da) * (float)(int)((u32)dq - 8u * as);
+      acc += (sw * da) * (float)dq;
+    } else if constexpr (KIND == AMDC_Q6_K) {
+      // half h of sub-block k: sum (q - 32) a = sum q a - 32 (sum a); the
+      // staged vector holds 32 (sum a) of each half (two u32 per block)
+      int d0, d1;
+      q6k_dots(it.n[k], hword(it.x[k >> 1], 2u * (k & 1u)), hword(it.x[k >> 1], 2u * (k & 1u) + 1u), s_lo[p], s_hi[p], d0, d1);
+      const u32x2 hs = ((const u32x2 *)s_as)[p];
+      d0 = (int)((u32)d0 - hs.x), d1 = (int)((u32)d1 - hs.y);
+      const u32 sw = hword(it.h, k >> 1) >> (16u * (k & 1u));
+      const float s0 = dsc * (float)(int)(int8_t)(sw & 255u), s1 = dsc * (float)(int)(int8_t)((sw >> 8) & 255u);
+      acc = __builtin_fmaf(__builtin_fmaf(s1, (float)d1, s0 * (float)d0), da, acc);
     } else {
-      const float sw = dsc * (float)q4k_sc(it.h, k), mm = dmn * (float)q4k_mn(it.h, k);
-      acc = __builtin_fmaf(-mm, da * (float)(int)as, __builtin_fmaf(sw * (float)dq, da, acc));
+      const int dq = nib_dot(it.n[k], s_lo[p], s_hi[p]);
+      const u32 as = s_as[p];
+      if constexpr (KIND == AMDC_Q4_0) {
+        const float sw = h2f(hword(it.h, k >> 1) >> (16u * (k & 1u)));
+        acc += (sw * da) * (float)(int)((u32)dq - 8u * as);
+      } else {
+        const float sw = dsc * (float)q4k_sc(it.h, k), mm = dmn * (float)q4k_mn(it.h, k);
+        acc = __builtin_fmaf(-mm, da * (float)(int)as, __builtin_fmaf(sw * (float)dq, da, acc));
+      }
     }
   }
   return acc;
@@ -522,8 +587,9 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_x1(const uint8_
 // alternate (a 2-way unrolled loop: no register copy, which would wait for
 // the loads). The bias and residual values of an item's row come with it
 // (loads out of range when absent).
+template <int KIND>
 struct Item2 {
-  Item w;
+  typename ItemOf<KIND>::type w;
   float b, r;
 };
 
@@ -535,7 +601,7 @@ __device__ __forceinline__ void gemv2_body(const uint8_t *__restrict__ W, const 
   const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw;
   const u32 nrg = (rows + rpg - 1u) / rpg, ni = (ng + L - 1u) / L;
   if (blockIdx.x >= nrg) return; // the whole workgroup
-  const u32 RB = 144u * ng, NR = rows * RB; // the host checks NR + RB < 2^32
+  const u32 RB = (u32)amdc_row_bytes_k(KIND, nb), NR = rows * RB; // the host checks NR + RB < 2^32
   const u32 nblk = 8u * ng;
   u32x4 *s_lo = (u32x4 *)smem;
   u32x4 *s_hi = s_lo + nblk;
@@ -546,15 +612,29 @@ __device__ __forceinline__ void gemv2_body(const uint8_t *__restrict__ W, const 
   const u32 rbase = wv * rpw + q;
 
   // an item's loads: position (j, i) = row group blockIdx.x + j gridDim.x, super-group l + L i
-  auto load = [&](Item2 &it, u32 f, u32 j, u32 i) {
+  auto load = [&](Item2<KIND> &it, u32 f, u32 j, u32 i) {
     const u32 r = (blockIdx.x + j * gridDim.x) * rpg + rbase, g = l + L * i;
     const bool ok = f < n && g < ng && r < rows;
     const u32 t = g >> 3, gt = ng - 8u * t < 8u ? ng - 8u * t : 8u;
     const u32 base = ok ? r * RB : NR;
     it.w.h = __builtin_amdgcn_raw_buffer_load_b128(rw, base + 16u * g, 0, 0);
-    const u32 o0 = base + 16u * ng + 1024u * t + 16u * (g & 7u);
+    if constexpr (KIND == AMDC_Q8_0) {
+      const u32 o0 = base + 16u * ng + 2048u * t + 16u * (g & 7u);
 #pragma unroll
-    for (u32 k = 0; k < 8u; k++) it.w.n[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, o0 + 16u * gt * k, 0, 0);
+      for (u32 k = 0; k < 16u; k++) it.w.n[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, o0 + 16u * gt * k, 0, 0);
+    } else if constexpr (KIND == AMDC_Q6_K) {
+      const u32 D = amdc_q6k_dpad(ng), o0 = base + 16u * ng + D + 1024u * t + 16u * (g & 7u);
+      const u32 o1 = base + 144u * ng + D + 512u * t + 16u * (g & 7u);
+#pragma unroll
+      for (u32 k = 0; k < 8u; k++) it.w.n[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, o0 + 16u * gt * k, 0, 0);
+#pragma unroll
+      for (u32 k = 0; k < 4u; k++) it.w.x[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, o1 + 16u * gt * k, 0, 0);
+      it.w.d = __builtin_amdgcn_raw_buffer_load_b16(rw, base + 16u * ng + 2u * g, 0, 0);
+    } else {
+      const u32 o0 = base + 16u * ng + 1024u * t + 16u * (g & 7u);
+#pragma unroll
+      for (u32 k = 0; k < 8u; k++) it.w.n[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, o0 + 16u * gt * k, 0, 0);
+    }
     const u32 ro = f < n && r < rows ? 4u * r : 0xFFFFFFF0u;
     it.b = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, ro, 0, 0));
     it.r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, ro, 0, 0));
@@ -578,7 +658,13 @@ __device__ __forceinline__ void gemv2_body(const uint8_t *__restrict__ W, const 
       const u32 p = (jb & 7u) * ng + (jb >> 3);
       const bool in = jb < nb;
       s_lo[p] = in ? slo[i] : (u32x4)(0u), s_hi[p] = in ? shi[i] : (u32x4)(0u);
-      s_d[p] = in ? sd[i] : 0.0f, s_as[p] = in ? sa[i] : 0u;
+      s_d[p] = in ? sd[i] : 0.0f;
+      if constexpr (KIND == AMDC_Q6_K) { // 32 x the sum of each half of the block
+        const int h0 = hsum16(slo[i]), h1 = hsum16(shi[i]);
+        ((u32x2 *)s_as)[p] = in ? (u32x2){32u * (u32)h0, 32u * (u32)h1} : (u32x2)(0u);
+      } else if constexpr (KIND != AMDC_Q8_0) {
+        s_as[p] = in ? sa[i] : 0u;
+      }
     }
   };
   for (u32 c = SCH; NT * c < nblk; c++) { // past SCH blocks per thread (more than 24576 columns)
@@ -588,7 +674,7 @@ __device__ __forceinline__ void gemv2_body(const uint8_t *__restrict__ W, const 
 #pragma unroll
   for (u32 c = 0; c < SCH; c++) sload(c, c);
   __asm__ volatile("" ::: "memory"); // the activation loads ahead of the weight loads
-  Item2 A, B;
+  Item2<KIND> A, B;
   load(A, 0u, 0u, 0u);
 #pragma unroll
   for (u32 c = 0; c < SCH; c++) sstore(c, c);
@@ -597,9 +683,9 @@ __device__ __forceinline__ void gemv2_body(const uint8_t *__restrict__ W, const 
   // the results of the workgroup's rows collect in LDS (after the staged
   // vector) and go out after the loop: a store inside the loop would make the
   // reuse of its registers wait for every load in flight
-  float *s_y = (float *)(s_as + nblk);
+  float *s_y = (float *)(s_as + (KIND == AMDC_Q6_K ? 2u : 1u) * nblk);
   float acc = 0.0f;
-  auto comp = [&](const Item2 &it, u32 j, u32 i) {
+  auto comp = [&](const Item2<KIND> &it, u32 j, u32 i) {
     const u32 g = l + L * i;
     const float a2 = item_dot<KIND>(it.w, g < ng ? g : 0u, ng, s_lo, s_hi, s_d, s_as, acc);
     acc = g < ng ? a2 : acc;
@@ -644,6 +730,14 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_0_p2(const uint8_
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_p2(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 L) {
   gemv2_body<AMDC_Q4_K>(W, xq, y, rows, nb, bias, res, L);
+}
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_p2(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+                                                                   const float *bias, const float *res, u32 L) {
+  gemv2_body<AMDC_Q8_0>(W, xq, y, rows, nb, bias, res, L);
+}
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_p2(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+                                                                   const float *bias, const float *res, u32 L) {
+  gemv2_body<AMDC_Q6_K>(W, xq, y, rows, nb, bias, res, L);
 }
 
 // ------------------------------------------------------------------ GEMV chain (one launch)
@@ -924,6 +1018,34 @@ extern "C" __global__ __launch_bounds__(256) void amdc_dots_q4_0(const uint8_t *
 }
 extern "C" __global__ __launch_bounds__(256) void amdc_dots_q4_k(const uint8_t *W, const uint8_t *xq, int *out, u32 rows, u32 nb) {
   dots_body<AMDC_Q4_K>(W, xq, out, rows, nb);
+}
+// Q8_0: out[r * nb + b] = sum q a (ie_q8q8_block). Q6_K: out[(r * nb + b) * 2
+// + h] = sum over half h of (q - 32) a (ie_q6k_dots), by the integer steps
+// of the GEMV (q8_dot, q6k_dots, hsum16). One thread per block.
+extern "C" __global__ __launch_bounds__(256) void amdc_dots_q8_0(const uint8_t *W, const uint8_t *xq, int *out, u32 rows, u32 nb) {
+  const u64 i = (u64)blockIdx.x * NT + threadIdx.x;
+  if (i >= (u64)rows * nb) return;
+  const u32 r = (u32)(i / nb), b = (u32)(i - (u64)r * nb), ng = amdc_ngroups(nb);
+  const uint8_t *wr = W + (u64)r * amdc_q8_row_bytes(nb);
+  const u32x4 w0 = *(const u32x4 *)(wr + amdc_q8_off(ng, b >> 3, 2u * (b & 7u)));
+  const u32x4 w1 = *(const u32x4 *)(wr + amdc_q8_off(ng, b >> 3, 2u * (b & 7u) + 1u));
+  const u32x4 lo = *(const u32x4 *)(xq + 32u * b), hi = *(const u32x4 *)(xq + 32u * b + 16u);
+  const int dq = q8_dot(w0, w1, lo, hi);
+  out[i] = dq;
+}
+extern "C" __global__ __launch_bounds__(256) void amdc_dots_q6_k(const uint8_t *W, const uint8_t *xq, int *out, u32 rows, u32 nb) {
+  const u64 i = (u64)blockIdx.x * NT + threadIdx.x;
+  if (i >= (u64)rows * nb) return;
+  const u32 r = (u32)(i / nb), b = (u32)(i - (u64)r * nb), ng = nb / 8u, k = b & 7u;
+  const uint8_t *wr = W + (u64)r * amdc_q6k_row_bytes(nb);
+  const u32x4 nw = *(const u32x4 *)(wr + amdc_q6k_nib_off(ng, b >> 3, k));
+  const u32x2 hw = *(const u32x2 *)(wr + amdc_q6k_hi_off(ng, b >> 3, k >> 1) + 8u * (k & 1u));
+  const u32x4 lo = *(const u32x4 *)(xq + 32u * b), hi = *(const u32x4 *)(xq + 32u * b + 16u);
+  int d0, d1;
+  q6k_dots(nw, hw.x, hw.y, lo, hi, d0, d1);
+  const int s0 = hsum16(lo), s1 = hsum16(hi);
+  out[2u * i] = d0 - 32 * s0;
+  out[2u * i + 1u] = d1 - 32 * s1;
 }
 
 // ------------------------------------------------------------------ prefill GEMM

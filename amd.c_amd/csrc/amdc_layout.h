@@ -24,7 +24,30 @@
  * one plane are consecutive in a tile): every load is 128 bits wide and every
  * wave load is a run of whole 128-byte lines. The prefill GEMM reads one plane
  * of one tile (8 blocks, 128 contiguous bytes per row) per K step.
- * Blocks past nb (Q4_0 with nb % 8 != 0) are zero bytes with scale 0. */
+ * Blocks past nb (Q4_0 with nb % 8 != 0) are zero bytes with scale 0.
+ *
+ * Q8_0 (amdc_q8_*): the same super-groups, row = 272 ng bytes (= 34 nb, the
+ * GGUF size, when nb % 8 == 0):
+ *   header panel  ng x 16 bytes: 8 x f16 d, as Q4_0
+ *   int8 panel    ng x 256 bytes from byte 16 ng: 16 planes of 16 bytes per
+ *     super-group (plane 2k + h: bytes 16h .. 16h + 15 of block 8g + k), in
+ *     tiles of 8 super-groups, plane-major: (g, p) at 16 ng + 2048 t +
+ *     16 (p gt + g % 8).
+ * Q6_K (amdc_q6k_*, nb % 8 == 0: a super-group is a Q6_K super-block), row =
+ * 208 ng + D bytes, D = 2 ng rounded up to 16 (= 210 ng + < 16 padding):
+ *   scale panel   ng x 16 bytes: the 16 int8 scales of super-group g at 16 g
+ *     (scale 2k + h: half h of sub-block k, the GGUF order)
+ *   d panel       ng x 2 bytes from 16 ng: f16 d of super-group g at 2 g
+ *   nibble panel  ng x 128 bytes from 16 ng + D: the low 4 bits of each
+ *     weight as a Q4_0-order block, placed as the Q4 nibble panel (tiles of
+ *     1024 bytes)
+ *   high panel    ng x 64 bytes from 144 ng + D: the high 2 bits, two words
+ *     per sub-block (word h: weights 16h .. 16h + 15, weight 16h + 4i + e at
+ *     bits 8e + 2i, the reference's MAT_Q6K packing, core/ie_core.h:314-349);
+ *     plane p (< 4) = the 4 words of sub-blocks 2p, 2p + 1, in tiles of 8
+ *     super-groups: (g, p) at 144 ng + D + 512 t + 16 (p gt + g % 8).
+ * A lane owning super-group g reads it in 17 (Q8_0) or 13 loads of 128 bits
+ * plus one of 16 bits (Q6_K), each a part of a wave-wide run of lines. */
 #ifndef AMDC_LAYOUT_H
 #define AMDC_LAYOUT_H
 
@@ -37,7 +60,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-enum { AMDC_Q4_0 = 0, AMDC_Q4_K = 3 }; /* the reference's MAT_Q4 / MAT_Q4K (src/model.h:15) */
+enum { AMDC_Q4_0 = 0, AMDC_Q8_0 = 2, AMDC_Q4_K = 3, AMDC_Q6_K = 4 }; /* the reference's MAT_* (src/model.h:15) */
 
 AMDC_INLINE uint32_t amdc_ngroups(uint32_t nb) { return (nb + 7u) >> 3; }
 AMDC_INLINE uint64_t amdc_row_bytes(uint32_t nb) { return 144ull * amdc_ngroups(nb); }
@@ -46,6 +69,30 @@ AMDC_INLINE uint64_t amdc_header_off(uint32_t g) { return 16ull * g; }
 AMDC_INLINE uint64_t amdc_nib_off(uint32_t ng, uint32_t g, uint32_t k) {
   const uint32_t t = g >> 3, gt = (ng - 8u * t) < 8u ? (ng - 8u * t) : 8u;
   return 16ull * ng + 1024ull * t + 16ull * (k * gt + (g & 7u));
+}
+
+/* tile t of 8 super-groups holds gt of them */
+AMDC_INLINE uint32_t amdc_tile_gt(uint32_t ng, uint32_t t) { return (ng - 8u * t) < 8u ? (ng - 8u * t) : 8u; }
+
+AMDC_INLINE uint64_t amdc_q8_row_bytes(uint32_t nb) { return 272ull * amdc_ngroups(nb); }
+/* plane p (< 16) of super-group g */
+AMDC_INLINE uint64_t amdc_q8_off(uint32_t ng, uint32_t g, uint32_t p) {
+  return 16ull * ng + 2048ull * (g >> 3) + 16ull * (p * amdc_tile_gt(ng, g >> 3) + (g & 7u));
+}
+
+AMDC_INLINE uint32_t amdc_q6k_dpad(uint32_t ng) { return (2u * ng + 15u) & ~15u; }
+AMDC_INLINE uint64_t amdc_q6k_row_bytes(uint32_t nb) { return 208ull * amdc_ngroups(nb) + amdc_q6k_dpad(amdc_ngroups(nb)); }
+AMDC_INLINE uint64_t amdc_q6k_d_off(uint32_t ng, uint32_t g) { return 16ull * ng + 2ull * g; }
+AMDC_INLINE uint64_t amdc_q6k_nib_off(uint32_t ng, uint32_t g, uint32_t k) {
+  return 16ull * ng + amdc_q6k_dpad(ng) + 1024ull * (g >> 3) + 16ull * (k * amdc_tile_gt(ng, g >> 3) + (g & 7u));
+}
+AMDC_INLINE uint64_t amdc_q6k_hi_off(uint32_t ng, uint32_t g, uint32_t p) {
+  return 144ull * ng + amdc_q6k_dpad(ng) + 512ull * (g >> 3) + 16ull * (p * amdc_tile_gt(ng, g >> 3) + (g & 7u));
+}
+
+/* bytes of a row of any kind */
+AMDC_INLINE uint64_t amdc_row_bytes_k(int kind, uint32_t nb) {
+  return kind == AMDC_Q8_0 ? amdc_q8_row_bytes(nb) : kind == AMDC_Q6_K ? amdc_q6k_row_bytes(nb) : amdc_row_bytes(nb);
 }
 
 #endif

@@ -31,15 +31,18 @@ extern "C" {
 
 enum { AMDC_OK = 0, AMDC_EINVAL = 1, AMDC_ENOHIP = 2, AMDC_EHIP = 3, AMDC_ENOTOPEN = 4 };
 
-/* Matrix kinds: the reference's MAT_Q4 and MAT_Q4K (src/model.h:15). */
-enum { AMDC_KIND_Q4_0 = 0, AMDC_KIND_Q4_K = 3 };
+/* Matrix kinds: the reference's MAT_Q4, MAT_Q8, MAT_Q4K and MAT_Q6K
+ * (src/model.h:15). */
+enum { AMDC_KIND_Q4_0 = 0, AMDC_KIND_Q8_0 = 2, AMDC_KIND_Q4_K = 3, AMDC_KIND_Q6_K = 4 };
 
 const char *amdc_last_error(void);
 
 /* ---------------------------------------------------------------- load time (host only) */
 
-/* Bytes of a repacked rows x cols matrix (cols % 32 == 0; Q4_K: cols % 256
- * == 0): 144 * ceil(cols / 256) per row, the GGUF size when cols % 256 == 0. */
+/* Bytes of a repacked rows x cols matrix (cols % 32 == 0; Q4_K and Q6_K:
+ * cols % 256 == 0) per row: Q4_0, Q4_K 144 * ceil(cols / 256), Q8_0 272 *
+ * ceil(cols / 256) (the GGUF sizes when cols % 256 == 0), Q6_K 210 cols / 256
+ * plus under 16 bytes of padding. 0 for an unknown kind or shape. */
 size_t amdc_mat_bytes(int kind, uint32_t rows, uint32_t cols);
 
 /* GGUF Q4_0 (18-byte blocks) / Q4_K (144-byte super-blocks) bytes of a
@@ -50,6 +53,13 @@ size_t amdc_mat_bytes(int kind, uint32_t rows, uint32_t cols);
  * src/model.c:24-31, then repacked 8 per 6 bytes). Host memory only. */
 int amdc_repack_q4(const uint8_t *gguf, uint32_t rows, uint32_t cols, uint8_t *dst);
 int amdc_repack_q4k(const uint8_t *gguf, uint32_t rows, uint32_t cols, uint8_t *dst);
+/* GGUF Q8_0 (34-byte blocks) / Q6_K (210-byte super-blocks) -> the CDNA4
+ * layout. Replace repack_q8 (src/model.c:221-237) and repack_q6k
+ * (src/model.c:269-292): the int8 weights, the Q6_K scales and d are kept bit
+ * for bit; the 6-bit Q6_K weights are split into Q4_0-order nibbles and the
+ * reference's high-bit words (core/ie_core.h:314-349). */
+int amdc_repack_q8(const uint8_t *gguf, uint32_t rows, uint32_t cols, uint8_t *dst);
+int amdc_repack_q6k(const uint8_t *gguf, uint32_t rows, uint32_t cols, uint8_t *dst);
 
 /* ---------------------------------------------------------------- runtime */
 
@@ -108,6 +118,16 @@ int amdc_gemv_q4(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint
                  void *stream);
 int amdc_gemv_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                   void *stream);
+/* The same for Q8_0 and Q6_K matrices (amdc_repack_q8 / _q6k; Q6_K: nb %
+ * 8 == 0; the matrix under 4 GiB): replace OP_GEMV_Q8 / ie_gemv_q8q8
+ * (src/hip.c:1027-1089, kernels/ie_kernels.c:837) and OP_GEMV_Q6K /
+ * ie_gemv_q6kq8 (src/hip.c:934-962, kernels/ie_kernels.c:675). Per block, the
+ * reference's integer dot (ie_q8q8_block; the two half dots sum (q - 32) a
+ * of ie_q6k_dots) and float step (src/cpu.c:168, 142). */
+int amdc_gemv_q8(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                 void *stream);
+int amdc_gemv_q6k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                  void *stream);
 
 /* The fused Q8 producers (the float op and the Q8 copy of its result, bit
  * for bit amdc_quant_q8 of that result, in one launch), as the reference's
@@ -136,6 +156,11 @@ int amdc_gemv_q4_x(const void *w, const float *x, float *y, uint32_t rows, uint3
                    void *stream);
 int amdc_gemv_q4k_x(const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res, uint8_t *q8,
                     void *stream);
+/* Q8_0 / Q6_K: always amdc_quant_q8 and the GEMV (two launches). */
+int amdc_gemv_q8_x(const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res, uint8_t *q8,
+                   void *stream);
+int amdc_gemv_q6k_x(const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res, uint8_t *q8,
+                    void *stream);
 
 /* y_t = W x_t for T Q8 vectors (MTP verify, any T >= 1; the weights are
  * read once per 16 vectors, T <= 8 on int8 MFMA, the exact integer dots of
@@ -151,6 +176,13 @@ int amdc_gemv_q4_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, ui
                    uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 int amdc_gemv_q4k_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                     uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
+/* Q8_0 / Q6_K over T vectors: the decode GEMV per vector (the multi-token
+ * branches of OP_GEMV_Q8 and OP_GEMV_Q6K, ie_gemv_q8q8_t / _tr and
+ * ie_gemv_q6kq8_tr / _tr8 / _ts2, src/hip.c:934-962, 1027-1089). */
+int amdc_gemv_q8_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                   uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
+int amdc_gemv_q6k_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                    uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 
 /* The prefill chunk GEMM for Q4_K weights (nb % 8 == 0): the arguments of
  * ie_gemm_q4kr (kernels/ie_kernels.c:1289, src/hip.c:998-1001). The integer
@@ -163,16 +195,18 @@ int amdc_gemv_q4k_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, u
 int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                   uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 
-/* The dispatch of launch_op for OP_GEMV_Q4 / OP_GEMV_Q4K over T tokens
- * (src/hip.c:928-1026): T == 1 -> the decode GEMV; Q4_K with T >=
- * IE_GEMM_MIN (env, default 17) and nb % 8 == 0 -> the GEMM; else the
- * multi-vector GEMV. kind: AMDC_KIND_Q4_0 or AMDC_KIND_Q4_K. */
+/* The dispatch of launch_op for OP_GEMV_Q4 / OP_GEMV_Q8 / OP_GEMV_Q4K /
+ * OP_GEMV_Q6K over T tokens (src/hip.c:928-1089): T == 1 -> the decode GEMV;
+ * Q4_K with T >= IE_GEMM_MIN (env, default 17) and nb % 8 == 0 -> the GEMM;
+ * else the multi-vector GEMV. kind: any AMDC_KIND_*. */
 int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                  const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 
 /* Parity probe: out[r * nb + b] = the int32 dot product of block b of row r
  * with Q8 block b, as the GEMV kernels compute it: sum (q - 8) a for Q4_0
- * (core/ie_core.h:161 ie_q4q8_block), sum q a for Q4_K (ie_q4k_dot, :281). */
+ * (core/ie_core.h:161 ie_q4q8_block), sum q a for Q4_K (ie_q4k_dot, :281)
+ * and Q8_0 (ie_q8q8_block, :222). Q6_K: two per block, out[(r * nb + b) * 2
+ * + h] = sum (q - 32) a over half h (ie_q6k_dots, :384). */
 int amdc_block_dots(int kind, const void *w, const uint8_t *xq, int32_t *out, uint32_t rows, uint32_t nb, void *stream);
 
 /* Tuning knobs (0 = automatic): lanes per row of the GEMV (4..64, power of

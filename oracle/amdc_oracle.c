@@ -155,6 +155,61 @@ void or_repack_q4k(const uint8_t *src, uint32_t rows, uint32_t nb, uint32_t *qw,
     }
 }
 
+/* GGUF Q8_0 (34-byte blocks: f16 d, 32 int8) -> MAT_Q8: word w of block b
+ * of row r = int8 bytes 4w..4w+3 at (r*nb + b)*8 + w; qs[r*nb + b] = d
+ * (src/model.c:221-237, core/ie_core.h:187-198). */
+void or_repack_q8(const uint8_t *src, uint32_t rows, uint32_t nb, uint32_t *qw, uint16_t *qs) {
+  for (size_t i = 0; i < (size_t)rows * nb; i++) {
+    const uint8_t *blk = src + 34u * i;
+    qs[i] = (uint16_t)(blk[0] | (blk[1] << 8));
+    for (u32 w = 0; w < 8; w++)
+      qw[8u * i + w] = (u32)blk[2 + 4 * w] | ((u32)blk[3 + 4 * w] << 8) | ((u32)blk[4 + 4 * w] << 16) | ((u32)blk[5 + 4 * w] << 24);
+  }
+}
+
+size_t or_q6k_qs_n(uint32_t rows, uint32_t nb) { return (size_t)rows * nb + (size_t)rows * (nb / 8u); }
+
+/* The 6-bit q (0..63) of weight e (< 256) of a GGUF Q6_K super-block
+ * (210 bytes: ql[128], qh[64], int8 sc[16], f16 d): e = 128 n + 32 m + l,
+ * low 4 bits = nibble (m < 2: low, else high) of ql[64 n + 32 (m & 1) + l],
+ * high 2 bits = (qh[32 n + l] >> 2 m) & 3 (core/ie_core.h:309-313, 338-341). */
+static u32 q6k_q(const uint8_t *blk, u32 e) {
+  const u32 n = e / 128u, m = (e / 32u) % 4u, l = e % 32u;
+  const uint8_t lo = blk[64u * n + 32u * (m & 1u) + l];
+  const u32 nib = m < 2u ? (lo & 15u) : (u32)(lo >> 4);
+  return nib | ((((u32)blk[128u + 32u * n + l] >> (2u * m)) & 3u) << 4);
+}
+
+/* GGUF Q6_K -> MAT_Q6K (src/model.c:269-292, core/ie_core.h:314-349): the
+ * low 4 bits of sub-block b as a Q4_0-order block at qw word (r*nb + b)*4;
+ * the high 2 bits in two words per sub-block at rows*nb*4 + (r*nb + b)*2 + h,
+ * weight 16h + 4k + i at bits 8i + 2k; qs[r*nb + b] = sc[2b'] | sc[2b'+1] << 8
+ * (b' = b % 8), then the f16 d of super-block s of row r at rows*nb + r*(nb/8) + s. */
+void or_repack_q6k(const uint8_t *src, uint32_t rows, uint32_t nb, uint32_t *qw, uint16_t *qs) {
+  const u32 ns = nb / 8u;
+  for (u32 r = 0; r < rows; r++)
+    for (u32 s = 0; s < ns; s++) {
+      const uint8_t *blk = src + ((size_t)r * ns + s) * 210u;
+      qs[(size_t)rows * nb + (size_t)r * ns + s] = (uint16_t)(blk[208] | (blk[209] << 8));
+      for (u32 k = 0; k < 8; k++) {
+        const u32 b = s * 8u + k;
+        u32 q[32];
+        for (u32 j = 0; j < 32; j++) q[j] = q6k_q(blk, 32u * k + j);
+        u32 *dst = qw + ((size_t)r * nb + b) * 4u;
+        for (u32 w = 0; w < 4; w++) {
+          dst[w] = 0;
+          for (u32 i = 0; i < 4; i++) dst[w] |= ((q[4 * w + i] & 15u) | ((q[4 * w + i + 16] & 15u) << 4)) << (8 * i);
+        }
+        u32 *hw = qw + (size_t)rows * nb * 4u + ((size_t)r * nb + b) * 2u;
+        for (u32 h = 0; h < 2; h++) {
+          hw[h] = 0;
+          for (u32 e = 0; e < 16; e++) hw[h] |= (q[16 * h + e] >> 4) << (8u * (e % 4u) + 2u * (e / 4u));
+        }
+        qs[(size_t)r * nb + b] = (uint16_t)(blk[192 + 2 * k] | (blk[193 + 2 * k] << 8));
+      }
+    }
+}
+
 /* ---------------------------------------------------------------- integer dots */
 
 static inline u32 sext8(u32 v) { return (v & 128u) ? (v | 0xFFFFFF00u) : (v & 255u); }
@@ -192,6 +247,47 @@ void or_block_dots_q4k(const uint32_t *qw, uint32_t rows, uint32_t nb, const uin
     for (u32 b = 0; b < nb; b++) out[r * nb + b] = (int32_t)q4k_dot(qw + (r * nb + b) * 4u, aw + 8u * b);
 }
 
+/* acc + the signed-by-signed dot4 (core/ie_core.h:205-218). */
+static inline u32 dot4_ss(u32 acc, u32 a, u32 b) {
+  for (u32 e = 0; e < 4; e++) acc += sext8((a >> (8 * e)) & 255u) * sext8((b >> (8 * e)) & 255u);
+  return acc;
+}
+
+/* The Q8_0 block dot: 8 dot4 of the int8 words (core/ie_core.h:222-233). */
+static inline u32 q8q8_block(const u32 *w, const u32 *a) {
+  u32 acc = 0;
+  for (u32 k = 0; k < 8; k++) acc = dot4_ss(acc, w[k], a[k]);
+  return acc;
+}
+
+/* Half h of a MAT_Q6K sub-block: sum over its 16 weights of (q - 32) a, by 4
+ * signed dot4 of the q - 32 bytes ((v | 0x80) - 0x20) ^ 0x80 per byte, where
+ * v = nibble | high bits << 4 (core/ie_core.h:355-389). */
+static inline u32 q6k_half(const u32 *nw, u32 hword, const u32 *a, u32 h) {
+  u32 acc = 0;
+  for (u32 k = 0; k < 4; k++) {
+    const u32 nib = h == 0 ? nw[k] & 0x0F0F0F0Fu : (nw[k] >> 4) & 0x0F0F0F0Fu;
+    const u32 v = nib | (((hword >> (2u * k)) & 0x03030303u) << 4);
+    acc = dot4_ss(acc, ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u, a[4 * h + k]);
+  }
+  return acc;
+}
+
+void or_block_dots_q8(const uint32_t *qw, uint32_t rows, uint32_t nb, const uint8_t *xq, int32_t *out) {
+  const u32 *aw = (const u32 *)xq;
+  for (size_t r = 0; r < rows; r++)
+    for (u32 b = 0; b < nb; b++) out[r * nb + b] = (int32_t)q8q8_block(qw + (r * nb + b) * 8u, aw + 8u * b);
+}
+
+void or_block_dots_q6k(const uint32_t *qw, uint32_t rows, uint32_t nb, const uint8_t *xq, int32_t *out) {
+  const u32 *aw = (const u32 *)xq;
+  for (size_t r = 0; r < rows; r++)
+    for (u32 b = 0; b < nb; b++)
+      for (u32 h = 0; h < 2; h++)
+        out[(r * nb + b) * 2u + h] =
+            (int32_t)q6k_half(qw + (r * nb + b) * 4u, qw[(size_t)rows * nb * 4u + (r * nb + b) * 2u + h], aw + 8u * b, h);
+}
+
 /* Nibble j (< 32) of block/sub-block b of row r, straight from the GGUF bytes. */
 static u32 gguf_nib(int kind, const uint8_t *src, u32 r, u32 b, u32 j, u32 nb) {
   if (kind == 2) {
@@ -206,12 +302,16 @@ void or_block_dots_gguf(int kind, const uint8_t *src, uint32_t rows, uint32_t nb
   const int8_t *qa = (const int8_t *)xq;
   for (u32 r = 0; r < rows; r++)
     for (u32 b = 0; b < nb; b++) {
-      int64_t s = 0;
+      int64_t s[2] = {0, 0};
       for (u32 j = 0; j < 32; j++) {
-        const int64_t q = (int64_t)gguf_nib(kind, src, r, b, j, nb) - (kind == 2 ? 8 : 0);
-        s += q * qa[32u * (size_t)b + j];
+        int64_t q;
+        if (kind == 8) q = (int8_t)src[((size_t)r * nb + b) * 34u + 2u + j];
+        else if (kind == 14) q = (int64_t)q6k_q(src + ((size_t)r * (nb / 8u) + b / 8u) * 210u, 32u * (b % 8u) + j) - 32;
+        else q = (int64_t)gguf_nib(kind, src, r, b, j, nb) - (kind == 2 ? 8 : 0);
+        s[j / 16u] += q * qa[32u * (size_t)b + j];
       }
-      out[(size_t)r * nb + b] = (int32_t)s;
+      if (kind == 14) out[((size_t)r * nb + b) * 2u] = (int32_t)s[0], out[((size_t)r * nb + b) * 2u + 1u] = (int32_t)s[1];
+      else out[(size_t)r * nb + b] = (int32_t)(s[0] + s[1]);
     }
 }
 
@@ -269,6 +369,57 @@ static void gemv_q4k_rows(const uint32_t *qw, const uint16_t *qs, uint32_t rows,
   }
 }
 
+static void gemv_q8_rows(const uint32_t *qw, const uint16_t *qs, uint32_t r0, uint32_t r1, uint32_t nb, const uint8_t *xq, float *y) {
+  const u32 *aw = (const u32 *)xq;
+  const float *da = (const float *)(xq + 32u * (size_t)nb);
+  for (u32 r = r0; r < r1; r++) {
+    float lane[32];
+    for (u32 l = 0; l < 32; l++) {
+      float acc = 0.0f;
+      for (u32 b = l; b < nb; b += 32) {
+        const int32_t dot = (int32_t)q8q8_block(qw + ((size_t)r * nb + b) * 8u, aw + 8u * b);
+        const float dw = or_f16_to_f32(qs[(size_t)r * nb + b]);
+        const float sc = dw * da[b];
+        acc = acc + sc * (float)dot; /* src/cpu.c:168 */
+      }
+      lane[l] = acc;
+    }
+    y[r] = tree32(lane);
+  }
+}
+
+static void gemv_q6k_rows(const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32_t r0, uint32_t r1, uint32_t nb, const uint8_t *xq,
+                          float *y) {
+  const u32 *aw = (const u32 *)xq;
+  const float *da = (const float *)(xq + 32u * (size_t)nb);
+  for (u32 r = r0; r < r1; r++) {
+    float lane[32];
+    for (u32 l = 0; l < 32; l++) {
+      float acc = 0.0f;
+      for (u32 b = l; b < nb; b += 32) {
+        const size_t i = (size_t)r * nb + b;
+        const u32 *hw = qw + (size_t)rows * nb * 4u + i * 2u;
+        const int d0 = (int)q6k_half(qw + i * 4u, hw[0], aw + 8u * b, 0);
+        const int d1 = (int)q6k_half(qw + i * 4u, hw[1], aw + 8u * b, 1);
+        const u32 sc = qs[i];
+        const float d = or_f16_to_f32(qs[(size_t)rows * nb + (size_t)r * (nb / 8u) + b / 8u]);
+        const float s0 = d * (float)(int8_t)(sc & 255u), s1 = d * (float)(int8_t)(sc >> 8);
+        acc = fmaf(fmaf(s1, (float)d1, s0 * (float)d0), da[b], acc); /* src/cpu.c:142 */
+      }
+      lane[l] = acc;
+    }
+    y[r] = tree32(lane);
+  }
+}
+
+void or_gemv_q8(const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32_t nb, const uint8_t *xq, float *y) {
+  gemv_q8_rows(qw, qs, 0, rows, nb, xq, y);
+}
+
+void or_gemv_q6k(const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32_t nb, const uint8_t *xq, float *y) {
+  gemv_q6k_rows(qw, qs, rows, 0, rows, nb, xq, y);
+}
+
 void or_gemv_q4(const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32_t nb, const uint8_t *xq, float *y) {
   gemv_q4_rows(qw, qs, 0, rows, nb, xq, y);
 }
@@ -291,7 +442,15 @@ void or_epilogue(float *y, uint32_t rows, const float *bias, const float *res) {
 void or_dequant(int kind, const uint8_t *src, uint64_t first, uint64_t n, float *out) {
   for (uint64_t i = 0; i < n; i++) {
     const uint64_t e = first + i;
-    if (kind == 2) { /* src/model.c:98-107 */
+    if (kind == 8) { /* src/model.c:89-97 */
+      const uint8_t *blk = src + e / 32 * 34;
+      out[i] = or_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8))) * (float)(int8_t)blk[2 + e % 32];
+    } else if (kind == 14) { /* src/model.c:108-140: d * sc[e / 16] * (q - 32) */
+      const uint8_t *blk = src + e / 256 * 210;
+      const u32 k = (u32)(e % 256);
+      const float d = or_f16_to_f32((uint16_t)(blk[208] | (blk[209] << 8)));
+      out[i] = d * (float)(int8_t)blk[192 + k / 16] * (float)((int)q6k_q(blk, k) - 32);
+    } else if (kind == 2) { /* src/model.c:98-107 */
       const uint8_t *blk = src + e / 32 * 18;
       const u32 j = (u32)(e % 32), q = j < 16 ? (blk[2 + j] & 15u) : (u32)(blk[2 + j - 16] >> 4);
       out[i] = or_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8))) * (float)((int)q - 8);
@@ -336,23 +495,27 @@ typedef struct {
   uint32_t rows, r0, r1, nb;
   const uint8_t *xq;
   float *y;
-  int k4;
+  int kind; /* 0 Q4_0, 2 Q8_0, 3 Q4_K, 4 Q6_K */
 } job;
 
 static void *run_job(void *p) {
   const job *j = p;
-  if (j->k4) gemv_q4k_rows(j->qw, j->qs, j->rows, j->r0, j->r1, j->nb, j->xq, j->y);
-  else gemv_q4_rows(j->qw, j->qs, j->r0, j->r1, j->nb, j->xq, j->y);
+  switch (j->kind) {
+    case 3: gemv_q4k_rows(j->qw, j->qs, j->rows, j->r0, j->r1, j->nb, j->xq, j->y); break;
+    case 4: gemv_q6k_rows(j->qw, j->qs, j->rows, j->r0, j->r1, j->nb, j->xq, j->y); break;
+    case 2: gemv_q8_rows(j->qw, j->qs, j->r0, j->r1, j->nb, j->xq, j->y); break;
+    default: gemv_q4_rows(j->qw, j->qs, j->r0, j->r1, j->nb, j->xq, j->y);
+  }
   return NULL;
 }
 
-static void gemv_mt(int k4, const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32_t nb, const uint8_t *xq, float *y, int nt) {
+static void gemv_mt(int kind, const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32_t nb, const uint8_t *xq, float *y, int nt) {
   if (nt < 1) nt = 1;
   if (nt > 256) nt = 256;
   pthread_t th[256];
   job jb[256];
   for (int i = 0; i < nt; i++) {
-    jb[i] = (job){qw, qs, rows, (u32)((uint64_t)rows * i / nt), (u32)((uint64_t)rows * (i + 1) / nt), nb, xq, y, k4};
+    jb[i] = (job){qw, qs, rows, (u32)((uint64_t)rows * i / nt), (u32)((uint64_t)rows * (i + 1) / nt), nb, xq, y, kind};
     if (i > 0) pthread_create(&th[i], NULL, run_job, &jb[i]);
   }
   run_job(&jb[0]);
@@ -363,5 +526,11 @@ void or_gemv_q4_mt(const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32
   gemv_mt(0, qw, qs, rows, nb, xq, y, nthreads);
 }
 void or_gemv_q4k_mt(const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32_t nb, const uint8_t *xq, float *y, int nthreads) {
-  gemv_mt(1, qw, qs, rows, nb, xq, y, nthreads);
+  gemv_mt(3, qw, qs, rows, nb, xq, y, nthreads);
+}
+void or_gemv_q8_mt(const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32_t nb, const uint8_t *xq, float *y, int nthreads) {
+  gemv_mt(2, qw, qs, rows, nb, xq, y, nthreads);
+}
+void or_gemv_q6k_mt(const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32_t nb, const uint8_t *xq, float *y, int nthreads) {
+  gemv_mt(4, qw, qs, rows, nb, xq, y, nthreads);
 }

@@ -15,7 +15,15 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-GGML_Q4_0, GGML_Q4_K = 2, 12
+GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 2, 8, 12, 14
+# words of qw per 32-weight block in the reference layouts
+_QW_PER = {GGML_Q4_0: 4, GGML_Q8_0: 8, GGML_Q4_K: 4, GGML_Q6_K: 6}
+
+
+def qs_len(kind, rows, nb):
+    """u16 entries of qs in the reference layouts (src/model.c:356-362)."""
+    extra = {GGML_Q4_K: rows * (nb // 8) * 2, GGML_Q6_K: rows * (nb // 8)}.get(kind, 0)
+    return rows * nb + extra
 
 _P = C.c_void_p
 _U32 = C.c_uint32
@@ -36,14 +44,14 @@ class Oracle:
         L.or_f32_to_f16.restype = C.c_uint16
         L.or_f32_to_f16.argtypes = [C.c_float]
         L.or_quant_q8.argtypes = [_P, _P, _U32]
-        for f in (L.or_repack_q4, L.or_repack_q4k):
+        for f in (L.or_repack_q4, L.or_repack_q4k, L.or_repack_q8, L.or_repack_q6k):
             f.argtypes = [_P, _U32, _U32, _P, _P]
-        for f in (L.or_gemv_q4, L.or_gemv_q4k):
+        for f in (L.or_gemv_q4, L.or_gemv_q4k, L.or_gemv_q8, L.or_gemv_q6k):
             f.argtypes = [_P, _P, _U32, _U32, _P, _P]
-        for f in (L.or_gemv_q4_mt, L.or_gemv_q4k_mt):
+        for f in (L.or_gemv_q4_mt, L.or_gemv_q4k_mt, L.or_gemv_q8_mt, L.or_gemv_q6k_mt):
             f.argtypes = [_P, _P, _U32, _U32, _P, _P, C.c_int]
         L.or_epilogue.argtypes = [_P, _U32, _P, _P]
-        for f in (L.or_block_dots_q4, L.or_block_dots_q4k):
+        for f in (L.or_block_dots_q4, L.or_block_dots_q4k, L.or_block_dots_q8, L.or_block_dots_q6k):
             f.argtypes = [_P, _U32, _U32, _P, _P]
         L.or_block_dots_gguf.argtypes = [C.c_int, _P, _U32, _U32, _P, _P]
         L.or_dequant.argtypes = [C.c_int, _P, C.c_uint64, C.c_uint64, _P]
@@ -85,27 +93,27 @@ class Oracle:
         return a
 
     # -- repack to the reference layouts
+    _SUF = {GGML_Q4_0: "q4", GGML_Q8_0: "q8", GGML_Q4_K: "q4k", GGML_Q6_K: "q6k"}
+
+    def _fn(self, stem, kind):
+        return getattr(self.lib, f"or_{stem}_{self._SUF[kind]}")
+
     def repack(self, kind, src, rows, nb):
+        """GGUF bytes -> the reference's (qw, qs) (src/model.c:205-292)."""
         src = np.ascontiguousarray(src, dtype=np.uint8)
-        qw = np.zeros(rows * nb * 4, dtype=np.uint32)
-        if kind == GGML_Q4_0:
-            qs = np.zeros(rows * nb, dtype=np.uint16)
-            self.lib.or_repack_q4(_ptr(src), rows, nb, _ptr(qw), _ptr(qs))
-        else:
-            qs = np.zeros(self.lib.or_q4k_qs_n(rows, nb), dtype=np.uint16)
-            self.lib.or_repack_q4k(_ptr(src), rows, nb, _ptr(qw), _ptr(qs))
+        qw = np.zeros(rows * nb * _QW_PER[kind], dtype=np.uint32)
+        qs = np.zeros(qs_len(kind, rows, nb), dtype=np.uint16)
+        self._fn("repack", kind)(_ptr(src), rows, nb, _ptr(qw), _ptr(qs))
         return qw, qs
 
     def gemv(self, kind, qw, qs, rows, nb, xq, threads=1):
-        """y = W x in the reference's order, bit for bit (src/cpu.c:64-118)."""
+        """y = W x in the reference's order, bit for bit (src/cpu.c:64-175)."""
         xq = np.ascontiguousarray(xq, dtype=np.uint8)
         y = np.zeros(rows, dtype=np.float32)
         if threads > 1:
-            f = self.lib.or_gemv_q4_mt if kind == GGML_Q4_0 else self.lib.or_gemv_q4k_mt
-            f(_ptr(qw), _ptr(qs), rows, nb, _ptr(xq), _ptr(y), threads)
+            getattr(self.lib, f"or_gemv_{self._SUF[kind]}_mt")(_ptr(qw), _ptr(qs), rows, nb, _ptr(xq), _ptr(y), threads)
         else:
-            f = self.lib.or_gemv_q4 if kind == GGML_Q4_0 else self.lib.or_gemv_q4k
-            f(_ptr(qw), _ptr(qs), rows, nb, _ptr(xq), _ptr(y))
+            self._fn("gemv", kind)(_ptr(qw), _ptr(qs), rows, nb, _ptr(xq), _ptr(y))
         return y
 
     def epilogue(self, y, bias=None, res=None):
@@ -116,15 +124,17 @@ class Oracle:
         return y
 
     def block_dots(self, kind, qw, rows, nb, xq):
-        out = np.zeros(rows * nb, dtype=np.int32)
-        f = self.lib.or_block_dots_q4 if kind == GGML_Q4_0 else self.lib.or_block_dots_q4k
-        f(_ptr(qw), rows, nb, _ptr(np.ascontiguousarray(xq)), _ptr(out))
-        return out.reshape(rows, nb)
+        """int32 [rows, nb] block dots; Q6_K: [rows, nb, 2] half dots."""
+        h = 2 if kind == GGML_Q6_K else 1
+        out = np.zeros(rows * nb * h, dtype=np.int32)
+        self._fn("block_dots", kind)(_ptr(qw), rows, nb, _ptr(np.ascontiguousarray(xq)), _ptr(out))
+        return out.reshape((rows, nb, 2) if h == 2 else (rows, nb))
 
     def block_dots_gguf(self, kind, src, rows, nb, xq):
-        out = np.zeros(rows * nb, dtype=np.int32)
+        h = 2 if kind == GGML_Q6_K else 1
+        out = np.zeros(rows * nb * h, dtype=np.int32)
         self.lib.or_block_dots_gguf(kind, _ptr(np.ascontiguousarray(src)), rows, nb, _ptr(np.ascontiguousarray(xq)), _ptr(out))
-        return out.reshape(rows, nb)
+        return out.reshape((rows, nb, 2) if h == 2 else (rows, nb))
 
     def dequant(self, kind, src, n):
         out = np.zeros(n, dtype=np.float32)
@@ -178,7 +188,7 @@ class RefCPU:
         src = np.ascontiguousarray(src, dtype=np.uint8)
         h = self.lib.ref_mat_new(ttype, _ptr(src), rows, cols)
         if not h:
-            raise ValueError("not a MAT_Q4 / MAT_Q4K matrix")
+            raise ValueError("not a MAT_Q4 / MAT_Q8 / MAT_Q4K / MAT_Q6K matrix")
         return RefMat(self, h, ttype, rows, cols // 32)
 
 
@@ -187,9 +197,8 @@ class RefMat:
         self.ref, self.h, self.ttype, self.rows, self.nb = ref, h, ttype, rows, nb
 
     def arrays(self):
-        qw = np.zeros(self.rows * self.nb * 4, dtype=np.uint32)
-        ns = self.rows * self.nb if self.ttype == GGML_Q4_0 else self.rows * self.nb + self.rows * (self.nb // 8) * 2
-        qs = np.zeros(ns, dtype=np.uint16)
+        qw = np.zeros(self.rows * self.nb * _QW_PER[self.ttype], dtype=np.uint32)
+        qs = np.zeros(qs_len(self.ttype, self.rows, self.nb), dtype=np.uint16)
         self.ref.lib.ref_mat_copy(self.h, _ptr(qw), _ptr(qs))
         return qw, qs
 

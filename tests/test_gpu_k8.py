@@ -1,0 +1,127 @@
+"""Parity of the Q8_0 and Q6_K decode GEMV (amdc_gemv_q8 / amdc_gemv_q6k and
+their multi-vector and f32-input forms, through the C ABI) with the oracle's
+restatement of cpu_gemv_q8 / cpu_gemv_q6k (hanw/amd.c src/cpu.c:120-175), on
+an MI355X. The same bar as the Q4 kinds: the per-block int32 dots (Q6_K: the
+two half dots of ie_q6k_dots) bit-exact against the oracle and an int64 brute
+force over the GGUF bytes; f32 outputs within 1e-5 of sum |terms| per row.
+"""
+import numpy as np
+import pytest
+
+from amdc import synth
+from test_gpu_parity import TOL, Case, rel_err, ttype
+
+pytestmark = pytest.mark.gpu
+Q8, Q6 = synth.KIND_Q8_0, synth.KIND_Q6_K
+
+
+@pytest.fixture(autouse=True)
+def _tuning_reset(dev):
+    dev.set_tuning()
+    yield
+    dev.set_tuning()
+
+
+@pytest.mark.parametrize("kind,rows,nb", [(Q8, 1, 1), (Q8, 7, 3), (Q8, 9, 11), (Q8, 13, 33), (Q8, 2, 511), (Q8, 5, 128),
+                                          (Q6, 1, 8), (Q6, 7, 16), (Q6, 9, 40), (Q6, 5, 72), (Q6, 3, 544)])
+def test_block_dots_bitexact(dev, orc, kind, rows, nb):
+    c = Case(dev, orc, kind, rows, nb, seed=rows * 31 + nb, xscale=3.0)
+    c.quant()
+    h = 2 if kind == Q6 else 1
+    out = dev.DevBuf(rows * nb * 4 * h)
+    dev.block_dots(kind, c.W, c.Q, out, rows, nb)
+    got = out.download(np.int32).reshape((rows, nb, 2) if h == 2 else (rows, nb))
+    assert np.array_equal(got, orc.block_dots(ttype(kind), c.qw, rows, nb, c.xq[0]))
+    assert np.array_equal(got, orc.block_dots_gguf(ttype(kind), c.src, rows, nb, c.xq[0]))
+
+
+SHAPES_Q8 = [(1, 1), (7, 3), (9, 11), (8, 32), (13, 33), (17, 36), (3, 100), (2, 511), (64, 128), (33, 344), (5, 3000)]
+SHAPES_Q6 = [(1, 8), (7, 16), (9, 40), (3, 64), (37, 160), (19, 544), (8, 192), (3, 1792)]
+
+
+@pytest.mark.parametrize("kind,rows,nb", [(Q8, r, n) for r, n in SHAPES_Q8] + [(Q6, r, n) for r, n in SHAPES_Q6])
+def test_gemv_t1(dev, orc, kind, rows, nb):
+    c = Case(dev, orc, kind, rows, nb, seed=rows + 100 * nb)
+    assert np.array_equal(c.quant()[0], c.xq[0])
+    dev.gemv(kind, c.W, c.Q, c.Y, rows, nb)
+    assert rel_err(c.y_gpu()[0], c.y_oracle(0), c.mag(0)) < TOL
+
+
+@pytest.mark.parametrize("lanes", [4, 8, 16, 32, 64])
+@pytest.mark.parametrize("wgs", [0, 3])
+@pytest.mark.parametrize("kind,rows,nb", [(Q8, 70, 344), (Q8, 33, 300), (Q6, 45, 160), (Q6, 6, 544)])
+def test_gemv_t1_tunings(dev, orc, kind, rows, nb, lanes, wgs):
+    c = Case(dev, orc, kind, rows, nb, seed=lanes + wgs)
+    c.quant()
+    dev.set_tuning(lanes, 0, wgs)
+    dev.gemv(kind, c.W, c.Q, c.Y, rows, nb)
+    assert rel_err(c.y_gpu()[0], c.y_oracle(0), c.mag(0)) < TOL
+
+
+@pytest.mark.parametrize("kind", [Q8, Q6])
+def test_gemv_epilogue_bias_res(dev, orc, kind):
+    rows, nb = 50, 64
+    c = Case(dev, orc, kind, rows, nb, seed=77)
+    c.quant()
+    g = np.random.default_rng(5)
+    bias, res = g.standard_normal(rows).astype(np.float32), g.standard_normal(rows).astype(np.float32)
+    B, R = dev.DevBuf.of(bias), dev.DevBuf.of(res)
+    for b, r in ((bias, res), (None, res), (bias, None)):
+        dev.gemv(kind, c.W, c.Q, c.Y, rows, nb, bias=None if b is None else B, res=None if r is None else R)
+        mag = c.mag(0) + (0 if b is None else np.abs(b)) + (0 if r is None else np.abs(r))
+        assert rel_err(c.y_gpu()[0], orc.epilogue(c.y_oracle(0), b, r), mag) < TOL
+
+
+@pytest.mark.parametrize("kind,rows,nb,T", [(Q8, 40, 128, 3), (Q8, 130, 43, 9), (Q6, 33, 160, 5), (Q6, 21, 544, 2)])
+def test_gemv_multi_and_dispatch(dev, orc, kind, rows, nb, T):
+    c = Case(dev, orc, kind, rows, nb, T, seed=T * 13 + nb)
+    assert np.array_equal(c.quant(), c.xq)
+    res = np.random.default_rng(T).standard_normal((T, rows)).astype(np.float32)
+    R = dev.DevBuf.of(res)
+    dev.gemv_t(kind, c.W, c.Q, c.Y, rows, nb, T, c.xs, rows, rows, res=R)
+    y = c.y_gpu()
+    for t in range(T):
+        assert rel_err(y[t], orc.epilogue(c.y_oracle(t), None, res[t]), c.mag(t) + np.abs(res[t])) < TOL, t
+    c.Y.fill(0)
+    dev.op_gemv(kind, c.W, c.Q, c.Y, rows, nb, T, c.xs, rows)
+    y = c.y_gpu()
+    for t in range(T):
+        assert rel_err(y[t], c.y_oracle(t), c.mag(t)) < TOL, t
+
+
+@pytest.mark.parametrize("kind,rows,nb", [(Q8, 70, 13), (Q8, 64, 344), (Q6, 45, 160)])
+def test_gemv_x_equals_quant_then_gemv(dev, orc, kind, rows, nb):
+    c = Case(dev, orc, kind, rows, nb, seed=rows + nb, xscale=2.0)
+    Q2, Y2 = dev.DevBuf(c.xs), dev.DevBuf(rows * 4)
+    dev.gemv_x(kind, c.W, c.X, Y2, rows, nb, q8=Q2)
+    assert np.array_equal(Q2.download(np.uint8)[:40 * nb], c.xq[0])
+    c.quant()
+    dev.gemv(kind, c.W, c.Q, c.Y, rows, nb)
+    assert np.array_equal(Y2.download(np.uint32), c.Y.download(np.uint32))
+    dev.gemv_x(kind, c.W, c.X, Y2, rows, nb)  # the library's workspace for the Q8 vector
+    assert np.array_equal(Y2.download(np.uint32), c.Y.download(np.uint32))
+
+
+@pytest.mark.parametrize("kind,rows,cols", [(Q8, 4096, 4096), (Q6, 5120, 17408), (Q6, 152064, 5120)])
+def test_gemv_full_size(dev, orc, kind, rows, cols):
+    """The shapes of real decode matrices (a Q8_0 attention projection, Q6_K ffn_down and lm_head of
+    the Q4_K_M configuration): every row within the bound, and a second run gives the same bits."""
+    nb = cols // 32
+    c = Case(dev, orc, kind, rows, nb, seed=3)
+    c.quant()
+    dev.gemv(kind, c.W, c.Q, c.Y, rows, nb)
+    first = c.Y.download(np.uint32)
+    assert rel_err(first.view(np.float32), c.y_oracle(0), c.mag(0)) < TOL
+    c.Y.fill(0)
+    dev.gemv(kind, c.W, c.Q, c.Y, rows, nb)
+    assert np.array_equal(c.Y.download(np.uint32), first)
+
+
+def test_errors_do_not_launch(dev, orc):
+    c = Case(dev, orc, Q6, 8, 16, seed=3)
+    with pytest.raises(dev.AmdcError):
+        dev.gemv_q6k(c.W, c.Q, c.Y, 8, 12)  # Q6_K nb % 8 != 0
+    with pytest.raises(dev.AmdcError):
+        dev.gemv_q8(c.W.ptr + 4, c.Q, c.Y, 8, 16)  # misaligned weights
+    with pytest.raises(dev.AmdcError):
+        dev.Chain([dev.chain_gemv(Q6, c.W, c.Q, c.Y, 8, 16)])  # the chain runs the Q4 kinds only

@@ -12,7 +12,6 @@ import numpy as np
 import pytest
 
 from amdc import synth
-from oracle import GGML_Q4_0, GGML_Q4_K
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -20,7 +19,7 @@ CPUS = min(16, os.cpu_count() or 1)
 
 
 def ttype(kind):
-    return GGML_Q4_K if kind == synth.KIND_Q4_K else GGML_Q4_0
+    return synth.GGML[kind]
 
 
 def q8_stride(nb):
