@@ -49,8 +49,9 @@ INT8_PEAK_TOPS = 5000.0
 ROTATE_BYTES = 2 << 30
 
 
-def wbytes(rows, cols):
-    return rows * (cols // 32) * 18
+def wbytes(rows, cols, kind=synth.KIND_Q4_0):
+    """GGUF weight bytes of a rows x cols matrix (the algorithmic bytes of one GEMV)."""
+    return synth.gguf_bytes(kind, rows, cols)
 
 
 def q8_stride(nb):
@@ -62,7 +63,7 @@ class Mats:
 
     def __init__(self, kind, shapes, seed, min_bytes=ROTATE_BYTES):
         self.kind, self.shapes = kind, shapes
-        self.set_bytes = sum(wbytes(r, c) for _, r, c in shapes)
+        self.set_bytes = sum(wbytes(r, c, kind) for _, r, c in shapes)
         self.copies = max(1, -(-min_bytes // self.set_bytes))
         host = [amdc.repack(kind, synth.gguf(kind, r, c, seed + i), r, c) for i, (_, r, c) in enumerate(shapes)]
         self.host = host
@@ -256,6 +257,28 @@ def prefill_set(steps, seed, timer):
     return out
 
 
+def k8_set(seed, timer):
+    """The Q8_0 and Q6_K decode GEMVs at the sizes they have in the c1 / c2 models (the Q6_K
+    matrices of a Q4_K_M file: ffn_down, attn_v, lm_head; Q8_0 projections): us per launch and the
+    GGUF weight bytes per second."""
+    out = {}
+    sets = [(synth.KIND_Q8_0, "q8_0_q", 4096, 4096), (synth.KIND_Q8_0, "q8_0_gate", 11008, 4096),
+            (synth.KIND_Q8_0, "q8_0_down", 4096, 11008), (synth.KIND_Q6_K, "q6_k_ffn_down", 5120, 17408),
+            (synth.KIND_Q6_K, "q6_k_attn_v", 1024, 5120), (synth.KIND_Q6_K, "q6_k_lm_head", 152064, 5120)]
+    for i, (kind, name, r, c) in enumerate(sets):
+        M = Mats(kind, [(name, r, c)], seed + i, min_bytes=1 << 30)
+        nb = c // 32
+        X = amdc.DevBuf.of(synth.activations(1, c, seed + 90 + i))
+        Q, Y = amdc.DevBuf(q8_stride(nb)), amdc.DevBuf(4 * r)
+        amdc.quant_q8(X, Q, nb)
+        t = timer.per_launch_ms(lambda j, s: amdc.gemv(kind, M.dev[j % M.copies][0], Q, Y, r, nb, stream=s), M.copies)
+        b = wbytes(r, c, kind)
+        out[name] = {"rows": r, "cols": c, "us": round(t * 1e3, 3), "GB/s": round(b / t / 1e6, 1),
+                     "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4)}
+        del M
+    return out
+
+
 # ---------------------------------------------------------------- CPU baseline
 
 def producers_set(timer):
@@ -365,6 +388,8 @@ def main():
         print(f"bench: c4 {json.dumps(detail['c4'])}", file=sys.stderr, flush=True)
         detail["producers"] = producers_set(timer)
         print(f"bench: producers {json.dumps(detail['producers'])}", file=sys.stderr, flush=True)
+        detail["q8_0_q6_k"] = k8_set(a.seed + 4000, timer)
+        print(f"bench: q8_0_q6_k {json.dumps(detail['q8_0_q6_k'])}", file=sys.stderr, flush=True)
     cpu = None
     if not a.quick and not a.no_cpu:
         cpu = cpu_baseline(a.seed)
