@@ -59,6 +59,8 @@ ABI = {
     "amdc_quant_q8": (C.c_int, [_P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_gemv_q4": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
     "amdc_gemv_q4k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
+    "amdc_gemm_q8": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
+    "amdc_gemm_q6k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_gemv_q8": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
     "amdc_gemv_q6k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
     "amdc_gemv_q8_x": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P, _P]),
@@ -346,6 +348,12 @@ def gemv_t(kind, w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, strea
 
 def gemm_q4k(w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stream=None):
     _check(lib().amdc_gemm_q4k(_p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), T, xs, ys, rs, stream))
+
+
+def gemm(kind, w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stream=None):
+    """The prefill GEMM of a Q4_K, Q8_0 or Q6_K matrix."""
+    f = getattr(lib(), "amdc_gemm_" + _SUF[kind])
+    _check(f(_p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), T, xs, ys, rs, stream))
 
 
 def op_gemv(kind, w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stream=None):

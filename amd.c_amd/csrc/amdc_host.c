@@ -256,6 +256,10 @@ enum {
   K_GEMV_Q6K_P2,
   K_DOTS_Q8,
   K_DOTS_Q6K,
+  K_GEMMH_Q8_N128,
+  K_GEMMH_Q8_N64,
+  K_GEMMH_Q6K_N128,
+  K_GEMMH_Q6K_N64,
   K_N
 };
 static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1",  "amdc_gemv_q4_k_t1",  "amdc_gemv_q4_0_t1u1",
@@ -266,7 +270,8 @@ static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1
                                        "amdc_gemm_reduce",    "amdc_gemv_q4_0_v8",  "amdc_gemv_q4_k_v8",
                                        "amdc_gemv_q4_0_x1",   "amdc_gemv_q4_k_x1",  "amdc_gemv_q4_0_p2",  "amdc_gemv_q4_k_p2",
                                        "amdc_chain",          "amdc_rmsnorm_q8",    "amdc_swiglu_q8",     "amdc_gemv_q8_0_p2",
-                                       "amdc_gemv_q6_k_p2",   "amdc_dots_q8_0",     "amdc_dots_q6_k"};
+                                       "amdc_gemv_q6_k_p2",   "amdc_dots_q8_0",     "amdc_dots_q6_k",     "amdc_gemmh_q8_0_m64_n128",
+                                       "amdc_gemmh_q8_0_m64_n64", "amdc_gemmh_q6_k_m64_n128", "amdc_gemmh_q6_k_m64_n64"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -800,15 +805,16 @@ static const struct {
   u32 mr, nt, threads;
 } gh[2] = {{K_GEMMH_M64_N128, 64, 128, 256}, {K_GEMMH_M64_N64, 64, 64, 256}};
 
-int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
-                  uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+/* The prefill GEMM of a kind with an f16-MFMA kernel (Q4_K, Q8_0, Q6_K). */
+static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
+                       const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
   NEED_OPEN();
-  int rc = check_mat("gemm_q4k", AMDC_KIND_Q4_K, w, xq, y, rows, nb);
-  if (!rc) rc = check_t("gemm_q4k", nb, rows, T, xs, ys, rs, res);
+  int rc = check_mat(op, kind, w, xq, y, rows, nb);
+  if (!rc) rc = check_t(op, nb, rows, T, xs, ys, rs, res);
   if (rc) return rc;
   if (T == 1u) xs = 40u * nb, ys = rows, rs = rows; /* one row: the strides are not used */
-  if (xs % 16u) return fail(AMDC_EINVAL, "gemm_q4k: xs %u not a multiple of 16", xs);
-  if (t_gemm == 1 || t_gemm == 2) { /* the int8-MFMA kernel */
+  if (xs % 16u) return fail(AMDC_EINVAL, "%s: xs %u not a multiple of 16", op, xs);
+  if (kind == AMDC_KIND_Q4_K && (t_gemm == 1 || t_gemm == 2)) { /* the int8-MFMA kernel */
     const u32 n = t_gemm == 2 ? 128u : 64u;
     const u64 grid = (u64)((rows + 63u) / 64u) * ((T + n - 1u) / n);
     if (grid > 0x7FFFFFFFull) return fail(AMDC_EINVAL, "gemm_q4k: grid too large");
@@ -818,7 +824,7 @@ int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uin
   /* the f16-MFMA kernel: 128 tokens per workgroup when there are that many;
    * the K split doubles until the workgroups number three per CU (measured
    * best on the c4 shapes: 17408 x 5120 split 2, 5120 x 17408 split 8) */
-  const u32 ng = nb / 8u, cus = g_cus > 0 ? (u32)g_cus : 256u;
+  const u32 ng = amdc_ngroups(nb), cus = g_cus > 0 ? (u32)g_cus : 256u;
   const int v = t_gemm >= 3 ? t_gemm - 3 : (T > 64u ? 0 : 1);
   u32 ks = t_ksplit > 0 ? (u32)t_ksplit : 0u;
   if (!ks) {
@@ -838,15 +844,33 @@ int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uin
   rc = launch(K_Q8_PREP, (unsigned)((np + 255u) / 256u), 1, 0, stream, pa);
   if (rc) return rc;
   const u64 grid = (u64)((rows + gh[v].mr - 1u) / gh[v].mr) * ((T + gh[v].nt - 1u) / gh[v].nt);
-  if (grid > 0x7FFFFFFFull) return fail(AMDC_EINVAL, "gemm_q4k: grid too large");
+  if (grid > 0x7FFFFFFFull) return fail(AMDC_EINVAL, "%s: grid too large", op);
   void *ga[] = {&w, &xh, &da, &xa, &y, &rows, &nb, &bias, &res, &T, (void *)&Tp, &ys, &rs, &part};
-  HIPCALL(H.ModuleLaunchKernel(g_k[gh[v].k], (unsigned)grid, ks, 1, gh[v].threads, 1, 1, 0, stream, ga, NULL));
+  const int kk = kind == AMDC_KIND_Q8_0 ? (v ? K_GEMMH_Q8_N64 : K_GEMMH_Q8_N128)
+                 : kind == AMDC_KIND_Q6_K ? (v ? K_GEMMH_Q6K_N64 : K_GEMMH_Q6K_N128)
+                                          : gh[v].k;
+  HIPCALL(H.ModuleLaunchKernel(g_k[kk], (unsigned)grid, ks, 1, gh[v].threads, 1, 1, 0, stream, ga, NULL));
   if (ks > 1u) {
     const u64 n = (u64)rows * T;
     void *ra[] = {&part, &ks, &y, &rows, &T, &bias, &res, &ys, &rs};
     return launch(K_GEMM_REDUCE, (unsigned)((n + 255u) / 256u), 1, 0, stream, ra);
   }
   return AMDC_OK;
+}
+
+int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                  uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  return gemm_launch(AMDC_KIND_Q4_K, "gemm_q4k", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+}
+
+int amdc_gemm_q8(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                 uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  return gemm_launch(AMDC_KIND_Q8_0, "gemm_q8", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+}
+
+int amdc_gemm_q6k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                  uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  return gemm_launch(AMDC_KIND_Q6_K, "gemm_q6k", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
 }
 
 int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
@@ -856,7 +880,7 @@ int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t 
     int rc = check_mat("op_gemv", kind, w, xq, y, rows, nb);
     return rc ? rc : gemv_launch(kind, w, xq, y, rows, nb, bias, res, 1, 0, 0, 0, stream);
   }
-  if (kind == AMDC_KIND_Q4_K && (int)T >= t_gemm_min && nb % 8u == 0u) return amdc_gemm_q4k(w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+  if (kind != AMDC_KIND_Q4_0 && (int)T >= t_gemm_min) return gemm_launch(kind, "op_gemv", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
   return gemv_t(kind, "op_gemv", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
 }
 

@@ -1233,6 +1233,44 @@ __device__ __forceinline__ h8 a_frag(u32 w0, u32 w1, u32 h, _Float16 sc) {
   return (h8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
+// The A operand of a Q8_0 block tile: lane (row i, h) holds weights
+// 8h..8h+7, the int8 bytes w0, w1 (plane h >> 1, bytes 8 (h & 1) ..) as f16:
+// byte ^ 0x80 = w + 128 in the mantissa of 1024, then - 1152 (exact).
+__device__ __forceinline__ h8 a_frag_q8(u32 w0, u32 w1) {
+  h2 p0, p1, p2, p3;
+  nib_to_h(w0 ^ 0x80808080u, p0, p1);
+  nib_to_h(w1 ^ 0x80808080u, p2, p3);
+  const h2 c = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  p0 += c, p1 += c, p2 += c, p3 += c;
+  return (h8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// The A operands of a Q6_K sub-block tile: lane (row i, h) holds weights
+// 8h..8h+7, of half h >> 1, as (q - 32) sc split into hi = (q - 32) 16 (sc >> 4)
+// and lo = (q - 32) (sc & 15), both exact in f16 (|.| <= 4096, multiples of
+// 16; |.| <= 480), so that the two MFMAs add the integer (q - 32) sc a exactly
+// (every partial sum stays under 128 * 32 * 32 * 127 < 2^24). w0, w1: nibble
+// bytes 8 (h & 1) .. + 7 (the low 4 bits of the half's weights in the low
+// nibble for h < 2, else the high); hw: the half's high-bit word (weight
+// 4i + e at bits 8e + 2i, i = 2 (h & 1) for w0's weights, + 1 for w1's).
+__device__ __forceinline__ void a_frag_q6(u32 w0, u32 w1, u32 hw, u32 h, int sc, h8 &ahi, h8 &alo) {
+  const u32 sft = (h >> 1) * 4u, hs = 4u * (h & 1u);
+  const u32 q0 = ((w0 >> sft) & 0x0F0F0F0Fu) | (((hw >> hs) & 0x03030303u) << 4);
+  const u32 q1 = ((w1 >> sft) & 0x0F0F0F0Fu) | (((hw >> (hs + 2u)) & 0x03030303u) << 4);
+  h2 p[4];
+  nib_to_h(q0, p[0], p[1]);
+  nib_to_h(q1, p[2], p[3]);
+  const _Float16 fl = (_Float16)(float)(sc & 15), fh = (_Float16)(float)(sc - (sc & 15));
+  const h2 c = {(_Float16)-1056.0f, (_Float16)-1056.0f}, l2 = {fl, fl}, h2v = {fh, fh};
+#pragma unroll
+  for (u32 m = 0; m < 4u; m++) p[m] += c; // q - 32, exact
+  h2 hi[4], lo[4];
+#pragma unroll
+  for (u32 m = 0; m < 4u; m++) hi[m] = p[m] * h2v, lo[m] = p[m] * l2;
+  ahi = (h8){hi[0][0], hi[0][1], hi[1][0], hi[1][1], hi[2][0], hi[2][1], hi[3][0], hi[3][1]};
+  alo = (h8){lo[0][0], lo[0][1], lo[1][0], lo[1][1], lo[2][0], lo[2][1], lo[3][0], lo[3][1]};
+}
+
 // Y[t][r] for Q4_K weights and T tokens (the arguments of ie_gemm_q4kr plus the
 // prepared activations of amdc_q8_prep): per sub-block b of super-block g
 //   X_rtb = sum_k (q sc)_rk a_tk          v_mfma_f32_16x16x32_f16, exact
@@ -1253,7 +1291,7 @@ __device__ __forceinline__ h8 a_frag(u32 w0, u32 w1, u32 h, _Float16 sc) {
 // Inside a block all MFMAs are issued before their results are used.
 // Split K (gridDim.y > 1): super-blocks [g0, g1) per split; the partial sums
 // go to part[split][t][r] and amdc_gemm_reduce adds them in split order.
-template <int NJ>
+template <int NJ, int KIND>
 __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const _Float16 *__restrict__ xh, const float *__restrict__ DA,
                                            const float *__restrict__ XA, float *__restrict__ y, u32 rows, u32 nb,
                                            const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 Tp, u32 ys, u32 rs,
@@ -1263,12 +1301,12 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
   __shared__ __attribute__((aligned(16))) _Float16 sb[2][NTT * BSTR];
   __shared__ __attribute__((aligned(16))) float sda[2][2][NTT];
   __shared__ __attribute__((aligned(16))) float sxa[2][8][NTT]; // d_a asum of a super-block's 8 blocks, by parity
-  const u32 ng = nb >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6, wm = w & 1u, wn = w >> 1;
+  const u32 ng = KIND == AMDC_Q8_0 ? amdc_ngroups(nb) : nb >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6, wm = w & 1u, wn = w >> 1;
   const u32 i16 = lane & 15u, h = lane >> 4;
   const u32 ntt = (T + NTT - 1u) / NTT, tt = blockIdx.x % ntt, rt = blockIdx.x / ntt;
   const u32 tbase = tt * NTT, twave = 16u * NJ * wn;
   const u32 ks = blockIdx.y, nks = gridDim.y, g0 = ng * ks / nks, g1 = ng * (ks + 1u) / nks;
-  const u32 RB = (u32)amdc_row_bytes(nb), K2 = 64u * nb; // bytes per weight row, per activation row
+  const u32 RB = (u32)amdc_row_bytes_k(KIND, nb), K2 = 64u * nb; // bytes per weight row, per activation row
   // uniform bases (buffer resources), 32-bit lane offsets
   const uint8_t *wbase = W + (u64)rt * MR * RB;
   const __amdgpu_buffer_rsrc_t rw = rsrc(wbase, (u32)min((u64)(rows - rt * MR) * RB, (u64)0xFFFFFFF0u));
@@ -1317,62 +1355,106 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
       sxa[(s >> 2) & 1u][2u * (s & 3u) + tid / NTT][tid % NTT] = rxv; // the next super-block writes the other half
     }
   };
-  auto load_w = [&](u32 s, u32 (&wv)[2][2][2]) { // the lane's 8 nibble bytes, 2 blocks x 2 row tiles
+  // the lane's 8 weight bytes (nibbles, or int8), 2 blocks x 2 row tiles, and
+  // for Q6_K the high-bit word of its half
+  auto load_w = [&](u32 s, u32 (&wv)[2][2][3]) {
     const u32 g = s >> 2, kb = 2u * (s & 3u);
 #pragma unroll
     for (u32 bb = 0; bb < 2u; bb++) {
-      const u32 so = (u32)amdc_nib_off(ng, g, kb + bb);
+      const u32 k = kb + bb;
+      const u32 so = KIND == AMDC_Q8_0   ? (u32)amdc_q8_off(ng, g, 2u * k + (h >> 1))
+                     : KIND == AMDC_Q6_K ? (u32)amdc_q6k_nib_off(ng, g, k)
+                                         : (u32)amdc_nib_off(ng, g, k);
 #pragma unroll
       for (u32 i = 0; i < 2u; i++) {
         const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rw, wo[i] + 8u * (h & 1u), so, 0);
         wv[bb][i][0] = v.x, wv[bb][i][1] = v.y;
+        if constexpr (KIND == AMDC_Q6_K)
+          wv[bb][i][2] = __builtin_amdgcn_raw_buffer_load_b32(rw, wo[i] + 4u * (h >> 1), (u32)amdc_q6k_hi_off(ng, g, k >> 1) + 8u * (k & 1u), 0);
       }
     }
   };
-  u32x4 hd[2];
+  u32x4 hd[2]; // the super-group header of the lane's A rows (scales; Q8_0: the 8 d)
+  u32 hdd[2];  // Q6_K: f16 d
   auto load_h = [&](u32 g) {
 #pragma unroll
-    for (u32 i = 0; i < 2u; i++) hd[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo[i], 16u * g, 0);
+    for (u32 i = 0; i < 2u; i++) {
+      hd[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo[i], 16u * g, 0);
+      if constexpr (KIND == AMDC_Q6_K) hdd[i] = __builtin_amdgcn_raw_buffer_load_b16(rw, wo[i], 16u * ng + 2u * g, 0);
+    }
   };
 
   // one stage: the MFMAs and fmas of blocks kb, kb + 1 of the super-block (kb
   // a constant) from LDS buffer bf and the nibbles wv
-  auto compute = [&](u32 kb, u32 bf, const u32(&wv)[2][2][2]) {
+  // the A operands of block k from its weight words (Q6_K: two, hi and lo)
+  auto frag = [&](const u32(&wk)[3], u32 i, u32 k, h8 &a0, h8 &a1) {
+    if constexpr (KIND == AMDC_Q8_0) {
+      a0 = a_frag_q8(wk[0], wk[1]);
+    } else if constexpr (KIND == AMDC_Q6_K) {
+      const int sc = (int)(int8_t)(hword(hd[i], k >> 1) >> (16u * (k & 1u) + 8u * (h >> 1)));
+      a_frag_q6(wk[0], wk[1], wk[2], h, sc, a0, a1);
+    } else {
+      a0 = a_frag(wk[0], wk[1], h, (_Float16)(float)q4k_sc(hd[i], k));
+    }
+  };
+  auto compute = [&](u32 kb, u32 bf, const u32(&wv)[2][2][3]) {
     const _Float16 *lb = &sb[bf][(twave + i16) * BSTR + 8u * h];
     h8 bq[NJ];
 #pragma unroll
     for (u32 j = 0; j < NJ; j++) bq[j] = *(const h8 *)(lb + 16u * j * BSTR);
-    h8 af[2];
+    h8 af[2], al[2];
 #pragma unroll
-    for (u32 i = 0; i < 2u; i++) af[i] = a_frag(wv[0][i][0], wv[0][i][1], h, (_Float16)(float)q4k_sc(hd[i], kb));
+    for (u32 i = 0; i < 2u; i++) frag(wv[0][i], i, kb, af[i], al[i]);
 #pragma unroll
     for (u32 bb = 0; bb < 2u; bb++) {
       float dj[NJ];
 #pragma unroll
       for (u32 j = 0; j < NJ; j++) dj[j] = sda[bf][bb][twave + 16u * j + i16];
+      float dw[2][4]; // Q8_0: the block's d of the C rows 4h + v of each row tile
+      if constexpr (KIND == AMDC_Q8_0) {
+#pragma unroll
+        for (u32 i = 0; i < 2u; i++) {
+          const float dr = h2f(hword(hd[i], (kb + bb) >> 1) >> (16u * ((kb + bb) & 1u)));
+#pragma unroll
+          for (u32 v = 0; v < 4u; v++) dw[i][v] = __shfl(dr, (int)(4u * h + v));
+        }
+      }
 #pragma unroll
       for (u32 i = 0; i < 2u; i++) { // a row tile at a time: NJ MFMAs in flight, then their fmas
         v4f x[NJ];
 #pragma unroll
-        for (u32 j = 0; j < NJ; j++) x[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bq[j], (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        for (u32 j = 0; j < NJ; j++) {
+          if constexpr (KIND == AMDC_Q6_K) {
+            x[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bq[j], (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            x[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bq[j], x[j], 0, 0, 0);
+          } else {
+            x[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bq[j], (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+          }
+        }
         if (bb == 0u && i == 1u) { // the second block's operands while the MFMAs run
 #pragma unroll
           for (u32 j = 0; j < NJ; j++) bq[j] = *(const h8 *)(lb + 16u * j * BSTR + 32u);
 #pragma unroll
-          for (u32 i2 = 0; i2 < 2u; i2++) af[i2] = a_frag(wv[1][i2][0], wv[1][i2][1], h, (_Float16)(float)q4k_sc(hd[i2], kb + 1u));
+          for (u32 i2 = 0; i2 < 2u; i2++) frag(wv[1][i2], i2, kb + 1u, af[i2], al[i2]);
         }
 #pragma unroll
         for (u32 j = 0; j < NJ; j++)
 #pragma unroll
-          for (u32 v = 0; v < 4u; v++) tmp[i][j][v] = __builtin_fmaf(dj[j], x[j][v], tmp[i][j][v]);
+          for (u32 v = 0; v < 4u; v++) {
+            if constexpr (KIND == AMDC_Q8_0) // (d_w d_a) dot, as src/cpu.c:168
+              acc[i][j][v] = __builtin_fmaf(dw[i][v] * dj[j], x[j][v], acc[i][j][v]);
+            else
+              tmp[i][j][v] = __builtin_fmaf(dj[j], x[j][v], tmp[i][j][v]);
+          }
       }
     }
   };
   // the end of a super-block: d, and the min term from the 8 blocks' d_a asum
   auto close_group = [&](u32 gp) {
+    if constexpr (KIND == AMDC_Q8_0) return;
 #pragma unroll
     for (u32 i = 0; i < 2u; i++) {
-      const float dmine = h2f(hd[i].x), dmn = h2f(hd[i].x >> 16);
+      const float dmine = KIND == AMDC_Q6_K ? h2f(hdd[i]) : h2f(hd[i].x), dmn = h2f(hd[i].x >> 16);
       float dv[4];
 #pragma unroll
       for (u32 v = 0; v < 4u; v++) dv[v] = __shfl(dmine, (int)(4u * h + v));
@@ -1384,9 +1466,11 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
 #pragma unroll
         for (u32 v = 0; v < 4u; v++) acc[i][j][v] = __builtin_fmaf(dv[v], tmp[i][j][v], acc[i][j][v]);
         tmp[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (KIND == AMDC_Q4_K) {
 #pragma unroll
-        for (u32 q = 0; q < 2u; q++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(am[q], sxa[gp][4u * q + h][twave + 16u * j + i16], acc[i][j], 0, 0, 0);
+          for (u32 q = 0; q < 2u; q++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(am[q], sxa[gp][4u * q + h][twave + 16u * j + i16], acc[i][j], 0, 0, 0);
+        }
       }
     }
   };
@@ -1395,7 +1479,7 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
   // wb); the activations and the nibbles of the next stage are in flight
   // during a stage
   const u32 s0 = 4u * g0, s1 = 4u * g1;
-  u32 wa[2][2][2], wb[2][2][2];
+  u32 wa[2][2][3], wb[2][2][3];
   if (s0 < s1) { // a split may own no super-block (then its partial sums are 0)
     fetch(s0);
     store(0, s0);
@@ -1444,14 +1528,18 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
     }
 }
 
-#define GEMMH_KERNEL(NAME, NJ)                                                                                                     \
+#define GEMMH_KERNEL(NAME, NJ, KIND)                                                                                               \
   extern "C" __global__ __launch_bounds__(256) void NAME(const uint8_t *W, const _Float16 *xh, const float *DA, const float *XA,  \
                                                          float *y, u32 rows, u32 nb, const float *bias, const float *res, u32 T,  \
                                                          u32 Tp, u32 ys, u32 rs, float *part) {                                   \
-    gemmh_body<NJ>(W, xh, DA, XA, y, rows, nb, bias, res, T, Tp, ys, rs, part);                                                   \
+    gemmh_body<NJ, KIND>(W, xh, DA, XA, y, rows, nb, bias, res, T, Tp, ys, rs, part);                                             \
   }
-GEMMH_KERNEL(amdc_gemmh_m64_n128, 4)
-GEMMH_KERNEL(amdc_gemmh_m64_n64, 2)
+GEMMH_KERNEL(amdc_gemmh_m64_n128, 4, AMDC_Q4_K)
+GEMMH_KERNEL(amdc_gemmh_m64_n64, 2, AMDC_Q4_K)
+GEMMH_KERNEL(amdc_gemmh_q8_0_m64_n128, 4, AMDC_Q8_0)
+GEMMH_KERNEL(amdc_gemmh_q8_0_m64_n64, 2, AMDC_Q8_0)
+GEMMH_KERNEL(amdc_gemmh_q6_k_m64_n128, 4, AMDC_Q6_K)
+GEMMH_KERNEL(amdc_gemmh_q6_k_m64_n64, 2, AMDC_Q6_K)
 
 // The split-K sums: y[t][r] = part[0][t][r] + part[1][t][r] + ... (in split
 // order), then the epilogue. All nks (<= 16) loads are issued before the

@@ -194,10 +194,23 @@ int amdc_gemv_q6k_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, u
  * (call once outside graph capture before capturing). */
 int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                   uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
+/* The same for Q8_0 and Q6_K matrices: replace ie_gemm_q8r / ie_gemm_q8
+ * (kernels/ie_kernels.c:1018, 1166; src/hip.c:1040-1056) and ie_gemm_q6kr
+ * (kernels/ie_kernels.c:2015; src/hip.c:938-944). Q8_0: the integer block
+ * sums exact on the f16 MFMA (int8 weights are f16 integers), then
+ * (d_w d_a) sum per block as src/cpu.c:168. Q6_K: (q - 32) sc split into two
+ * exact f16 operands (16 (sc >> 4) and sc & 15 parts), so that the sums
+ * (q - 32) sc a of a sub-block are exact, then d d_a per sub-block. f32 outputs
+ * within 1e-5 of cpu_gemv_q8 / cpu_gemv_q6k per token row. The same
+ * workspace as amdc_gemm_q4k. */
+int amdc_gemm_q8(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                 uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
+int amdc_gemm_q6k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                  uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 
 /* The dispatch of launch_op for OP_GEMV_Q4 / OP_GEMV_Q8 / OP_GEMV_Q4K /
  * OP_GEMV_Q6K over T tokens (src/hip.c:928-1089): T == 1 -> the decode GEMV;
- * Q4_K with T >= IE_GEMM_MIN (env, default 17) and nb % 8 == 0 -> the GEMM;
+ * Q4_K, Q8_0 and Q6_K with T >= IE_GEMM_MIN (env, default 17) -> the GEMM;
  * else the multi-vector GEMV. kind: any AMDC_KIND_*. */
 int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                  const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);

@@ -125,3 +125,57 @@ def test_errors_do_not_launch(dev, orc):
         dev.gemv_q8(c.W.ptr + 4, c.Q, c.Y, 8, 16)  # misaligned weights
     with pytest.raises(dev.AmdcError):
         dev.Chain([dev.chain_gemv(Q6, c.W, c.Q, c.Y, 8, 16)])  # the chain runs the Q4 kinds only
+
+
+@pytest.mark.parametrize("kind,rows,nb,T", [(Q8, 1, 1, 17), (Q8, 63, 13, 64), (Q8, 130, 128, 65), (Q8, 70, 344, 33), (Q8, 300, 40, 256),
+                                            (Q6, 1, 8, 17), (Q6, 63, 16, 64), (Q6, 64, 160, 65), (Q6, 130, 40, 130), (Q6, 70, 544, 33)])
+@pytest.mark.parametrize("ks", [0, 3])
+def test_gemm(dev, orc, kind, rows, nb, T, ks):
+    """The prefill GEMM (f16 MFMA, exact integer block sums) against the oracle per token row, with a
+    bias, with and without split K."""
+    c = Case(dev, orc, kind, rows, nb, T, seed=rows + T + kind)
+    assert np.array_equal(c.quant(), c.xq)
+    ng = (nb + 7) // 8
+    if ks and ng < ks:
+        pytest.skip("fewer super-groups than splits")
+    bias = np.random.default_rng(T).standard_normal(rows).astype(np.float32)
+    B = dev.DevBuf.of(bias)
+    dev.set_tuning(gemm_ksplit=ks)
+    dev.gemm(kind, c.W, c.Q, c.Y, rows, nb, T, c.xs, rows, bias=B)
+    y = c.y_gpu()
+    for t in range(T):
+        assert rel_err(y[t], orc.epilogue(c.y_oracle(t), bias, None), c.mag(t) + np.abs(bias)) < TOL, t
+
+
+@pytest.mark.parametrize("kind", [Q8, Q6])
+def test_gemm_extreme_values(dev, orc, kind):
+    """Weights and activations at the ends of their ranges, where the exactness of the f16 sums is
+    tightest: Q6_K q = 0 (q - 32 = -32) with scales -128 / 127, Q8_0 weights -128 / 127; activations
+    of one block all +-127 (x = +-1)."""
+    rows, nb, T = 64, 16, 32
+    c = Case(dev, orc, kind, rows, nb, T, seed=5, upload=False)
+    src = c.src.copy()
+    if kind == Q6:
+        blk = src.reshape(-1, 210)
+        blk[:, 0:192] = 0  # q = 0 everywhere
+        blk[0::2, 192:208] = 0x80  # sc = -128
+        blk[1::2, 192:208] = 0x7F  # sc = 127
+    else:
+        blk = src.reshape(-1, 34)
+        blk[0::2, 2:] = 0x80
+        blk[1::2, 2:] = 0x7F
+    x = c.x.copy()
+    x[:, 0:32] = 1.0
+    x[1::2, 32:64] = -1.0
+    c.src, c.x = src, x
+    c.qw, c.qs = orc.repack(ttype(kind), src, rows, nb)
+    c.xq = orc.quant_q8(x)
+    c.W = dev.DevBuf.of(dev.repack(kind, src, rows, 32 * nb))
+    c.X = dev.DevBuf.of(x)
+    c.Q = dev.DevBuf(T * c.xs)
+    c.Y = dev.DevBuf(T * rows * 4)
+    assert np.array_equal(c.quant(), c.xq)
+    dev.gemm(kind, c.W, c.Q, c.Y, rows, nb, T, c.xs, rows)
+    y = c.y_gpu()
+    for t in range(T):
+        assert rel_err(y[t], c.y_oracle(t), c.mag(t)) < TOL, t
