@@ -260,6 +260,8 @@ enum {
   K_GEMMH_Q8_N64,
   K_GEMMH_Q6K_N128,
   K_GEMMH_Q6K_N64,
+  K_GEMV_Q8_V8,
+  K_GEMV_Q6K_V8,
   K_N
 };
 static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1",  "amdc_gemv_q4_k_t1",  "amdc_gemv_q4_0_t1u1",
@@ -271,7 +273,8 @@ static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1
                                        "amdc_gemv_q4_0_x1",   "amdc_gemv_q4_k_x1",  "amdc_gemv_q4_0_p2",  "amdc_gemv_q4_k_p2",
                                        "amdc_chain",          "amdc_rmsnorm_q8",    "amdc_swiglu_q8",     "amdc_gemv_q8_0_p2",
                                        "amdc_gemv_q6_k_p2",   "amdc_dots_q8_0",     "amdc_dots_q6_k",     "amdc_gemmh_q8_0_m64_n128",
-                                       "amdc_gemmh_q8_0_m64_n64", "amdc_gemmh_q6_k_m64_n128", "amdc_gemmh_q6_k_m64_n64"};
+                                       "amdc_gemmh_q8_0_m64_n64", "amdc_gemmh_q6_k_m64_n128", "amdc_gemmh_q6_k_m64_n64",
+                                       "amdc_gemv_q8_0_v8",   "amdc_gemv_q6_k_v8"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -587,7 +590,8 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
     part = g_ws;
   }
   void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs, &part};
-  HIPCALL(H.ModuleLaunchKernel(g_k[kind == AMDC_KIND_Q4_K ? K_GEMV_Q4K_V8 : K_GEMV_Q4_V8], wgs, ks, 1, 256, 1, 1, 0, stream, args, NULL));
+  const int k = kind == AMDC_KIND_Q4_K ? K_GEMV_Q4K_V8 : kind == AMDC_KIND_Q8_0 ? K_GEMV_Q8_V8 : kind == AMDC_KIND_Q6_K ? K_GEMV_Q6K_V8 : K_GEMV_Q4_V8;
+  HIPCALL(H.ModuleLaunchKernel(g_k[k], wgs, ks, 1, 256, 1, 1, 0, stream, args, NULL));
   if (ks > 1u) {
     const u64 n = (u64)rows * T;
     void *ra[] = {&part, &ks, &y, &rows, &T, &bias, &res, &ys, &rs};
@@ -632,7 +636,16 @@ static int gemv_k8_launch(int kind, const void *w, const uint8_t *xq, float *y, 
 
 static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                        const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
-  if (kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) return gemv_k8_launch(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+  if (kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) {
+    if (T == 1u || t_unroll > 0) return gemv_k8_launch(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+    for (u32 t0 = 0; t0 < T; t0 += 8u) { /* the int8-MFMA verify kernel, 8 vectors per launch */
+      const u32 tn = T - t0 < 8u ? T - t0 : 8u;
+      int rc = gemv8_launch(kind, w, xq + (u64)t0 * xs, y + (u64)t0 * ys, rows, nb, bias, res ? res + (u64)t0 * rs : NULL, tn, xs, ys, rs,
+                            stream);
+      if (rc) return rc;
+    }
+    return AMDC_OK;
+  }
   if (T > 1u && T <= 8u && t_unroll <= 0) return gemv8_launch(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
   const u32 ng = amdc_ngroups(nb), L = gemv_lanes(ng), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
   const u32 TT = T == 1u ? 1u : T <= 8u ? 8u : 16u;

@@ -1571,9 +1571,10 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *
 //   B (64 x 16 columns n = t + 8 pp): the 32 activations of token t, block
 //     (g + pp, k), in K half pp, zeros in the other half
 // so that C[r][t + 8 pp] is the exact integer dot of block (g + pp, k) with
-// vector t (Q4_K: sum q a; Q4_0: sum q a, then - 8 asum). Per element the
-// reference's block arithmetic (src/cpu.c:81, 111-112):
-//   Q4_0: acc += (d_w d_a) (dq - 8 asum)
+// vector t (Q4_K: sum q a; Q4_0: sum q a, then - 8 asum; Q8_0: the int8
+// weights of planes 2k, 2k + 1 as A, sum w a). Per element the reference's
+// block arithmetic (src/cpu.c:81, 111-112, 168):
+//   Q4_0: acc += (d_w d_a) (dq - 8 asum); Q8_0: acc += (d_w d_a) dq
 //   Q4_K: acc = fma(s dq, d_a, acc), s = d sc; the min term - sum (dmin mn)
 //         (d_a asum) of every block on v_mfma_f32_16x16x4_f32 (column pp = 0).
 // The columns pp = 0 and 1 of a token hold the sums of alternate blocks; a
@@ -1596,7 +1597,7 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
   __shared__ __attribute__((aligned(16))) float smn[4][64][16]; // per wave, Q4_K: -(dmin mn) [block][row]
   const u32 ng = amdc_ngroups(nb), nt = (ng + 7u) >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
   const u32 i16 = lane & 15u, h = lane >> 4, n = i16, tk = n & 7u, pp = n >> 3;
-  const u32 RB = (u32)amdc_row_bytes(nb);
+  const u32 RB = (u32)amdc_row_bytes_k(KIND, nb);
   const u32 rt0 = blockIdx.x * 64u, r0 = rt0 + 16u * w, ra = r0 + i16 < rows ? r0 + i16 : rows - 1u; // A row of this lane
   // a workgroup-uniform resource over the tile's rows; the lane's row in the 32-bit offset
   const __amdgpu_buffer_rsrc_t rw = rsrc(W + (u64)rt0 * RB, (u32)min((u64)(rows - rt0) * RB, (u64)0xFFFFFFF0u));
@@ -1619,7 +1620,8 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
 #pragma unroll
     for (u32 p = 0; p < 4u; p++) {
       const u32 gl = 2u * p + (h >> 1);
-      wq[p] = __builtin_amdgcn_raw_buffer_load_b128(rw, gl < gt ? wo + (u32)amdc_nib_off(ng, 8u * t + gl, k) : OOB, 0, 0);
+      const u32 o = KIND == AMDC_Q8_0 ? (u32)amdc_q8_off(ng, 8u * t + gl, 2u * k + (h & 1u)) : (u32)amdc_nib_off(ng, 8u * t + gl, k);
+      wq[p] = __builtin_amdgcn_raw_buffer_load_b128(rw, gl < gt ? wo + o : OOB, 0, 0);
     }
   };
   // activations of tile t in registers (thread: 2 of the 16-byte halves, 2 of the (block, token) scale pairs)
@@ -1666,7 +1668,7 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
       const u32x4 hd = rh[q];
 #pragma unroll
       for (u32 k = 0; k < 8u; k++) {
-        if (KIND == AMDC_Q4_0) {
+        if (KIND == AMDC_Q4_0 || KIND == AMDC_Q8_0) {
           ssc[w][8u * gl + k][i16] = h2f(hword(hd, k >> 1) >> (16u * (k & 1u)));
         } else {
           ssc[w][8u * gl + k][i16] = h2f(hd.x) * (float)q4k_sc(hd, k);
@@ -1682,7 +1684,7 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
 #pragma unroll
     for (u32 p = 0; p < 4u; p++) { // the MFMAs of the plane first
       if (p < npair) {
-        const u32x4 a = (wq[p] >> (4u * (h & 1u))) & 0x0F0F0F0Fu;
+        const u32x4 a = KIND == AMDC_Q8_0 ? wq[p] : (wq[p] >> (4u * (h & 1u))) & 0x0F0F0F0Fu;
         const u32x4 bq = sB[p + 4u * k][h][n];
         c[p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, bq), (v4i){0, 0, 0, 0}, 0, 0, 0);
       }
@@ -1697,6 +1699,9 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
         const u32 as = __builtin_bit_cast(u32, sxa[bl][tk]);
 #pragma unroll
         for (u32 v = 0; v < 4u; v++) acc[v] += (s4[v] * da) * (float)(int)((u32)c[p][v] - 8u * as);
+      } else if (KIND == AMDC_Q8_0) {
+#pragma unroll
+        for (u32 v = 0; v < 4u; v++) acc[v] += (s4[v] * da) * (float)c[p][v];
       } else {
 #pragma unroll
         for (u32 v = 0; v < 4u; v++) acc[v] = __builtin_fmaf(s4[v] * (float)c[p][v], da, acc[v]);
@@ -1766,4 +1771,168 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_v8(const uint8_
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *part) {
   gemv8_body<AMDC_Q4_K>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+}
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+                                                                   const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
+                                                                   float *part) {
+  gemv8_body<AMDC_Q8_0>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+}
+
+// The verify GEMV for Q6_K (T <= 8): the scale of a Q6_K weight changes every
+// 16 weights, so one v_mfma_i32_16x16x32_i8 per sub-block (g, k):
+//   A (16 rows x 32): lane (row i, h) = q - 32 of weights 8h .. 8h + 7 (half
+//     h >> 1), from its nibble bytes and high-bit word (q6k_dots' packing)
+//   B (32 x 16 columns n = t + 8 hh): activations 16 hh .. 16 hh + 15 of token
+//     t in K rows 16 hh .., zeros in the other half
+// so that C[r][t + 8 hh] = the exact half dot sum (q - 32) a of ie_q6k_dots.
+// Per element acc = fma(s C, d_a, acc) with s = d sc_hh (the reference's
+// fma(fma(s1, d1, s0 d0), d_a, acc) of src/cpu.c:142 regrouped by half); the
+// two half columns of a token are joined at the end. Tiles of 8 super-groups
+// (64 sub-blocks) as gemv8_body: the activations and d_a staged in LDS, each
+// wave's table of d sc per (sub-block, half, row) from the scale panel; the
+// weights from memory one plane ahead (a ring of 4 planes: per plane 8
+// sub-blocks x 12 bytes per lane). Split K over gridDim.y as gemv8_body.
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq,
+                                                                   float *__restrict__ y, u32 rows, u32 nb, const float *__restrict__ bias,
+                                                                   const float *__restrict__ res, u32 T, u32 xs, u32 ys, u32 rs,
+                                                                   float *__restrict__ part) {
+  __shared__ __attribute__((aligned(16))) u32x2 sB[64][4][16];     // [sub-block of tile][K quarter][column]
+  __shared__ __attribute__((aligned(16))) float sda[64][8];        // d_a [sub-block][token]
+  __shared__ __attribute__((aligned(16))) float ssc[4][64][2][16]; // per wave: d sc [sub-block][half][row]
+  const u32 ng = nb >> 3, nt = (ng + 7u) >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
+  const u32 i16 = lane & 15u, h = lane >> 4, n = i16, tk = n & 7u, hh = n >> 3;
+  const u32 RB = (u32)amdc_q6k_row_bytes(nb);
+  const u32 rt0 = blockIdx.x * 64u, r0 = rt0 + 16u * w, ra = r0 + i16 < rows ? r0 + i16 : rows - 1u;
+  const __amdgpu_buffer_rsrc_t rw = rsrc(W + (u64)rt0 * RB, (u32)min((u64)(rows - rt0) * RB, (u64)0xFFFFFFF0u));
+  const u32 wo = (ra - rt0) * RB;
+  const __amdgpu_buffer_rsrc_t rxq = rsrc(xq, (u32)min((u64)T * xs, (u64)0xFFFFFFF0u));
+  constexpr u32 OOB = 0xFFFFFFF0u;
+  const u32 ks = blockIdx.y, nks = gridDim.y, t0 = nt * ks / nks, t1 = nt * (ks + 1u) / nks;
+  for (u32 i = tid; i < 64u * 4u * 16u; i += NT) { // the zero halves of B
+    const u32 col = i & 15u, q = (i >> 4) & 3u;
+    if ((q >> 1) != (col >> 3)) (&sB[0][0][0])[i] = (u32x2)(0u);
+  }
+  auto gtile = [&](u32 t) { return ng - 8u * t < 8u ? ng - 8u * t : 8u; };
+  // plane k of tile t: per super-group gl, the lane's 8 nibble bytes and its half's high-bit word
+  auto load_plane = [&](u32 t, u32 k, u32 (&wq)[8][3]) {
+    const u32 gt = gtile(t);
+#pragma unroll
+    for (u32 gl = 0; gl < 8u; gl++) {
+      const u32 g = 8u * t + gl;
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rw, gl < gt ? wo + (u32)amdc_q6k_nib_off(ng, g, k) + 8u * (h & 1u) : OOB, 0, 0);
+      wq[gl][0] = v.x, wq[gl][1] = v.y;
+      wq[gl][2] = __builtin_amdgcn_raw_buffer_load_b32(
+          rw, gl < gt ? wo + (u32)amdc_q6k_hi_off(ng, g, k >> 1) + 8u * (k & 1u) + 4u * (h >> 1) : OOB, 0, 0);
+    }
+  };
+  u32x4 ra4[4];
+  float rd[2];
+  u32x4 rh[2];
+  u32 rdd[2];
+  auto fetch_tile = [&](u32 t) {
+    const u32 gt = gtile(t);
+#pragma unroll
+    for (u32 c = 0; c < 4u; c++) {
+      const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, b = 64u * t + bl;
+      const bool ok = tok < T && (bl >> 3) < gt;
+      ra4[c] = __builtin_amdgcn_raw_buffer_load_b128(rxq, ok ? tok * xs + 32u * b + 16u * half : OOB, 0, 0);
+    }
+#pragma unroll
+    for (u32 c = 0; c < 2u; c++) {
+      const u32 i = tid + c * NT, tok = i & 7u, bl = i >> 3, b = 64u * t + bl;
+      const bool ok = tok < T && (bl >> 3) < gt;
+      rd[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxq, ok ? tok * xs + 32u * nb + 4u * b : OOB, 0, 0));
+    }
+#pragma unroll
+    for (u32 q = 0; q < 2u; q++) {
+      const u32 gl = h + 4u * q, g = 8u * t + gl;
+      rh[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, gl < gt ? wo + 16u * g : OOB, 0, 0);
+      rdd[q] = __builtin_amdgcn_raw_buffer_load_b16(rw, gl < gt ? wo + (u32)amdc_q6k_d_off(ng, g) : OOB, 0, 0);
+    }
+  };
+  auto stage_tile = [&]() {
+#pragma unroll
+    for (u32 c = 0; c < 4u; c++) {
+      const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7;
+      sB[bl][2u * half][tok + 8u * half] = (u32x2){ra4[c].x, ra4[c].y};
+      sB[bl][2u * half + 1u][tok + 8u * half] = (u32x2){ra4[c].z, ra4[c].w};
+    }
+#pragma unroll
+    for (u32 c = 0; c < 2u; c++) {
+      const u32 i = tid + c * NT;
+      sda[i >> 3][i & 7u] = rd[c];
+    }
+#pragma unroll
+    for (u32 q = 0; q < 2u; q++) { // this wave's table: row i16, super-groups h, h + 4
+      const u32 gl = h + 4u * q;
+      const float d = h2f(rdd[q]);
+#pragma unroll
+      for (u32 k = 0; k < 8u; k++)
+#pragma unroll
+        for (u32 e = 0; e < 2u; e++)
+          ssc[w][8u * gl + k][e][i16] = d * (float)(int)(int8_t)(hword(rh[q], k >> 1) >> (16u * (k & 1u) + 8u * e));
+    }
+  };
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto plane = [&](u32 k, u32 gt, const u32 (&wq)[8][3]) {
+    v4i c[8];
+    const u32 sft = 4u * (h >> 1), hs = 4u * (h & 1u);
+#pragma unroll
+    for (u32 gl = 0; gl < 8u; gl++) { // the MFMAs of the plane first
+      if (gl < gt) {
+        const u32 v0 = ((wq[gl][0] >> sft) & 0x0F0F0F0Fu) | (((wq[gl][2] >> hs) & 0x03030303u) << 4);
+        const u32 v1 = ((wq[gl][1] >> sft) & 0x0F0F0F0Fu) | (((wq[gl][2] >> (hs + 2u)) & 0x03030303u) << 4);
+        const u32 s0 = ((v0 | 0x80808080u) - 0x20202020u) ^ 0x80808080u, s1 = ((v1 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+        const u32x2 bq = sB[8u * gl + k][h][n];
+        c[gl] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)((u64)s0 | ((u64)s1 << 32)), (long)((u64)bq.x | ((u64)bq.y << 32)),
+                                                      (v4i){0, 0, 0, 0}, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (u32 gl = 0; gl < 8u; gl++) {
+      if (gl >= gt) break;
+      const u32 bl = 8u * gl + k;
+      const v4f s4 = *(const v4f *)&ssc[w][bl][hh][4u * h];
+      const float da = sda[bl][tk];
+#pragma unroll
+      for (u32 v = 0; v < 4u; v++) acc[v] = __builtin_fmaf(s4[v] * (float)c[gl][v], da, acc[v]);
+    }
+  };
+  u32 wq[4][8][3];
+  if (t0 < t1) {
+    fetch_tile(t0);
+#pragma unroll
+    for (u32 k = 0; k < 4u; k++) load_plane(t0, k, wq[k]);
+  }
+  for (u32 t = t0; t < t1; t++) {
+    const bool more = t + 1u < t1;
+    const u32 gt = gtile(t);
+    __syncthreads();
+    stage_tile();
+    __syncthreads();
+    if (more) fetch_tile(t + 1u);
+#pragma unroll
+    for (u32 k = 0; k < 8u; k++) {
+      plane(k, gt, wq[k & 3u]);
+      if (k < 4u) load_plane(t, k + 4u, wq[k & 3u]);
+      else if (more) load_plane(t + 1u, k - 4u, wq[k & 3u]);
+    }
+  }
+#pragma unroll
+  for (u32 v = 0; v < 4u; v++) acc[v] += dpp<0x128>(acc[v]); // row_ror:8: the two halves of a token
+  if (hh == 0u && tk < T) {
+#pragma unroll
+    for (u32 v = 0; v < 4u; v++) {
+      const u32 r = r0 + 4u * h + v;
+      if (r >= rows) continue;
+      if (part) {
+        part[((u64)ks * T + tk) * rows + r] = acc[v];
+      } else {
+        float o = acc[v];
+        if (bias) o = o + bias[r];
+        if (res) o = res[(u64)tk * rs + r] + o;
+        y[(u64)tk * ys + r] = o;
+      }
+    }
+  }
 }

@@ -260,21 +260,24 @@ def prefill_set(steps, seed, timer):
 def k8_set(seed, timer):
     """The Q8_0 and Q6_K decode GEMVs at the sizes they have in the c1 / c2 models (the Q6_K
     matrices of a Q4_K_M file: ffn_down, attn_v, lm_head; Q8_0 projections): us per launch and the
-    GGUF weight bytes per second."""
+    GGUF weight bytes per second, at T = 1 and for the T = 8 verify (weights read once)."""
     out = {}
     sets = [(synth.KIND_Q8_0, "q8_0_q", 4096, 4096), (synth.KIND_Q8_0, "q8_0_gate", 11008, 4096),
             (synth.KIND_Q8_0, "q8_0_down", 4096, 11008), (synth.KIND_Q6_K, "q6_k_ffn_down", 5120, 17408),
             (synth.KIND_Q6_K, "q6_k_attn_v", 1024, 5120), (synth.KIND_Q6_K, "q6_k_lm_head", 152064, 5120)]
     for i, (kind, name, r, c) in enumerate(sets):
         M = Mats(kind, [(name, r, c)], seed + i, min_bytes=1 << 30)
-        nb = c // 32
-        X = amdc.DevBuf.of(synth.activations(1, c, seed + 90 + i))
-        Q, Y = amdc.DevBuf(q8_stride(nb)), amdc.DevBuf(4 * r)
-        amdc.quant_q8(X, Q, nb)
+        nb, xs = c // 32, q8_stride(c // 32)
+        X = amdc.DevBuf.of(synth.activations(8, c, seed + 90 + i))
+        Q, Y = amdc.DevBuf(8 * xs), amdc.DevBuf(4 * 8 * r)
+        amdc.quant_q8(X, Q, nb, 8, 4 * c, xs)
         t = timer.per_launch_ms(lambda j, s: amdc.gemv(kind, M.dev[j % M.copies][0], Q, Y, r, nb, stream=s), M.copies)
+        amdc.gemv_t(kind, M.dev[0][0], Q, Y, r, nb, 8, xs, r)  # sizes the workspace before the capture
+        t8 = timer.per_launch_ms(lambda j, s: amdc.gemv_t(kind, M.dev[j % M.copies][0], Q, Y, r, nb, 8, xs, r, stream=s), M.copies)
         b = wbytes(r, c, kind)
         out[name] = {"rows": r, "cols": c, "us": round(t * 1e3, 3), "GB/s": round(b / t / 1e6, 1),
-                     "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4)}
+                     "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4), "T8_us": round(t8 * 1e3, 3),
+                     "T8_GB/s": round(b / t8 / 1e6, 1)}
         del M
     return out
 

@@ -179,3 +179,37 @@ def test_gemm_extreme_values(dev, orc, kind):
     y = c.y_gpu()
     for t in range(T):
         assert rel_err(y[t], c.y_oracle(t), c.mag(t)) < TOL, t
+
+
+@pytest.mark.parametrize("kind,rows,nb", [(Q8, 200, 544), (Q8, 77, 13), (Q6, 200, 544), (Q6, 70, 24)])
+@pytest.mark.parametrize("T", [1, 2, 7, 8])
+def test_verify_splitk(dev, orc, kind, rows, nb, T):
+    """The T <= 8 verify kernels (int8 MFMA; Q6_K one sub-block per MFMA, half dots in separate
+    columns) with K split over workgroups: several splits in a row, with bias and residual, all
+    within the bound and a repeated split gives the same bits; the per-vector decode kernel
+    (tuning unroll=1) agrees within the bound."""
+    c = Case(dev, orc, kind, rows, nb, T, seed=21 + T)
+    c.quant()
+    g = np.random.default_rng(3)
+    bias = g.standard_normal(rows).astype(np.float32)
+    res = g.standard_normal((T, rows)).astype(np.float32)
+    B, R = dev.DevBuf.of(bias), dev.DevBuf.of(res)
+    bits = {}
+    for ks in (1, 9, 4, 9, 2, 1):
+        dev.set_tuning(gemm_ksplit=ks)
+        c.Y.fill(0)
+        dev.gemv_t(kind, c.W, c.Q, c.Y, rows, nb, T, c.xs, rows, rs=rows, bias=B, res=R)
+        y = c.y_gpu()
+        for t in range(T):
+            want = orc.epilogue(c.y_oracle(t), bias, res[t])
+            assert rel_err(y[t], want, c.mag(t) + np.abs(bias) + np.abs(res[t])) < TOL, (ks, t)
+        u = y.view(np.uint32).copy()
+        if ks in bits:
+            assert np.array_equal(u, bits[ks]), ks
+        bits[ks] = u
+    dev.set_tuning(unroll=1)
+    c.Y.fill(0)
+    dev.gemv_t(kind, c.W, c.Q, c.Y, rows, nb, T, c.xs, rows, rs=rows, bias=B, res=R)
+    y = c.y_gpu()
+    for t in range(T):
+        assert rel_err(y[t], orc.epilogue(c.y_oracle(t), bias, res[t]), c.mag(t) + np.abs(bias) + np.abs(res[t])) < TOL, t
