@@ -26,8 +26,45 @@ KIND_Q4_0, KIND_Q8_0, KIND_Q4_K, KIND_Q6_K = 0, 2, 3, 4
 _SUF = {KIND_Q4_0: "q4", KIND_Q8_0: "q8", KIND_Q4_K: "q4k", KIND_Q6_K: "q6k"}
 _P, _U32 = C.c_void_p, C.c_uint32
 
-# every function of include/amdc_q4.h: name -> (restype, argtypes)
+_I64, _U64 = C.c_int64, C.c_uint64
+_PP = C.POINTER(C.c_void_p)
+
+
+class GgufTensor(C.Structure):
+    """amdc_gguf_tensor (include/amdc_gguf.h)."""
+    _fields_ = [("name", C.c_char_p), ("type", C.c_uint32), ("n_dims", C.c_uint32), ("ne", C.c_uint64 * 4),
+                ("offset", C.c_uint64), ("nbytes", C.c_uint64), ("data", C.c_void_p)]
+
+
+class Mat(C.Structure):
+    """amdc_mat (include/amdc_gguf.h): a matrix in the CDNA4 layout."""
+    _fields_ = [("kind", C.c_int), ("rows", C.c_uint32), ("cols", C.c_uint32), ("nb", C.c_uint32), ("bytes", C.c_uint64),
+                ("w", C.c_void_p)]
+
+
+# every function of include/amdc_q4.h and include/amdc_gguf.h: name -> (restype, argtypes)
 ABI = {
+    "amdc_gguf_open": (C.c_int, [C.c_char_p, _PP]),
+    "amdc_gguf_close": (None, [_P]),
+    "amdc_gguf_version": (C.c_uint32, [_P]),
+    "amdc_gguf_alignment": (C.c_uint32, [_P]),
+    "amdc_gguf_data_offset": (_U64, [_P]),
+    "amdc_gguf_n_kv": (_U64, [_P]),
+    "amdc_gguf_n_tensors": (_U64, [_P]),
+    "amdc_gguf_key_at": (C.c_int, [_P, _U64, C.POINTER(C.c_char_p), C.POINTER(C.c_uint32)]),
+    "amdc_gguf_get_int": (C.c_int, [_P, C.c_char_p, C.POINTER(_I64)]),
+    "amdc_gguf_get_float": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_double)]),
+    "amdc_gguf_get_str": (C.c_int, [_P, C.c_char_p, _PP, C.POINTER(_U64)]),
+    "amdc_gguf_get_arr": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_uint32), C.POINTER(_U64), _PP]),
+    "amdc_gguf_get_arr_str": (C.c_int, [_P, C.c_char_p, _U64, _PP, C.POINTER(_U64)]),
+    "amdc_gguf_tensor_at": (C.c_int, [_P, _U64, C.POINTER(GgufTensor)]),
+    "amdc_gguf_find_tensor": (_I64, [_P, C.c_char_p]),
+    "amdc_ggml_nbytes": (_U64, [C.c_uint32, _U64]),
+    "amdc_gguf_mat_kind": (C.c_int, [C.c_uint32]),
+    "amdc_gguf_mat_info": (C.c_int, [_P, C.c_char_p, C.POINTER(Mat)]),
+    "amdc_gguf_repack": (C.c_int, [_P, C.c_char_p, C.c_int, C.POINTER(Mat), _P]),
+    "amdc_gguf_load": (C.c_int, [_P, C.c_char_p, C.c_int, C.POINTER(Mat), _P]),
+    "amdc_mat_release": (C.c_int, [C.POINTER(Mat)]),
     "amdc_last_error": (C.c_char_p, []),
     "amdc_mat_bytes": (C.c_size_t, [C.c_int, _U32, _U32]),
     "amdc_repack_q4": (C.c_int, [_P, _U32, _U32, _P]),
@@ -190,7 +227,7 @@ class DevBuf:
 def _p(x):
     if x is None:
         return None
-    return x.ptr if isinstance(x, DevBuf) else int(x)
+    return x.ptr if isinstance(x, (DevBuf, DevMat)) else int(x)
 
 
 class Event:
@@ -411,3 +448,130 @@ class Chain:
         if getattr(self, "h", None) and _lib is not None:
             lib().amdc_chain_destroy(self.h)
             self.h = None
+
+
+# ---------------------------------------------------------------- GGUF files (include/amdc_gguf.h)
+
+class Gguf:
+    """A GGUF v3 file opened by amdc_gguf_open (memory-mapped)."""
+
+    def __init__(self, path):
+        h = _P()
+        _check(lib().amdc_gguf_open(os.fsencode(path), C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None) and _lib is not None:
+            lib().amdc_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    @property
+    def version(self):
+        return lib().amdc_gguf_version(self.h)
+
+    @property
+    def alignment(self):
+        return lib().amdc_gguf_alignment(self.h)
+
+    @property
+    def data_offset(self):
+        return lib().amdc_gguf_data_offset(self.h)
+
+    def keys(self):
+        out = []
+        for i in range(lib().amdc_gguf_n_kv(self.h)):
+            k, t = C.c_char_p(), C.c_uint32()
+            _check(lib().amdc_gguf_key_at(self.h, i, C.byref(k), C.byref(t)))
+            out.append((k.value.decode(), t.value))
+        return out
+
+    def get_int(self, key):
+        v = _I64()
+        return v.value if lib().amdc_gguf_get_int(self.h, key.encode(), C.byref(v)) else None
+
+    def get_float(self, key):
+        v = C.c_double()
+        return v.value if lib().amdc_gguf_get_float(self.h, key.encode(), C.byref(v)) else None
+
+    def get_str(self, key):
+        p, n = C.c_void_p(), _U64()
+        if not lib().amdc_gguf_get_str(self.h, key.encode(), C.byref(p), C.byref(n)):
+            return None
+        return C.string_at(p.value, n.value).decode() if n.value else ""
+
+    def get_arr(self, key):
+        """(element type, count, numpy view of the packed scalars or None)."""
+        t, n, d = C.c_uint32(), _U64(), C.c_void_p()
+        if not lib().amdc_gguf_get_arr(self.h, key.encode(), C.byref(t), C.byref(n), C.byref(d)):
+            return None
+        dt = {0: np.uint8, 1: np.int8, 2: np.uint16, 3: np.int16, 4: np.uint32, 5: np.int32, 6: np.float32, 7: np.uint8,
+              10: np.uint64, 11: np.int64, 12: np.float64}.get(t.value)
+        arr = None
+        if d.value and dt is not None:
+            arr = np.frombuffer(C.string_at(d.value, n.value * np.dtype(dt).itemsize), dtype=dt)
+        return t.value, n.value, arr
+
+    def get_arr_str(self, key, i):
+        p, n = C.c_void_p(), _U64()
+        if not lib().amdc_gguf_get_arr_str(self.h, key.encode(), i, C.byref(p), C.byref(n)):
+            return None
+        return C.string_at(p.value, n.value).decode() if n.value else ""
+
+    def tensors(self):
+        out = []
+        for i in range(lib().amdc_gguf_n_tensors(self.h)):
+            t = GgufTensor()
+            _check(lib().amdc_gguf_tensor_at(self.h, i, C.byref(t)))
+            out.append(t)
+        return out
+
+    def find(self, name):
+        return lib().amdc_gguf_find_tensor(self.h, name.encode())
+
+    def mat_info(self, name):
+        m = Mat()
+        _check(lib().amdc_gguf_mat_info(self.h, name.encode(), C.byref(m)))
+        return m
+
+    def repack(self, name, threads=0):
+        """The tensor repacked into the CDNA4 layout on the host: (Mat, uint8 array)."""
+        m = self.mat_info(name)
+        dst = np.empty(m.bytes, dtype=np.uint8)
+        _check(lib().amdc_gguf_repack(self.h, name.encode(), threads, C.byref(m), dst.ctypes.data_as(_P)))
+        return m, dst
+
+    def load(self, name, threads=0, stream=None):
+        """The streaming load to the device (amdc_gguf_load): a DevMat owning the device memory."""
+        m = Mat()
+        _check(lib().amdc_gguf_load(self.h, name.encode(), threads, C.byref(m), stream))
+        return DevMat(m)
+
+
+class DevMat:
+    """A device matrix from Gguf.load; .ptr is the weights, .m the amdc_mat."""
+
+    def __init__(self, m):
+        self.m = m
+        self.ptr = m.w
+
+    def download(self):
+        out = np.empty(self.m.bytes, dtype=np.uint8)
+        _check(lib().amdc_memcpy_d2h(out.ctypes.data_as(_P), self.ptr, self.m.bytes))
+        return out
+
+    def free(self):
+        if self.m.w and _lib is not None:
+            lib().amdc_mat_release(C.byref(self.m))
+            self.ptr = None
+
+    def __del__(self):
+        self.free()

@@ -9,6 +9,7 @@
  * repack_q4 / repack_q4k of src/model.c. */
 #define _GNU_SOURCE
 #include "../../include/amdc_q4.h"
+#include "../../include/amdc_gguf.h"
 
 #include <dlfcn.h>
 #include <stdarg.h>
@@ -16,6 +17,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "amdc_internal.h"
 #include "amdc_layout.h"
 
 typedef uint32_t u32;
@@ -25,10 +27,15 @@ typedef uint64_t u64;
 
 static char g_err[512];
 
+int amdc_fail_v(int code, const char *fmt, va_list ap) {
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  return code;
+}
+
 static int fail(int code, const char *fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
-  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  amdc_fail_v(code, fmt, ap);
   va_end(ap);
   return code;
 }
@@ -218,6 +225,9 @@ static struct {
   hipError_t (*GraphLaunch)(hipGraphExec_t, hipStream_t);
   hipError_t (*GraphExecDestroy)(hipGraphExec_t);
   hipError_t (*OccupancyMaxActiveBlocks)(int *, hipFunction_t, int, size_t);
+  hipError_t (*HostMalloc)(void **, size_t, unsigned);
+  hipError_t (*HostFree)(void *);
+  hipError_t (*MemcpyAsync)(void *, const void *, size_t, int, hipStream_t);
 } H;
 
 /* The kernels of amdc_kernels.hip. */
@@ -340,6 +350,9 @@ static int hip_load(void) {
   SYM(GraphLaunch, "hipGraphLaunch");
   SYM(GraphExecDestroy, "hipGraphExecDestroy");
   SYM(OccupancyMaxActiveBlocks, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+  SYM(HostMalloc, "hipHostMalloc");
+  SYM(HostFree, "hipHostFree");
+  SYM(MemcpyAsync, "hipMemcpyAsync");
 #undef SYM
   return AMDC_OK;
 }
@@ -1045,5 +1058,71 @@ int amdc_chain_destroy(void *chain) {
   if (!c) return AMDC_OK;
   HIPCALL(H.Free(c->ops));
   free(c);
+  return AMDC_OK;
+}
+
+/* ---------------------------------------------------------------- the streaming matrix load */
+
+AMDC_HIDDEN int amdc_gguf_repack_rows(const amdc_gguf_tensor *t, const amdc_mat *m, u32 r0, u32 r1, int nthreads, uint8_t *dst);
+AMDC_HIDDEN int amdc_gguf_tensor_ptr(const amdc_gguf *g, const char *name, const amdc_gguf_tensor **t);
+
+
+/* Chunks of rows alternate between two pinned staging buffers: chunk c is
+ * repacked into buffer c & 1 once the copy of chunk c - 2 out of it has
+ * finished (its event), then copied with hipMemcpyAsync on the stream, so the
+ * repack of one chunk runs while the previous one crosses PCIe. */
+int amdc_gguf_load(const amdc_gguf *g, const char *name, int nthreads, amdc_mat *m, void *stream) {
+  NEED_OPEN();
+  int rc = amdc_gguf_mat_info(g, name, m);
+  const amdc_gguf_tensor *t = NULL;
+  if (!rc) rc = amdc_gguf_tensor_ptr(g, name, &t);
+  if (rc) return rc;
+  const u64 rb = m->bytes / m->rows;
+  /* bytes of repacked rows per staging buffer: 32 MiB (AMDC_LOAD_CHUNK_KB) */
+  const u64 chunk = (u64)envi("AMDC_LOAD_CHUNK_KB", 32768) << 10;
+  u32 per = (u32)(chunk / rb);
+  if (per < 1u) per = 1u;
+  if (per > m->rows) per = m->rows;
+  void *dev = NULL, *stg[2] = {NULL, NULL};
+  hipEvent_t ev[2] = {NULL, NULL};
+  int used[2] = {0, 0};
+  hipError_t e = H.Malloc(&dev, m->bytes);
+  if (e) return fail(AMDC_EHIP, "gguf_load: hipMalloc of %llu bytes: %s", (unsigned long long)m->bytes, H.GetErrorString(e));
+  for (int b = 0; b < 2 && !rc; b++) {
+    if ((e = H.HostMalloc(&stg[b], (size_t)per * rb, 0)) || (e = H.EventCreate(&ev[b])))
+      rc = fail(AMDC_EHIP, "gguf_load: staging buffers: %s", H.GetErrorString(e));
+  }
+  for (u32 r0 = 0, c = 0; !rc && r0 < m->rows; r0 += per, c++) {
+    const u32 r1 = m->rows - r0 < per ? m->rows : r0 + per, b = c & 1u;
+    if (used[b] && (e = H.EventSynchronize(ev[b]))) {
+      rc = fail(AMDC_EHIP, "gguf_load: %s", H.GetErrorString(e));
+      break;
+    }
+    if ((rc = amdc_gguf_repack_rows(t, m, r0, r1, nthreads, (uint8_t *)stg[b]))) break;
+    if ((e = H.MemcpyAsync((uint8_t *)dev + (u64)r0 * rb, stg[b], (size_t)(r1 - r0) * rb, hipMemcpyHostToDevice, stream)) ||
+        (e = H.EventRecord(ev[b], stream)))
+      rc = fail(AMDC_EHIP, "gguf_load: copy: %s", H.GetErrorString(e));
+    used[b] = 1;
+  }
+  for (int b = 0; b < 2; b++) { /* every copy out of the staging buffers is done before they go */
+    if (used[b] && (e = H.EventSynchronize(ev[b])) && !rc) rc = fail(AMDC_EHIP, "gguf_load: %s", H.GetErrorString(e));
+    if (ev[b]) H.EventDestroy(ev[b]);
+    if (stg[b]) H.HostFree(stg[b]);
+  }
+  if (rc) {
+    H.Free(dev);
+    return rc;
+  }
+  m->w = dev;
+  return AMDC_OK;
+}
+
+int amdc_mat_release(amdc_mat *m) {
+  if (!m) return fail(AMDC_EINVAL, "mat_release: null");
+  if (m->w) {
+    NEED_OPEN();
+    HIPCALL(H.Free(m->w));
+  }
+  m->w = NULL;
   return AMDC_OK;
 }

@@ -12,18 +12,18 @@ import pytest
 import amdc
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "amdc_q4.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("amdc_q4.h", "amdc_gguf.h")]
 
 
 def declared():
-    src = open(HEADER).read()
+    src = "".join(open(h).read() for h in HEADERS)
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     return sorted(set(re.findall(r"\b(amdc_\w+)\s*\(", src)))
 
 
 def test_header_functions_exported_and_bound():
     names = declared()
-    assert len(names) >= 25
+    assert len(names) >= 70
     lib = amdc.lib()
     for n in names:
         assert hasattr(lib, n), n
