@@ -442,7 +442,7 @@ static void *rjob_run(void *p) {
  * row r0 at dst) over nthreads threads */
 AMDC_HIDDEN int amdc_gguf_repack_rows(const amdc_gguf_tensor *t, const amdc_mat *m, u32 r0, u32 r1, int nthreads, uint8_t *dst) {
   const u64 sb = amdc_ggml_nbytes(t->type, m->cols), db = m->bytes / m->rows;
-  int nt = nthreads > 0 ? nthreads : (int)(((u64)(r1 - r0) * sb) / (8u << 20)) + 1;
+  int nt = nthreads > 0 ? nthreads : (int)(((u64)(r1 - r0) * sb) / (1u << 20)) + 1;
   if (nt > 16) nt = 16;
   if ((u32)nt > r1 - r0) nt = (int)(r1 - r0);
   if (nt < 1) nt = 1;

@@ -390,7 +390,10 @@ int amdc_open(const char *hsaco) {
   return AMDC_OK;
 }
 
+static void stage_free(void);
+
 void amdc_close(void) {
+  if (g_open) stage_free();
   if (g_open && g_ws) H.Free(g_ws);
   g_ws = NULL, g_ws_bytes = 0;
   if (g_open && g_mod) H.ModuleUnload(g_mod);
@@ -1067,6 +1070,37 @@ AMDC_HIDDEN int amdc_gguf_repack_rows(const amdc_gguf_tensor *t, const amdc_mat 
 AMDC_HIDDEN int amdc_gguf_tensor_ptr(const amdc_gguf *g, const char *name, const amdc_gguf_tensor **t);
 
 
+/* The two pinned staging buffers of the load and their events, kept for
+ * later loads (pinning memory costs milliseconds), freed by amdc_close. */
+static void *g_stg[2];
+static hipEvent_t g_stg_ev[2];
+static size_t g_stg_bytes;
+
+static int stage_reserve(size_t n) {
+  if (n <= g_stg_bytes && g_stg[0]) return AMDC_OK;
+  for (int b = 0; b < 2; b++) {
+    if (g_stg[b]) H.HostFree(g_stg[b]);
+    g_stg[b] = NULL;
+  }
+  g_stg_bytes = 0;
+  hipError_t e;
+  for (int b = 0; b < 2; b++) {
+    if ((e = H.HostMalloc(&g_stg[b], n, 0))) return fail(AMDC_EHIP, "gguf_load: pinned staging of %zu bytes: %s", n, H.GetErrorString(e));
+    if (!g_stg_ev[b] && (e = H.EventCreate(&g_stg_ev[b]))) return fail(AMDC_EHIP, "gguf_load: %s", H.GetErrorString(e));
+  }
+  g_stg_bytes = n;
+  return AMDC_OK;
+}
+
+static void stage_free(void) {
+  for (int b = 0; b < 2; b++) {
+    if (g_stg[b]) H.HostFree(g_stg[b]);
+    if (g_stg_ev[b]) H.EventDestroy(g_stg_ev[b]);
+    g_stg[b] = NULL, g_stg_ev[b] = NULL;
+  }
+  g_stg_bytes = 0;
+}
+
 /* Chunks of rows alternate between two pinned staging buffers: chunk c is
  * repacked into buffer c & 1 once the copy of chunk c - 2 out of it has
  * finished (its event), then copied with hipMemcpyAsync on the stream, so the
@@ -1083,32 +1117,29 @@ int amdc_gguf_load(const amdc_gguf *g, const char *name, int nthreads, amdc_mat 
   u32 per = (u32)(chunk / rb);
   if (per < 1u) per = 1u;
   if (per > m->rows) per = m->rows;
-  void *dev = NULL, *stg[2] = {NULL, NULL};
-  hipEvent_t ev[2] = {NULL, NULL};
+  void *dev = NULL, *stg[2];
   int used[2] = {0, 0};
   hipError_t e = H.Malloc(&dev, m->bytes);
   if (e) return fail(AMDC_EHIP, "gguf_load: hipMalloc of %llu bytes: %s", (unsigned long long)m->bytes, H.GetErrorString(e));
-  for (int b = 0; b < 2 && !rc; b++) {
-    if ((e = H.HostMalloc(&stg[b], (size_t)per * rb, 0)) || (e = H.EventCreate(&ev[b])))
-      rc = fail(AMDC_EHIP, "gguf_load: staging buffers: %s", H.GetErrorString(e));
+  if ((rc = stage_reserve((size_t)per * rb))) {
+    H.Free(dev);
+    return rc;
   }
+  stg[0] = g_stg[0], stg[1] = g_stg[1];
   for (u32 r0 = 0, c = 0; !rc && r0 < m->rows; r0 += per, c++) {
     const u32 r1 = m->rows - r0 < per ? m->rows : r0 + per, b = c & 1u;
-    if (used[b] && (e = H.EventSynchronize(ev[b]))) {
+    if (used[b] && (e = H.EventSynchronize(g_stg_ev[b]))) {
       rc = fail(AMDC_EHIP, "gguf_load: %s", H.GetErrorString(e));
       break;
     }
     if ((rc = amdc_gguf_repack_rows(t, m, r0, r1, nthreads, (uint8_t *)stg[b]))) break;
     if ((e = H.MemcpyAsync((uint8_t *)dev + (u64)r0 * rb, stg[b], (size_t)(r1 - r0) * rb, hipMemcpyHostToDevice, stream)) ||
-        (e = H.EventRecord(ev[b], stream)))
+        (e = H.EventRecord(g_stg_ev[b], stream)))
       rc = fail(AMDC_EHIP, "gguf_load: copy: %s", H.GetErrorString(e));
     used[b] = 1;
   }
-  for (int b = 0; b < 2; b++) { /* every copy out of the staging buffers is done before they go */
-    if (used[b] && (e = H.EventSynchronize(ev[b])) && !rc) rc = fail(AMDC_EHIP, "gguf_load: %s", H.GetErrorString(e));
-    if (ev[b]) H.EventDestroy(ev[b]);
-    if (stg[b]) H.HostFree(stg[b]);
-  }
+  for (int b = 0; b < 2; b++) /* every copy out of the staging buffers is done before the next use */
+    if (used[b] && (e = H.EventSynchronize(g_stg_ev[b])) && !rc) rc = fail(AMDC_EHIP, "gguf_load: %s", H.GetErrorString(e));
   if (rc) {
     H.Free(dev);
     return rc;

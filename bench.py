@@ -282,6 +282,48 @@ def k8_set(seed, timer):
     return out
 
 
+def load_set(seed):
+    """The load of quantized matrices from a GGUF file (amdc_gguf_load: host repack in row chunks
+    on threads into pinned buffers, async copies to the device) against the host repack alone on
+    one thread (the reference's load-time repack_q4k / repack_q6k is single-threaded): GB/s of GGUF
+    bytes, the file in the page cache (read once before timing)."""
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import gguf_writer as gw
+    shapes = [("ffn_up", synth.KIND_Q4_K, 17408, 5120), ("ffn_down", synth.KIND_Q6_K, 5120, 17408),
+              ("attn_q", synth.KIND_Q8_0, 5120, 5120)]
+    tensors, total = [], 0
+    for i, (name, kind, r, c) in enumerate(shapes):
+        src = synth.gguf(kind, r, c, seed + i)
+        tensors.append((name, synth.GGML[kind], (c, r), src.tobytes()))
+        total += src.size
+    out = {}
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "bench.gguf")
+        gw.write(path, [("general.architecture", gw.STR, "bench")], tensors)
+        del tensors
+        with amdc.Gguf(path) as g:
+            for name, _, _, _ in shapes:  # page the file in
+                g.repack(name, 0)
+            t0 = time.perf_counter()
+            for name, _, _, _ in shapes:
+                g.repack(name, 1)
+            t_one = time.perf_counter() - t0
+            mats = []
+            amdc.sync()
+            t0 = time.perf_counter()
+            for name, _, _, _ in shapes:
+                mats.append(g.load(name, 0))
+            amdc.sync()
+            t_load = time.perf_counter() - t0
+            for m in mats:
+                m.free()
+    out = {"gguf_bytes": total, "host_repack_1thread_GBps": round(total / t_one / 1e9, 2),
+           "load_to_device_GBps": round(total / t_load / 1e9, 2), "load_ms": round(t_load * 1e3, 1),
+           "matrices": [f"{n} {synth.GGML[k]} {r}x{c}" for n, k, r, c in shapes]}
+    return out
+
+
 # ---------------------------------------------------------------- CPU baseline
 
 def producers_set(timer):
@@ -393,6 +435,8 @@ def main():
         print(f"bench: producers {json.dumps(detail['producers'])}", file=sys.stderr, flush=True)
         detail["q8_0_q6_k"] = k8_set(a.seed + 4000, timer)
         print(f"bench: q8_0_q6_k {json.dumps(detail['q8_0_q6_k'])}", file=sys.stderr, flush=True)
+        detail["gguf_load"] = load_set(a.seed + 5000)
+        print(f"bench: gguf_load {json.dumps(detail['gguf_load'])}", file=sys.stderr, flush=True)
     cpu = None
     if not a.quick and not a.no_cpu:
         cpu = cpu_baseline(a.seed)

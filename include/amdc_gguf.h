@@ -100,7 +100,7 @@ int amdc_gguf_mat_kind(uint32_t ggml_type);
 int amdc_gguf_mat_info(const amdc_gguf *g, const char *name, amdc_mat *m);
 
 /* Repack tensor `name` into host memory dst (m->bytes after amdc_gguf_mat_info)
- * with nthreads threads (0: one per 8 MiB of weights, at most 16); the same
+ * with nthreads threads (0: one per MiB of weights, at most 16); the same
  * bytes as amdc_repack_q4 / _q8 / _q4k / _q6k of the whole matrix. Host only. */
 int amdc_gguf_repack(const amdc_gguf *g, const char *name, int nthreads, amdc_mat *m, uint8_t *dst);
 
@@ -108,7 +108,9 @@ int amdc_gguf_repack(const amdc_gguf *g, const char *name, int nthreads, amdc_ma
  * and fill it with the repacked matrix in chunks of rows: nthreads threads
  * repack a chunk into one of two pinned staging buffers while the previous
  * chunk's copy runs on `stream` (NULL: the default stream); returns when the
- * matrix is on the device. Free with amdc_mat_release. */
+ * matrix is on the device. The staging buffers (2 x 32 MiB by default,
+ * AMDC_LOAD_CHUNK_KB) stay allocated for later loads until amdc_close; loads
+ * must not run concurrently. Free the matrix with amdc_mat_release. */
 int amdc_gguf_load(const amdc_gguf *g, const char *name, int nthreads, amdc_mat *m, void *stream);
 int amdc_mat_release(amdc_mat *m);
 
