@@ -1569,7 +1569,8 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *
 //   A (16 rows x 64): lane (row i, h) = the nibbles of block (g + h / 2, k),
 //     low (h even) or high (h odd) half: weights 16 (h & 1) .. + 15
 //   B (64 x 16 columns n = t + 8 pp): the 32 activations of token t, block
-//     (g + pp, k), in K half pp, zeros in the other half
+//     (g + pp, k), in K half pp, zeros in the other half (LDS holds only the
+//     nonzero half of each column; the lanes of the other half use 0)
 // so that C[r][t + 8 pp] is the exact integer dot of block (g + pp, k) with
 // vector t (Q4_K: sum q a; Q4_0: sum q a, then - 8 asum; Q8_0: the int8
 // weights of planes 2k, 2k + 1 as A, sum w a). Per element the reference's
@@ -1590,7 +1591,7 @@ template <int KIND>
 __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
                                            u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 xs, u32 ys,
                                            u32 rs, float *__restrict__ part) {
-  __shared__ __attribute__((aligned(16))) u32x4 sB[32][4][16]; // [pair p + 4 k][K quarter][column]: a quarter's columns contiguous
+  __shared__ __attribute__((aligned(16))) u32x4 sB[32][2][16]; // [pair p + 4 k][quarter & 1][column]: a column's nonzero half of K
   __shared__ __attribute__((aligned(16))) float sda[64][8];    // d_a [block of tile][token]
   __shared__ __attribute__((aligned(16))) float sxa[64][8];    // Q4_K: d_a asum; Q4_0: asum (as int bits)
   __shared__ __attribute__((aligned(16))) float ssc[4][64][16]; // per wave: s (Q4_K d sc, Q4_0 d) [block][row]
@@ -1606,11 +1607,6 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
   const __amdgpu_buffer_rsrc_t rxq = rsrc(xq, xn); // the T Q8 rows
   constexpr u32 OOB = 0xFFFFFFF0u;                 // an offset past every resource: the load returns zeros
   const u32 ks = blockIdx.y, nks = gridDim.y, t0 = nt * ks / nks, t1 = nt * (ks + 1u) / nks;
-  // the zero halves of B (never written again)
-  for (u32 i = tid; i < 32u * 16u * 4u; i += NT) {
-    const u32 col = i & 15u, q = (i >> 4) & 3u;
-    if ((q >> 1) != (col >> 3)) (&sB[0][0][0])[i] = (u32x4)(0u);
-  }
   auto gtile = [&](u32 t) { return ng - 8u * t < 8u ? ng - 8u * t : 8u; };
   // the weights of plane k of tile t: this lane's 16 bytes of the 4 pairs
   // (every load unconditional: out-of-range ones read as zeros, so the
@@ -1654,7 +1650,7 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
 #pragma unroll
     for (u32 c = 0; c < 4u; c++) {
       const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, gl = bl >> 3, k = bl & 7u;
-      sB[(gl >> 1) + 4u * k][2u * (gl & 1u) + half][tok + 8u * (gl & 1u)] = ra4[c];
+      sB[(gl >> 1) + 4u * k][half][tok + 8u * (gl & 1u)] = ra4[c];
     }
 #pragma unroll
     for (u32 c = 0; c < 2u; c++) {
@@ -1685,7 +1681,7 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
     for (u32 p = 0; p < 4u; p++) { // the MFMAs of the plane first
       if (p < npair) {
         const u32x4 a = KIND == AMDC_Q8_0 ? wq[p] : (wq[p] >> (4u * (h & 1u))) & 0x0F0F0F0Fu;
-        const u32x4 bq = sB[p + 4u * k][h][n];
+        const u32x4 bq = (h >> 1) == pp ? sB[p + 4u * k][h & 1u][n] : (u32x4)(0u); // the other half of K is zero
         c[p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, bq), (v4i){0, 0, 0, 0}, 0, 0, 0);
       }
     }
@@ -1778,29 +1774,32 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v8(const uint8_
   gemv8_body<AMDC_Q8_0>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
 }
 
-// The verify GEMV for Q6_K (T <= 8): the scale of a Q6_K weight changes every
-// 16 weights, so one v_mfma_i32_16x16x32_i8 per sub-block (g, k):
-//   A (16 rows x 32): lane (row i, h) = q - 32 of weights 8h .. 8h + 7 (half
-//     h >> 1), from its nibble bytes and high-bit word (q6k_dots' packing)
-//   B (32 x 16 columns n = t + 8 hh): activations 16 hh .. 16 hh + 15 of token
-//     t in K rows 16 hh .., zeros in the other half
-// so that C[r][t + 8 hh] = the exact half dot sum (q - 32) a of ie_q6k_dots.
-// Per element acc = fma(s C, d_a, acc) with s = d sc_hh (the reference's
-// fma(fma(s1, d1, s0 d0), d_a, acc) of src/cpu.c:142 regrouped by half); the
-// two half columns of a token are joined at the end. Tiles of 8 super-groups
-// (64 sub-blocks) as gemv8_body: the activations and d_a staged in LDS, each
-// wave's table of d sc per (sub-block, half, row) from the scale panel; the
-// weights from memory one plane ahead (a ring of 4 planes: per plane 8
-// sub-blocks x 12 bytes per lane). Split K over gridDim.y as gemv8_body.
+// The verify GEMV for Q6_K (T <= 8). A Q6_K weight's scale changes every 16
+// weights, so each K quarter of v_mfma_i32_16x16x64_i8 is one half sub-block
+// and each of the 16 columns one (quarter, token) pair:
+//   A (16 rows x 64): lane (row i, h) = q - 32 of the 16 weights of half h & 1
+//     of sub-block (g + h / 2, k) (a pair of super-groups, one plane, as the Q4
+//     pair kernel): its 16 nibble bytes (one 128-bit load) and its half's
+//     high-bit word (one 32-bit load), then ((v | 0x80) - 0x20) ^ 0x80 per byte
+//   B (64 x 16 columns n = 4 q + t): the 16 activations of quarter q for token
+//     t (4 tokens per MFMA, two MFMAs for 8), zeros in the other quarters (LDS
+//     holds only the nonzero quarter of each column; the other lanes use 0)
+// so that C[r][4 q + t] is the exact half dot sum (q - 32) a of ie_q6k_dots for
+// quarter q. Per element acc = fma(s C, d_a, acc), s = d sc of the quarter (the
+// reference's fma(fma(s1, d1, s0 d0), d_a, acc), src/cpu.c:142, regrouped);
+// the four quarters of a token are joined at the end (row_ror 8, then 4).
+// Tiles of 8 super-groups as gemv8_body: activations and d_a staged in LDS in
+// B form, each wave's d sc table per (sub-block, half, row); the weights from
+// memory one plane ahead in a ring of 4 planes. Split K over gridDim.y.
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq,
                                                                    float *__restrict__ y, u32 rows, u32 nb, const float *__restrict__ bias,
                                                                    const float *__restrict__ res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *__restrict__ part) {
-  __shared__ __attribute__((aligned(16))) u32x2 sB[64][4][16];     // [sub-block of tile][K quarter][column]
-  __shared__ __attribute__((aligned(16))) float sda[64][8];        // d_a [sub-block][token]
+  __shared__ __attribute__((aligned(16))) u32x4 sB[2][32][16]; // [token half][pair p + 4 k][column]: the column's nonzero quarter
+  __shared__ __attribute__((aligned(16))) float sda[64][8];       // d_a [sub-block][token]
   __shared__ __attribute__((aligned(16))) float ssc[4][64][2][16]; // per wave: d sc [sub-block][half][row]
   const u32 ng = nb >> 3, nt = (ng + 7u) >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
-  const u32 i16 = lane & 15u, h = lane >> 4, n = i16, tk = n & 7u, hh = n >> 3;
+  const u32 i16 = lane & 15u, h = lane >> 4, n = i16, qn = n >> 2, tq = n & 3u;
   const u32 RB = (u32)amdc_q6k_row_bytes(nb);
   const u32 rt0 = blockIdx.x * 64u, r0 = rt0 + 16u * w, ra = r0 + i16 < rows ? r0 + i16 : rows - 1u;
   const __amdgpu_buffer_rsrc_t rw = rsrc(W + (u64)rt0 * RB, (u32)min((u64)(rows - rt0) * RB, (u64)0xFFFFFFF0u));
@@ -1808,21 +1807,16 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
   const __amdgpu_buffer_rsrc_t rxq = rsrc(xq, (u32)min((u64)T * xs, (u64)0xFFFFFFF0u));
   constexpr u32 OOB = 0xFFFFFFF0u;
   const u32 ks = blockIdx.y, nks = gridDim.y, t0 = nt * ks / nks, t1 = nt * (ks + 1u) / nks;
-  for (u32 i = tid; i < 64u * 4u * 16u; i += NT) { // the zero halves of B
-    const u32 col = i & 15u, q = (i >> 4) & 3u;
-    if ((q >> 1) != (col >> 3)) (&sB[0][0][0])[i] = (u32x2)(0u);
-  }
   auto gtile = [&](u32 t) { return ng - 8u * t < 8u ? ng - 8u * t : 8u; };
-  // plane k of tile t: per super-group gl, the lane's 8 nibble bytes and its half's high-bit word
-  auto load_plane = [&](u32 t, u32 k, u32 (&wq)[8][3]) {
+  // plane k of tile t: per pair p, the 16 nibble bytes of sub-block (2p + h / 2, k) and the high word of half h & 1
+  auto load_plane = [&](u32 t, u32 k, u32x4 (&wq)[4], u32 (&hq)[4]) {
     const u32 gt = gtile(t);
 #pragma unroll
-    for (u32 gl = 0; gl < 8u; gl++) {
-      const u32 g = 8u * t + gl;
-      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rw, gl < gt ? wo + (u32)amdc_q6k_nib_off(ng, g, k) + 8u * (h & 1u) : OOB, 0, 0);
-      wq[gl][0] = v.x, wq[gl][1] = v.y;
-      wq[gl][2] = __builtin_amdgcn_raw_buffer_load_b32(
-          rw, gl < gt ? wo + (u32)amdc_q6k_hi_off(ng, g, k >> 1) + 8u * (k & 1u) + 4u * (h >> 1) : OOB, 0, 0);
+    for (u32 p = 0; p < 4u; p++) {
+      const u32 gl = 2u * p + (h >> 1), g = 8u * t + gl;
+      wq[p] = __builtin_amdgcn_raw_buffer_load_b128(rw, gl < gt ? wo + (u32)amdc_q6k_nib_off(ng, g, k) : OOB, 0, 0);
+      hq[p] = __builtin_amdgcn_raw_buffer_load_b32(rw, gl < gt ? wo + (u32)amdc_q6k_hi_off(ng, g, k >> 1) + 8u * (k & 1u) + 4u * (h & 1u) : OOB,
+                                                   0, 0);
     }
   };
   u32x4 ra4[4];
@@ -1852,10 +1846,10 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
   };
   auto stage_tile = [&]() {
 #pragma unroll
-    for (u32 c = 0; c < 4u; c++) {
-      const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7;
-      sB[bl][2u * half][tok + 8u * half] = (u32x2){ra4[c].x, ra4[c].y};
-      sB[bl][2u * half + 1u][tok + 8u * half] = (u32x2){ra4[c].z, ra4[c].w};
+    for (u32 c = 0; c < 4u; c++) { // (half, sub-block (gl, k), token) -> quarter 2 (gl & 1) + half of pair gl / 2
+      const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, gl = bl >> 3, k = bl & 7u;
+      const u32 q = 2u * (gl & 1u) + half;
+      sB[tok >> 2][(gl >> 1) + 4u * k][4u * q + (tok & 3u)] = ra4[c];
     }
 #pragma unroll
     for (u32 c = 0; c < 2u; c++) {
@@ -1873,65 +1867,88 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
           ssc[w][8u * gl + k][e][i16] = d * (float)(int)(int8_t)(hword(rh[q], k >> 1) >> (16u * (k & 1u) + 8u * e));
     }
   };
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  auto plane = [&](u32 k, u32 gt, const u32 (&wq)[8][3]) {
-    v4i c[8];
-    const u32 sft = 4u * (h >> 1), hs = 4u * (h & 1u);
+  float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+  const u32 nth = T > 4u ? 2u : 1u; // token halves with tokens
+  auto plane = [&](u32 k, u32 npair, const u32x4 (&wq)[4], const u32 (&hq)[4]) {
+    v4i c[2][4];
+    const u32 sft = 4u * (h & 1u);
 #pragma unroll
-    for (u32 gl = 0; gl < 8u; gl++) { // the MFMAs of the plane first
-      if (gl < gt) {
-        const u32 v0 = ((wq[gl][0] >> sft) & 0x0F0F0F0Fu) | (((wq[gl][2] >> hs) & 0x03030303u) << 4);
-        const u32 v1 = ((wq[gl][1] >> sft) & 0x0F0F0F0Fu) | (((wq[gl][2] >> (hs + 2u)) & 0x03030303u) << 4);
-        const u32 s0 = ((v0 | 0x80808080u) - 0x20202020u) ^ 0x80808080u, s1 = ((v1 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
-        const u32x2 bq = sB[8u * gl + k][h][n];
-        c[gl] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)((u64)s0 | ((u64)s1 << 32)), (long)((u64)bq.x | ((u64)bq.y << 32)),
-                                                      (v4i){0, 0, 0, 0}, 0, 0, 0);
+    for (u32 p = 0; p < 4u; p++) { // the MFMAs of the plane first
+      if (p < npair) {
+        u32 a[4];
+#pragma unroll
+        for (u32 i = 0; i < 4u; i++) {
+          const u32 v = ((wq[p][i] >> sft) & 0x0F0F0F0Fu) | (((hq[p] >> (2u * i)) & 0x03030303u) << 4);
+          a[i] = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+        }
+        const v4i av = {(int)a[0], (int)a[1], (int)a[2], (int)a[3]};
+#pragma unroll
+        for (u32 th = 0; th < 2u; th++)
+          if (th < nth)
+            c[th][p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, h == qn ? __builtin_bit_cast(v4i, sB[th][p + 4u * k][n]) : (v4i){0, 0, 0, 0},
+                                                             (v4i){0, 0, 0, 0}, 0, 0, 0);
       }
     }
 #pragma unroll
-    for (u32 gl = 0; gl < 8u; gl++) {
-      if (gl >= gt) break;
-      const u32 bl = 8u * gl + k;
-      const v4f s4 = *(const v4f *)&ssc[w][bl][hh][4u * h];
-      const float da = sda[bl][tk];
+    for (u32 p = 0; p < 4u; p++) {
+      if (p >= npair) break;
+      const u32 bl = 8u * (2u * p + (qn >> 1)) + k; // this lane's sub-block (column quarter qn)
+      const v4f s4 = *(const v4f *)&ssc[w][bl][qn & 1u][4u * h];
 #pragma unroll
-      for (u32 v = 0; v < 4u; v++) acc[v] = __builtin_fmaf(s4[v] * (float)c[gl][v], da, acc[v]);
+      for (u32 th = 0; th < 2u; th++) {
+        if (th >= nth) break;
+        const float da = sda[bl][tq + 4u * th];
+#pragma unroll
+        for (u32 v = 0; v < 4u; v++) acc[th][v] = __builtin_fmaf(s4[v] * (float)c[th][p][v], da, acc[th][v]);
+      }
     }
   };
-  u32 wq[4][8][3];
+  u32x4 wq[4][4];
+  u32 hq[4][4];
   if (t0 < t1) {
     fetch_tile(t0);
 #pragma unroll
-    for (u32 k = 0; k < 4u; k++) load_plane(t0, k, wq[k]);
+    for (u32 k = 0; k < 4u; k++) load_plane(t0, k, wq[k], hq[k]);
   }
   for (u32 t = t0; t < t1; t++) {
     const bool more = t + 1u < t1;
-    const u32 gt = gtile(t);
+    const u32 npair = (gtile(t) + 1u) >> 1;
     __syncthreads();
     stage_tile();
     __syncthreads();
     if (more) fetch_tile(t + 1u);
 #pragma unroll
     for (u32 k = 0; k < 8u; k++) {
-      plane(k, gt, wq[k & 3u]);
-      if (k < 4u) load_plane(t, k + 4u, wq[k & 3u]);
-      else if (more) load_plane(t + 1u, k - 4u, wq[k & 3u]);
+      plane(k, npair, wq[k & 3u], hq[k & 3u]);
+      if (k < 4u) load_plane(t, k + 4u, wq[k & 3u], hq[k & 3u]);
+      else if (more) load_plane(t + 1u, k - 4u, wq[k & 3u], hq[k & 3u]);
     }
   }
+  // join the four quarters of each token (columns t, t + 4, t + 8, t + 12 of a row of 16 lanes)
 #pragma unroll
-  for (u32 v = 0; v < 4u; v++) acc[v] += dpp<0x128>(acc[v]); // row_ror:8: the two halves of a token
-  if (hh == 0u && tk < T) {
+  for (u32 th = 0; th < 2u; th++)
 #pragma unroll
     for (u32 v = 0; v < 4u; v++) {
-      const u32 r = r0 + 4u * h + v;
-      if (r >= rows) continue;
-      if (part) {
-        part[((u64)ks * T + tk) * rows + r] = acc[v];
-      } else {
-        float o = acc[v];
-        if (bias) o = o + bias[r];
-        if (res) o = res[(u64)tk * rs + r] + o;
-        y[(u64)tk * ys + r] = o;
+      acc[th][v] += dpp<0x128>(acc[th][v]); // row_ror:8
+      acc[th][v] += dpp<0x124>(acc[th][v]); // row_ror:4
+    }
+  if (qn == 0u) {
+#pragma unroll
+    for (u32 th = 0; th < 2u; th++) {
+      const u32 tk = tq + 4u * th;
+      if (tk >= T) continue;
+#pragma unroll
+      for (u32 v = 0; v < 4u; v++) {
+        const u32 r = r0 + 4u * h + v;
+        if (r >= rows) continue;
+        if (part) {
+          part[((u64)ks * T + tk) * rows + r] = acc[th][v];
+        } else {
+          float o = acc[th][v];
+          if (bias) o = o + bias[r];
+          if (res) o = res[(u64)tk * rs + r] + o;
+          y[(u64)tk * ys + r] = o;
+        }
       }
     }
   }
