@@ -260,7 +260,8 @@ def prefill_set(steps, seed, timer):
 def k8_set(seed, timer):
     """The Q8_0 and Q6_K decode GEMVs at the sizes they have in the c1 / c2 models (the Q6_K
     matrices of a Q4_K_M file: ffn_down, attn_v, lm_head; Q8_0 projections): us per launch and the
-    GGUF weight bytes per second, at T = 1 and for the T = 8 verify (weights read once)."""
+    GGUF weight bytes per second, at T = 1 and for the T = 8 verify (weights read once); TOPS of the
+    T = 256 prefill GEMM on the ffn-sized ones."""
     out = {}
     sets = [(synth.KIND_Q8_0, "q8_0_q", 4096, 4096), (synth.KIND_Q8_0, "q8_0_gate", 11008, 4096),
             (synth.KIND_Q8_0, "q8_0_down", 4096, 11008), (synth.KIND_Q6_K, "q6_k_ffn_down", 5120, 17408),
@@ -278,6 +279,15 @@ def k8_set(seed, timer):
         out[name] = {"rows": r, "cols": c, "us": round(t * 1e3, 3), "GB/s": round(b / t / 1e6, 1),
                      "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4), "T8_us": round(t8 * 1e3, 3),
                      "T8_GB/s": round(b / t8 / 1e6, 1)}
+        if r * c >= 4096 * 11008 and r * c < 10 ** 9:  # the prefill GEMM at T = 256 on the ffn-sized matrices
+            T = 256
+            X2 = amdc.DevBuf.of(synth.activations(T, c, seed + 95 + i))
+            Q2, Y2 = amdc.DevBuf(T * xs), amdc.DevBuf(4 * T * r)
+            amdc.quant_q8(X2, Q2, nb, T, 4 * c, xs)
+            amdc.gemm(kind, M.dev[0][0], Q2, Y2, r, nb, T, xs, r)  # sizes the workspace before the capture
+            tg = timer.per_launch_ms(lambda j, s: amdc.gemm(kind, M.dev[j % M.copies][0], Q2, Y2, r, nb, T, xs, r, stream=s), M.copies, reps=2)
+            out[name].update({"T256_us": round(tg * 1e3, 1), "T256_TOPS": round(2.0 * T * r * c / tg / 1e9, 1)})
+            del X2, Q2, Y2
         del M
     return out
 
@@ -400,6 +410,8 @@ def main():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--quick", action="store_true", help="headline only (no c0/c2/c3/c4 detail, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sets", default="c0,c2,c3,c4,producers,k8,load",
+                    help="detail sets to run after the headline (comma list of c0, c2, c3, c4, producers, k8, load)")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run the probe copy kernel over 256 MiB 3 times (the FETCH_SIZE / WRITE_SIZE yardstick)")
     a = ap.parse_args()
@@ -423,20 +435,19 @@ def main():
     value = c1["set_bytes"] / (c1["ms_per_step"] * 1e-3) / 1e9
     print(f"bench: c1 {value:.1f} GB/s per step, kernels {c1['kernel_GBps']:.1f} GB/s", file=sys.stderr, flush=True)
     detail = {"c1": c1}
-    if not a.quick:
-        for name in ("c0", "c2"):
+    sets = set() if a.quick else set(a.sets.split(","))
+    for name in ("c0", "c2"):
+        if name in sets:
             detail[name] = gemv_set(name, a.steps, 2, a.seed + 1000, timer)
             print(f"bench: {name} kernels {detail[name]['kernel_GBps']:.1f} GB/s", file=sys.stderr, flush=True)
-        detail["c3"] = verify_set(a.steps, a.seed + 2000, timer)
-        print(f"bench: c3 {json.dumps(detail['c3'])}", file=sys.stderr, flush=True)
-        detail["c4"] = prefill_set(a.steps, a.seed + 3000, timer)
-        print(f"bench: c4 {json.dumps(detail['c4'])}", file=sys.stderr, flush=True)
-        detail["producers"] = producers_set(timer)
-        print(f"bench: producers {json.dumps(detail['producers'])}", file=sys.stderr, flush=True)
-        detail["q8_0_q6_k"] = k8_set(a.seed + 4000, timer)
-        print(f"bench: q8_0_q6_k {json.dumps(detail['q8_0_q6_k'])}", file=sys.stderr, flush=True)
-        detail["gguf_load"] = load_set(a.seed + 5000)
-        print(f"bench: gguf_load {json.dumps(detail['gguf_load'])}", file=sys.stderr, flush=True)
+    for key, name, fn in (("c3", "c3", lambda: verify_set(a.steps, a.seed + 2000, timer)),
+                          ("c4", "c4", lambda: prefill_set(a.steps, a.seed + 3000, timer)),
+                          ("producers", "producers", lambda: producers_set(timer)),
+                          ("k8", "q8_0_q6_k", lambda: k8_set(a.seed + 4000, timer)),
+                          ("load", "gguf_load", lambda: load_set(a.seed + 5000))):
+        if key in sets:
+            detail[name] = fn()
+            print(f"bench: {name} {json.dumps(detail[name])}", file=sys.stderr, flush=True)
     cpu = None
     if not a.quick and not a.no_cpu:
         cpu = cpu_baseline(a.seed)
