@@ -96,6 +96,7 @@ ABI = {
     "amdc_quant_q8": (C.c_int, [_P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_gemv_q4": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
     "amdc_gemv_q4k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
+    "amdc_gemm_q4": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_gemm_q8": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_gemm_q6k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_gemv_q8": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _P]),
@@ -388,7 +389,7 @@ def gemm_q4k(w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stream=No
 
 
 def gemm(kind, w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=None, stream=None):
-    """The prefill GEMM of a Q4_K, Q8_0 or Q6_K matrix."""
+    """The prefill GEMM of a matrix of any kind."""
     f = getattr(lib(), "amdc_gemm_" + _SUF[kind])
     _check(f(_p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), T, xs, ys, rs, stream))
 

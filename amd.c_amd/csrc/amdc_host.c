@@ -272,6 +272,8 @@ enum {
   K_GEMMH_Q6K_N64,
   K_GEMV_Q8_V8,
   K_GEMV_Q6K_V8,
+  K_GEMMH_Q4_N128,
+  K_GEMMH_Q4_N64,
   K_N
 };
 static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1",  "amdc_gemv_q4_k_t1",  "amdc_gemv_q4_0_t1u1",
@@ -284,7 +286,7 @@ static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1
                                        "amdc_chain",          "amdc_rmsnorm_q8",    "amdc_swiglu_q8",     "amdc_gemv_q8_0_p2",
                                        "amdc_gemv_q6_k_p2",   "amdc_dots_q8_0",     "amdc_dots_q6_k",     "amdc_gemmh_q8_0_m64_n128",
                                        "amdc_gemmh_q8_0_m64_n64", "amdc_gemmh_q6_k_m64_n128", "amdc_gemmh_q6_k_m64_n64",
-                                       "amdc_gemv_q8_0_v8",   "amdc_gemv_q6_k_v8"};
+                                       "amdc_gemv_q8_0_v8",   "amdc_gemv_q6_k_v8",  "amdc_gemmh_q4_0_m64_n128", "amdc_gemmh_q4_0_m64_n64"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -834,7 +836,7 @@ static const struct {
   u32 mr, nt, threads;
 } gh[2] = {{K_GEMMH_M64_N128, 64, 128, 256}, {K_GEMMH_M64_N64, 64, 64, 256}};
 
-/* The prefill GEMM of a kind with an f16-MFMA kernel (Q4_K, Q8_0, Q6_K). */
+/* The prefill GEMM on the f16-MFMA kernels (every kind). */
 static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                        const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
   NEED_OPEN();
@@ -877,6 +879,7 @@ static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *x
   void *ga[] = {&w, &xh, &da, &xa, &y, &rows, &nb, &bias, &res, &T, (void *)&Tp, &ys, &rs, &part};
   const int kk = kind == AMDC_KIND_Q8_0 ? (v ? K_GEMMH_Q8_N64 : K_GEMMH_Q8_N128)
                  : kind == AMDC_KIND_Q6_K ? (v ? K_GEMMH_Q6K_N64 : K_GEMMH_Q6K_N128)
+                 : kind == AMDC_KIND_Q4_0 ? (v ? K_GEMMH_Q4_N64 : K_GEMMH_Q4_N128)
                                           : gh[v].k;
   HIPCALL(H.ModuleLaunchKernel(g_k[kk], (unsigned)grid, ks, 1, gh[v].threads, 1, 1, 0, stream, ga, NULL));
   if (ks > 1u) {
@@ -890,6 +893,11 @@ static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *x
 int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                   uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
   return gemm_launch(AMDC_KIND_Q4_K, "gemm_q4k", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+}
+
+int amdc_gemm_q4(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                 uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  return gemm_launch(AMDC_KIND_Q4_0, "gemm_q4", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
 }
 
 int amdc_gemm_q8(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
@@ -909,7 +917,7 @@ int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t 
     int rc = check_mat("op_gemv", kind, w, xq, y, rows, nb);
     return rc ? rc : gemv_launch(kind, w, xq, y, rows, nb, bias, res, 1, 0, 0, 0, stream);
   }
-  if (kind != AMDC_KIND_Q4_0 && (int)T >= t_gemm_min) return gemm_launch(kind, "op_gemv", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+  if ((int)T >= t_gemm_min) return gemm_launch(kind, "op_gemv", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
   return gemv_t(kind, "op_gemv", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
 }
 

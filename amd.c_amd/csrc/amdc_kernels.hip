@@ -1245,6 +1245,19 @@ __device__ __forceinline__ h8 a_frag_q8(u32 w0, u32 w1) {
   return (h8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
+// The A operand of a Q4_0 block tile: lane (row i, h) holds weights 8h..8h+7
+// as q - 8 in f16 (exact): the nibbles of bytes 8 (h & 1) .. + 7 (low for
+// h < 2), in the mantissa of 1024, then - 1032.
+__device__ __forceinline__ h8 a_frag_q40(u32 w0, u32 w1, u32 h) {
+  const u32 sft = (h >> 1) * 4u;
+  h2 p0, p1, p2, p3;
+  nib_to_h((w0 >> sft) & 0x0F0F0F0Fu, p0, p1);
+  nib_to_h((w1 >> sft) & 0x0F0F0F0Fu, p2, p3);
+  const h2 c = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  p0 += c, p1 += c, p2 += c, p3 += c;
+  return (h8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
 // The A operands of a Q6_K sub-block tile: lane (row i, h) holds weights
 // 8h..8h+7, of half h >> 1, as (q - 32) sc split into hi = (q - 32) 16 (sc >> 4)
 // and lo = (q - 32) (sc & 15), both exact in f16 (|.| <= 4096, multiples of
@@ -1301,7 +1314,7 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
   __shared__ __attribute__((aligned(16))) _Float16 sb[2][NTT * BSTR];
   __shared__ __attribute__((aligned(16))) float sda[2][2][NTT];
   __shared__ __attribute__((aligned(16))) float sxa[2][8][NTT]; // d_a asum of a super-block's 8 blocks, by parity
-  const u32 ng = KIND == AMDC_Q8_0 ? amdc_ngroups(nb) : nb >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6, wm = w & 1u, wn = w >> 1;
+  const u32 ng = KIND == AMDC_Q8_0 || KIND == AMDC_Q4_0 ? amdc_ngroups(nb) : nb >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6, wm = w & 1u, wn = w >> 1;
   const u32 i16 = lane & 15u, h = lane >> 4;
   const u32 ntt = (T + NTT - 1u) / NTT, tt = blockIdx.x % ntt, rt = blockIdx.x / ntt;
   const u32 tbase = tt * NTT, twave = 16u * NJ * wn;
@@ -1390,6 +1403,8 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
   auto frag = [&](const u32(&wk)[3], u32 i, u32 k, h8 &a0, h8 &a1) {
     if constexpr (KIND == AMDC_Q8_0) {
       a0 = a_frag_q8(wk[0], wk[1]);
+    } else if constexpr (KIND == AMDC_Q4_0) {
+      a0 = a_frag_q40(wk[0], wk[1], h);
     } else if constexpr (KIND == AMDC_Q6_K) {
       const int sc = (int)(int8_t)(hword(hd[i], k >> 1) >> (16u * (k & 1u) + 8u * (h >> 1)));
       a_frag_q6(wk[0], wk[1], wk[2], h, sc, a0, a1);
@@ -1410,8 +1425,8 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
       float dj[NJ];
 #pragma unroll
       for (u32 j = 0; j < NJ; j++) dj[j] = sda[bf][bb][twave + 16u * j + i16];
-      float dw[2][4]; // Q8_0: the block's d of the C rows 4h + v of each row tile
-      if constexpr (KIND == AMDC_Q8_0) {
+      float dw[2][4]; // Q8_0, Q4_0: the block's d of the C rows 4h + v of each row tile
+      if constexpr (KIND == AMDC_Q8_0 || KIND == AMDC_Q4_0) {
 #pragma unroll
         for (u32 i = 0; i < 2u; i++) {
           const float dr = h2f(hword(hd[i], (kb + bb) >> 1) >> (16u * ((kb + bb) & 1u)));
@@ -1441,7 +1456,7 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
         for (u32 j = 0; j < NJ; j++)
 #pragma unroll
           for (u32 v = 0; v < 4u; v++) {
-            if constexpr (KIND == AMDC_Q8_0) // (d_w d_a) dot, as src/cpu.c:168
+            if constexpr (KIND == AMDC_Q8_0 || KIND == AMDC_Q4_0) // (d_w d_a) dot, as src/cpu.c:81, 168
               acc[i][j][v] = __builtin_fmaf(dw[i][v] * dj[j], x[j][v], acc[i][j][v]);
             else
               tmp[i][j][v] = __builtin_fmaf(dj[j], x[j][v], tmp[i][j][v]);
@@ -1451,7 +1466,7 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
   };
   // the end of a super-block: d, and the min term from the 8 blocks' d_a asum
   auto close_group = [&](u32 gp) {
-    if constexpr (KIND == AMDC_Q8_0) return;
+    if constexpr (KIND == AMDC_Q8_0 || KIND == AMDC_Q4_0) return;
 #pragma unroll
     for (u32 i = 0; i < 2u; i++) {
       const float dmine = KIND == AMDC_Q6_K ? h2f(hdd[i]) : h2f(hd[i].x), dmn = h2f(hd[i].x >> 16);
@@ -1540,6 +1555,8 @@ GEMMH_KERNEL(amdc_gemmh_q8_0_m64_n128, 4, AMDC_Q8_0)
 GEMMH_KERNEL(amdc_gemmh_q8_0_m64_n64, 2, AMDC_Q8_0)
 GEMMH_KERNEL(amdc_gemmh_q6_k_m64_n128, 4, AMDC_Q6_K)
 GEMMH_KERNEL(amdc_gemmh_q6_k_m64_n64, 2, AMDC_Q6_K)
+GEMMH_KERNEL(amdc_gemmh_q4_0_m64_n128, 4, AMDC_Q4_0)
+GEMMH_KERNEL(amdc_gemmh_q4_0_m64_n64, 2, AMDC_Q4_0)
 
 // The split-K sums: y[t][r] = part[0][t][r] + part[1][t][r] + ... (in split
 // order), then the epilogue. All nks (<= 16) loads are issued before the

@@ -205,13 +205,20 @@ int amdc_gemm_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uin
  * workspace as amdc_gemm_q4k. */
 int amdc_gemm_q8(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                  uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
+/* Q4_0 (any nb): the block's q - 8 as f16 on the f16 MFMA, then (d_w d_a) sum
+ * per block as src/cpu.c:81. No reference counterpart (the reference runs
+ * OP_GEMV_Q4 per token, src/hip.c:1583-1588); y within 1e-5 of cpu_gemv_q4
+ * per token row. */
+int amdc_gemm_q4(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                 uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 int amdc_gemm_q6k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                   uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 
 /* The dispatch of launch_op for OP_GEMV_Q4 / OP_GEMV_Q8 / OP_GEMV_Q4K /
  * OP_GEMV_Q6K over T tokens (src/hip.c:928-1089): T == 1 -> the decode GEMV;
- * Q4_K, Q8_0 and Q6_K with T >= IE_GEMM_MIN (env, default 17) -> the GEMM;
- * else the multi-vector GEMV. kind: any AMDC_KIND_*. */
+ * T >= IE_GEMM_MIN (env, default 17) -> the GEMM (Q4_0 included, where the
+ * reference runs one GEMV per token); else the multi-vector GEMV. kind: any
+ * AMDC_KIND_*. */
 int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                  const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 

@@ -128,11 +128,13 @@ def test_errors_do_not_launch(dev, orc):
 
 
 @pytest.mark.parametrize("kind,rows,nb,T", [(Q8, 1, 1, 17), (Q8, 63, 13, 64), (Q8, 130, 128, 65), (Q8, 70, 344, 33), (Q8, 300, 40, 256),
-                                            (Q6, 1, 8, 17), (Q6, 63, 16, 64), (Q6, 64, 160, 65), (Q6, 130, 40, 130), (Q6, 70, 544, 33)])
+                                            (Q6, 1, 8, 17), (Q6, 63, 16, 64), (Q6, 64, 160, 65), (Q6, 130, 40, 130), (Q6, 70, 544, 33),
+                                            (0, 1, 1, 17), (0, 63, 13, 64), (0, 130, 128, 65), (0, 70, 344, 33), (0, 300, 40, 256)])
 @pytest.mark.parametrize("ks", [0, 3])
 def test_gemm(dev, orc, kind, rows, nb, T, ks):
     """The prefill GEMM (f16 MFMA, exact integer block sums) against the oracle per token row, with a
-    bias, with and without split K."""
+    bias, with and without split K; Q8_0, Q6_K and the Q4_0 form (no reference kernel: the reference
+    runs one GEMV per token)."""
     c = Case(dev, orc, kind, rows, nb, T, seed=rows + T + kind)
     assert np.array_equal(c.quant(), c.xq)
     ng = (nb + 7) // 8
