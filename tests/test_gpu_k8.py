@@ -215,3 +215,47 @@ def test_verify_splitk(dev, orc, kind, rows, nb, T):
     y = c.y_gpu()
     for t in range(T):
         assert rel_err(y[t], orc.epilogue(c.y_oracle(t), bias, res[t]), c.mag(t) + np.abs(bias) + np.abs(res[t])) < TOL, t
+
+
+def test_graph_replay_matches_eager(dev, orc):
+    """Q8_0 / Q6_K decode, split-K verify and GEMM (and the Q4_0 GEMM) captured in one graph and replayed
+    several times, with eager work and synchronizations between the replays: every replay equals the
+    eager run bit for bit (no node of the graph depends on memory set outside it)."""
+    cases = [Case(dev, orc, Q8, 96, 136, 20, seed=4), Case(dev, orc, Q6, 80, 160, 20, seed=5), Case(dev, orc, 0, 64, 72, 20, seed=6)]
+    outs = []
+    for c in cases:
+        c.quant()
+        outs.append((dev.DevBuf(4 * c.rows), dev.DevBuf(4 * c.rows * 8), dev.DevBuf(4 * c.rows * c.T)))
+    S = dev.Stream()
+
+    def ops(s):
+        for c, (Y1, Y8, YG) in zip(cases, outs):
+            if c.kind != 0:
+                dev.gemv(c.kind, c.W, c.Q, Y1, c.rows, c.nb, stream=s)
+                dev.gemv_t(c.kind, c.W, c.Q, Y8, c.rows, c.nb, 8, c.xs, c.rows, stream=s)
+            dev.gemm(c.kind, c.W, c.Q, YG, c.rows, c.nb, c.T, c.xs, c.rows, stream=s)
+
+    bufs = [b for o in outs for b in o]
+    for b in bufs:
+        b.fill(0)
+    dev.set_tuning(gemm_ksplit=3)  # split K in the verify kernels and the GEMMs: partial sums in the workspace
+    ops(None)
+    dev.sync()
+    want = [b.download(np.uint32) for b in bufs]
+    g = dev.Graph(S, ops)
+    other = Case(dev, orc, Q6, 64, 64, seed=9)
+    for rep in range(3):
+        for b in bufs:
+            b.fill(0)
+        other.quant()
+        dev.gemv(Q6, other.W, other.Q, other.Y, 64, 64)  # eager work between replays
+        dev.sync()
+        g.launch()
+        S.sync()
+        for b, w in zip(bufs, want):
+            assert np.array_equal(b.download(np.uint32), w), rep
+    for c, (Y1, _, YG) in zip(cases, outs):
+        if c.kind != 0:
+            assert rel_err(Y1.download(np.float32), c.y_oracle(0), c.mag(0)) < TOL
+        y = YG.download(np.float32).reshape(c.T, c.rows)
+        assert rel_err(y[c.T - 1], c.y_oracle(c.T - 1), c.mag(c.T - 1)) < TOL
