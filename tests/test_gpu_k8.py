@@ -259,3 +259,23 @@ def test_graph_replay_matches_eager(dev, orc):
             assert rel_err(Y1.download(np.float32), c.y_oracle(0), c.mag(0)) < TOL
         y = YG.download(np.float32).reshape(c.T, c.rows)
         assert rel_err(y[c.T - 1], c.y_oracle(c.T - 1), c.mag(c.T - 1)) < TOL
+
+
+@pytest.mark.parametrize("kind,nb", [(0, 511), (0, 3000), (synth.KIND_Q4_K, 2040), (Q8, 2047), (Q6, 2040)])
+def test_max_sizes(dev, orc, kind, nb):
+    """The largest rows the reference's loader accepts for each kind (core/ie_core.h:60, 187, 258-260:
+    Q4_0 nb < 512, Q8_0 nb < 2048, Q4_K / Q6_K nb < 2048 with nb % 8 == 0; Q4_0 also past the
+    reference's limit, where it would switch to Q8_0): decode, verify (T = 8) and GEMM (T = 20)."""
+    rows = 37
+    c = Case(dev, orc, kind, rows, nb, 20, seed=nb)
+    c.quant()
+    dev.gemv(kind, c.W, c.Q, c.Y, rows, nb)
+    assert rel_err(c.y_gpu()[0], c.y_oracle(0), c.mag(0)) < TOL
+    dev.gemv_t(kind, c.W, c.Q, c.Y, rows, nb, 8, c.xs, rows)
+    y = c.y_gpu()
+    for t in (0, 7):
+        assert rel_err(y[t], c.y_oracle(t), c.mag(t)) < TOL, t
+    dev.op_gemv(kind, c.W, c.Q, c.Y, rows, nb, 20, c.xs, rows)
+    y = c.y_gpu()
+    for t in (0, 19):
+        assert rel_err(y[t], c.y_oracle(t), c.mag(t)) < TOL, t
