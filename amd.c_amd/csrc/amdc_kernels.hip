@@ -1314,6 +1314,8 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
   __shared__ __attribute__((aligned(16))) _Float16 sb[2][NTT * BSTR];
   __shared__ __attribute__((aligned(16))) float sda[2][2][NTT];
   __shared__ __attribute__((aligned(16))) float sxa[2][8][NTT]; // d_a asum of a super-block's 8 blocks, by parity
+  constexpr bool PB = KIND == AMDC_Q8_0 || KIND == AMDC_Q4_0;     // a d per (row, block): applied per block
+  __shared__ __attribute__((aligned(16))) float sdw[PB ? 4 : 1][2][8][16]; // per wave: d [row tile][block][row]
   const u32 ng = KIND == AMDC_Q8_0 || KIND == AMDC_Q4_0 ? amdc_ngroups(nb) : nb >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6, wm = w & 1u, wn = w >> 1;
   const u32 i16 = lane & 15u, h = lane >> 4;
   const u32 ntt = (T + NTT - 1u) / NTT, tt = blockIdx.x % ntt, rt = blockIdx.x / ntt;
@@ -1413,6 +1415,15 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
     }
   };
   auto compute = [&](u32 kb, u32 bf, const u32(&wv)[2][2][3]) {
+    if constexpr (PB) {
+      if (kb == 0u) { // a super-group's first stage: the d's of the lane's A rows into the wave's table (blocks 2h, 2h + 1)
+#pragma unroll
+        for (u32 i = 0; i < 2u; i++)
+#pragma unroll
+          for (u32 e = 0; e < 2u; e++) sdw[w][i][2u * h + e][i16] = h2f(hword(hd[i], h) >> (16u * e));
+        __asm__ volatile("" ::: "memory"); // the table's stores stay ahead of its loads (one wave: LDS keeps their order)
+      }
+    }
     const _Float16 *lb = &sb[bf][(twave + i16) * BSTR + 8u * h];
     h8 bq[NJ];
 #pragma unroll
@@ -1425,14 +1436,10 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
       float dj[NJ];
 #pragma unroll
       for (u32 j = 0; j < NJ; j++) dj[j] = sda[bf][bb][twave + 16u * j + i16];
-      float dw[2][4]; // Q8_0, Q4_0: the block's d of the C rows 4h + v of each row tile
-      if constexpr (KIND == AMDC_Q8_0 || KIND == AMDC_Q4_0) {
+      v4f dw[2]; // Q8_0, Q4_0: the block's d of the C rows 4h + v of each row tile
+      if constexpr (PB) {
 #pragma unroll
-        for (u32 i = 0; i < 2u; i++) {
-          const float dr = h2f(hword(hd[i], (kb + bb) >> 1) >> (16u * ((kb + bb) & 1u)));
-#pragma unroll
-          for (u32 v = 0; v < 4u; v++) dw[i][v] = __shfl(dr, (int)(4u * h + v));
-        }
+        for (u32 i = 0; i < 2u; i++) dw[i] = *(const v4f *)&sdw[w][i][kb + bb][4u * h];
       }
 #pragma unroll
       for (u32 i = 0; i < 2u; i++) { // a row tile at a time: NJ MFMAs in flight, then their fmas
