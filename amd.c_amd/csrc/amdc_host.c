@@ -856,7 +856,9 @@ static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *x
    * the K split doubles until the workgroups number three per CU (measured
    * best on the c4 shapes: 17408 x 5120 split 2, 5120 x 17408 split 8) */
   const u32 ng = amdc_ngroups(nb), cus = g_cus > 0 ? (u32)g_cus : 256u;
-  const int v = t_gemm >= 3 ? t_gemm - 3 : (T > 64u ? 0 : 1);
+  /* 64-token tiles for Q4_0 at any T (its 128-token kernel holds 284 VGPRs, one wave per SIMD:
+     measured 150 / 188 TOPS against 140 / 169 on 11008 x 4096 / 4096 x 11008, T = 256) */
+  const int v = t_gemm >= 3 ? t_gemm - 3 : (T > 64u && kind != AMDC_KIND_Q4_0 ? 0 : 1);
   u32 ks = t_ksplit > 0 ? (u32)t_ksplit : 0u;
   if (!ks) {
     const u64 tiles = (u64)((rows + gh[v].mr - 1u) / gh[v].mr) * ((T + gh[v].nt - 1u) / gh[v].nt);
