@@ -453,8 +453,14 @@ class Chain:
 
 # ---------------------------------------------------------------- GGUF files (include/amdc_gguf.h)
 
+def _k(name):
+    """A key or tensor name as the C strings of the file (any bytes round-trip through str)."""
+    return name.encode(errors="surrogateescape") if isinstance(name, str) else bytes(name)
+
+
 class Gguf:
-    """A GGUF v3 file opened by amdc_gguf_open (memory-mapped)."""
+    """A GGUF v3 file opened by amdc_gguf_open (memory-mapped). Keys and names are str (bytes that are
+    not UTF-8 kept as surrogate escapes) or bytes."""
 
     def __init__(self, path):
         h = _P()
@@ -492,27 +498,27 @@ class Gguf:
         for i in range(lib().amdc_gguf_n_kv(self.h)):
             k, t = C.c_char_p(), C.c_uint32()
             _check(lib().amdc_gguf_key_at(self.h, i, C.byref(k), C.byref(t)))
-            out.append((k.value.decode(), t.value))
+            out.append((k.value.decode(errors="surrogateescape"), t.value))
         return out
 
     def get_int(self, key):
         v = _I64()
-        return v.value if lib().amdc_gguf_get_int(self.h, key.encode(), C.byref(v)) else None
+        return v.value if lib().amdc_gguf_get_int(self.h, _k(key), C.byref(v)) else None
 
     def get_float(self, key):
         v = C.c_double()
-        return v.value if lib().amdc_gguf_get_float(self.h, key.encode(), C.byref(v)) else None
+        return v.value if lib().amdc_gguf_get_float(self.h, _k(key), C.byref(v)) else None
 
     def get_str(self, key):
         p, n = C.c_void_p(), _U64()
-        if not lib().amdc_gguf_get_str(self.h, key.encode(), C.byref(p), C.byref(n)):
+        if not lib().amdc_gguf_get_str(self.h, _k(key), C.byref(p), C.byref(n)):
             return None
-        return C.string_at(p.value, n.value).decode() if n.value else ""
+        return C.string_at(p.value, n.value).decode(errors="surrogateescape") if n.value else ""
 
     def get_arr(self, key):
         """(element type, count, numpy view of the packed scalars or None)."""
         t, n, d = C.c_uint32(), _U64(), C.c_void_p()
-        if not lib().amdc_gguf_get_arr(self.h, key.encode(), C.byref(t), C.byref(n), C.byref(d)):
+        if not lib().amdc_gguf_get_arr(self.h, _k(key), C.byref(t), C.byref(n), C.byref(d)):
             return None
         dt = {0: np.uint8, 1: np.int8, 2: np.uint16, 3: np.int16, 4: np.uint32, 5: np.int32, 6: np.float32, 7: np.uint8,
               10: np.uint64, 11: np.int64, 12: np.float64}.get(t.value)
@@ -523,9 +529,9 @@ class Gguf:
 
     def get_arr_str(self, key, i):
         p, n = C.c_void_p(), _U64()
-        if not lib().amdc_gguf_get_arr_str(self.h, key.encode(), i, C.byref(p), C.byref(n)):
+        if not lib().amdc_gguf_get_arr_str(self.h, _k(key), i, C.byref(p), C.byref(n)):
             return None
-        return C.string_at(p.value, n.value).decode() if n.value else ""
+        return C.string_at(p.value, n.value).decode(errors="surrogateescape") if n.value else ""
 
     def tensors(self):
         out = []
@@ -536,24 +542,24 @@ class Gguf:
         return out
 
     def find(self, name):
-        return lib().amdc_gguf_find_tensor(self.h, name.encode())
+        return lib().amdc_gguf_find_tensor(self.h, _k(name))
 
     def mat_info(self, name):
         m = Mat()
-        _check(lib().amdc_gguf_mat_info(self.h, name.encode(), C.byref(m)))
+        _check(lib().amdc_gguf_mat_info(self.h, _k(name), C.byref(m)))
         return m
 
     def repack(self, name, threads=0):
         """The tensor repacked into the CDNA4 layout on the host: (Mat, uint8 array)."""
         m = self.mat_info(name)
         dst = np.empty(m.bytes, dtype=np.uint8)
-        _check(lib().amdc_gguf_repack(self.h, name.encode(), threads, C.byref(m), dst.ctypes.data_as(_P)))
+        _check(lib().amdc_gguf_repack(self.h, _k(name), threads, C.byref(m), dst.ctypes.data_as(_P)))
         return m, dst
 
     def load(self, name, threads=0, stream=None):
         """The streaming load to the device (amdc_gguf_load): a DevMat owning the device memory."""
         m = Mat()
-        _check(lib().amdc_gguf_load(self.h, name.encode(), threads, C.byref(m), stream))
+        _check(lib().amdc_gguf_load(self.h, _k(name), threads, C.byref(m), stream))
         return DevMat(m)
 
 

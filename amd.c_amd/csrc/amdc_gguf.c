@@ -425,16 +425,15 @@ static repack_fn repack_of(int kind) {
 
 typedef struct {
   repack_fn f;
-  const uint8_t *src;
-  uint8_t *dst;
-  u32 r0, r1, cols;
-  u64 sb, db; /* source and destination bytes per row */
+  const uint8_t *src; /* the job's first source row */
+  uint8_t *dst;       /* the job's first destination row */
+  u32 n, cols;        /* rows of the job */
   int rc;
 } rjob;
 
 static void *rjob_run(void *p) {
   rjob *j = p;
-  j->rc = j->r1 > j->r0 ? j->f(j->src + j->r0 * j->sb, j->r1 - j->r0, j->cols, j->dst + (u64)(j->r0) * j->db) : AMDC_OK;
+  j->rc = j->n ? j->f(j->src, j->n, j->cols, j->dst) : AMDC_OK;
   return NULL;
 }
 
@@ -451,7 +450,7 @@ AMDC_HIDDEN int amdc_gguf_repack_rows(const amdc_gguf_tensor *t, const amdc_mat 
   int started[16] = {0};
   for (int k = 0; k < nt; k++) {
     const u32 a = r0 + (u32)((u64)(r1 - r0) * (u64)k / (u64)nt), b = r0 + (u32)((u64)(r1 - r0) * (u64)(k + 1) / (u64)nt);
-    jobs[k] = (rjob){repack_of(m->kind), (const uint8_t *)t->data, dst - (u64)r0 * db, a, b, m->cols, sb, db, AMDC_OK};
+    jobs[k] = (rjob){repack_of(m->kind), (const uint8_t *)t->data + (u64)a * sb, dst + (u64)(a - r0) * db, b - a, m->cols, AMDC_OK};
     if (k > 0) started[k] = pthread_create(&th[k], NULL, rjob_run, &jobs[k]) == 0;
   }
   rjob_run(&jobs[0]);
