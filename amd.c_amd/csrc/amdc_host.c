@@ -654,9 +654,12 @@ static int gemv_k8_launch(int kind, const void *w, const uint8_t *xq, float *y, 
 
 static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                        const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
-  if (kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) {
-    if (T == 1u || t_unroll > 0) return gemv_k8_launch(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
-    for (u32 t0 = 0; t0 < T; t0 += 8u) { /* the int8-MFMA verify kernel, 8 vectors per launch */
+  if ((kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) && (T == 1u || t_unroll > 0))
+    return gemv_k8_launch(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+  if (T > 1u && t_unroll <= 0) {
+    /* the int8-MFMA verify kernels, 8 vectors per launch (measured on MI355X, T = 16: 17408 x 5120
+       Q4_K 42.9 us as two such launches against 176 us on the dot4 multi-vector kernel) */
+    for (u32 t0 = 0; t0 < T; t0 += 8u) {
       const u32 tn = T - t0 < 8u ? T - t0 : 8u;
       int rc = gemv8_launch(kind, w, xq + (u64)t0 * xs, y + (u64)t0 * ys, rows, nb, bias, res ? res + (u64)t0 * rs : NULL, tn, xs, ys, rs,
                             stream);
@@ -664,7 +667,6 @@ static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uin
     }
     return AMDC_OK;
   }
-  if (T > 1u && T <= 8u && t_unroll <= 0) return gemv8_launch(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
   const u32 ng = amdc_ngroups(nb), L = gemv_lanes(ng), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
   const u32 TT = T == 1u ? 1u : T <= 8u ? 8u : 16u;
   u32 GC = (TT == 1u ? GEMV_LDS_T1 : GEMV_LDS_TN) / (320u * TT);
@@ -728,7 +730,7 @@ static int gemv_t(int kind, const char *op, const void *w, const uint8_t *xq, fl
   NEED_OPEN();
   int rc = check_mat(op, kind, w, xq, y, rows, nb);
   if (!rc) rc = check_t(op, nb, rows, T, xs, ys, rs, res);
-  for (u32 t0 = 0; !rc && t0 < T; t0 += 16u) { /* the weights read once per 16 vectors */
+  for (u32 t0 = 0; !rc && t0 < T; t0 += 16u) { /* 16 vectors per gemv_launch (the dot4 kernels' most; the MFMA kernels take 8) */
     const u32 tn = T - t0 < 16u ? T - t0 : 16u;
     rc = gemv_launch(kind, w, xq + (u64)t0 * xs, y + (u64)t0 * ys, rows, nb, bias, res ? res + (u64)t0 * rs : NULL, tn, xs, ys, rs,
                      stream);

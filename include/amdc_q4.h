@@ -163,15 +163,15 @@ int amdc_gemv_q6k_x(const void *w, const float *x, float *y, uint32_t rows, uint
                     void *stream);
 
 /* y_t = W x_t for T Q8 vectors (MTP verify, any T >= 1; the weights are
- * read once per 16 vectors, T <= 8 on int8 MFMA, the exact integer dots of
+ * read once per 8 vectors, on int8 MFMA, the exact integer dots of
  * ie_q4q8_block / ie_q4k_dot): x_t at xq + t * xs bytes, y_t at y + t * ys
  * floats, res_t at res + t * rs floats. A library workspace holds split-K
  * partial sums (allocated on the first call of a size: call once outside
  * graph capture before capturing). Replaces the multi-token branch of
  * OP_GEMV_Q4K (ie_gemv_q4kq8_ts2 / _tr8 / _tr, src/hip.c:1004-1020); the
  * Q4_0 form has no reference kernel (the reference runs OP_GEMV_Q4 per
- * token, src/hip.c:1583-1588) and gives the same values as T calls of
- * amdc_gemv_q4. */
+ * token, src/hip.c:1583-1588); its values agree with T calls of
+ * amdc_gemv_q4 within the same bound (the float sums run in another order). */
 int amdc_gemv_q4_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                    uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 int amdc_gemv_q4k_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,

@@ -154,12 +154,10 @@ def test_gemv_epilogue_bias_res(dev, orc, kind, form):
 
 # ---------------------------------------------------------------- multi-vector GEMV (verify)
 
-@pytest.mark.parametrize("path", [0, 1])  # 0: int8-MFMA verify kernel for T <= 8; 1: the dot4 kernels
+@pytest.mark.parametrize("path", [0, 1])  # 0: int8-MFMA verify kernels, 8 vectors per launch; 1: the dot4 kernels
 @pytest.mark.parametrize("T", [2, 5, 8, 9, 16, 19])
 @pytest.mark.parametrize("kind,rows,nb", [(0, 40, 128), (0, 130, 43), (3, 33, 160), (3, 21, 544), (3, 200, 72)])
 def test_gemv_multi(dev, orc, kind, rows, nb, T, path):
-    if path and T > 8:
-        pytest.skip("T > 8 uses the dot4 kernel in both paths")
     dev.set_tuning(unroll=path)
     c = Case(dev, orc, kind, rows, nb, T, seed=T * 13 + nb)
     assert np.array_equal(c.quant(), c.xq)
