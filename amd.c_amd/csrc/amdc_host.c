@@ -385,7 +385,11 @@ int amdc_open(const char *hsaco) {
   if (t_wgs < 0) t_wgs = envi("AMDC_GEMV_WG", 0);
   if (t_gemm < 0) t_gemm = envi("AMDC_GEMM_KERNEL", 0);
   if (t_ksplit < 0) t_ksplit = envi("AMDC_GEMM_KSPLIT", 0);
-  if (t_gemm_min < 0) t_gemm_min = envi("IE_GEMM_MIN", 17);
+  /* the token count from which op_gemv runs the prefill GEMM: the reference's IE_GEMM_MIN
+     variable, with a default measured on MI355X (the verify kernels, 8 vectors per launch, are
+     faster up to about 24 tokens: 17408 x 5120 Q4_K, T = 17: 53 us against 67 us for the GEMM;
+     T = 32: 83 against 70) */
+  if (t_gemm_min < 0) t_gemm_min = envi("IE_GEMM_MIN", 25);
   x_fuse_nb = (u32)envi("AMDC_GEMVX_FUSE_NB", 128);
   t_form = envi("AMDC_GEMV_FORM", 0);
   g_open = 1;

@@ -216,7 +216,8 @@ int amdc_gemm_q6k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uin
 
 /* The dispatch of launch_op for OP_GEMV_Q4 / OP_GEMV_Q8 / OP_GEMV_Q4K /
  * OP_GEMV_Q6K over T tokens (src/hip.c:928-1089): T == 1 -> the decode GEMV;
- * T >= IE_GEMM_MIN (env, default 17) -> the GEMM (Q4_0 included, where the
+ * T >= IE_GEMM_MIN (env, default 25 on MI355X; the reference's default is
+ * 17) -> the GEMM (Q4_0 included, where the
  * reference runs one GEMV per token); else the multi-vector GEMV. kind: any
  * AMDC_KIND_*. */
 int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,

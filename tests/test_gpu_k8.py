@@ -265,9 +265,9 @@ def test_graph_replay_matches_eager(dev, orc):
 def test_max_sizes(dev, orc, kind, nb):
     """The largest rows the reference's loader accepts for each kind (core/ie_core.h:60, 187, 258-260:
     Q4_0 nb < 512, Q8_0 nb < 2048, Q4_K / Q6_K nb < 2048 with nb % 8 == 0; Q4_0 also past the
-    reference's limit, where it would switch to Q8_0): decode, verify (T = 8) and GEMM (T = 20)."""
+    reference's limit, where it would switch to Q8_0): decode, verify (T = 8) and GEMM (T = 32)."""
     rows = 37
-    c = Case(dev, orc, kind, rows, nb, 20, seed=nb)
+    c = Case(dev, orc, kind, rows, nb, 32, seed=nb)
     c.quant()
     dev.gemv(kind, c.W, c.Q, c.Y, rows, nb)
     assert rel_err(c.y_gpu()[0], c.y_oracle(0), c.mag(0)) < TOL
@@ -275,7 +275,7 @@ def test_max_sizes(dev, orc, kind, nb):
     y = c.y_gpu()
     for t in (0, 7):
         assert rel_err(y[t], c.y_oracle(t), c.mag(t)) < TOL, t
-    dev.op_gemv(kind, c.W, c.Q, c.Y, rows, nb, 20, c.xs, rows)
+    dev.op_gemv(kind, c.W, c.Q, c.Y, rows, nb, 32, c.xs, rows)
     y = c.y_gpu()
-    for t in (0, 19):
+    for t in (0, 31):
         assert rel_err(y[t], c.y_oracle(t), c.mag(t)) < TOL, t

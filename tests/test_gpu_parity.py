@@ -197,7 +197,7 @@ def test_gemm_q4k(dev, orc, rows, nb, T, kern, ks):
 
 def test_op_gemv_dispatch(dev, orc):
     rows, nb = 48, 64
-    for kind, T in ((0, 1), (3, 1), (0, 8), (3, 8), (0, 20), (3, 20)):
+    for kind, T in ((0, 1), (3, 1), (0, 8), (3, 8), (0, 20), (3, 20), (0, 40), (3, 40)):
         c = Case(dev, orc, kind, rows, nb, T, seed=T + kind)
         c.quant()
         dev.op_gemv(kind, c.W, c.Q, c.Y, rows, nb, T, c.xs, rows)
