@@ -391,6 +391,31 @@ def cpu_baseline(seed, budget_s=12.0):
                       f"{'cpu_gemv_q4 of hanw/amd.c src/cpu.c' if kind == 'reference' else 'oracle/amdc_oracle.c'}"}
 
 
+def cpu_baseline_rows(seed, budget_s=6.0):
+    """The same c1 step on the host's cores: the restatement's row-parallel GEMV (the same per-row
+    arithmetic as cpu_gemv_q4, so the same bits), one thread per core up to 16 (the GPU box's CPU
+    share). A second baseline, reported beside the one-core one."""
+    from oracle import GGML_Q4_0, Oracle
+
+    cores = min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1))
+    shapes = synth.CONFIGS["c1"]["shapes"]
+    x = synth.activations(1, 11008, seed + 99)[0]
+    orc = Oracle()
+    arrs = [orc.repack(GGML_Q4_0, synth.gguf(synth.KIND_Q4_0, r, c, seed + i), r, c // 32) for i, (_, r, c) in enumerate(shapes)]
+    xq = {c: orc.quant_q8(x[:c]) for _, _, c in shapes}
+    set_bytes = sum(wbytes(r, c) for _, r, c in shapes)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        for (qw, qs), (_, r, c) in zip(arrs, shapes):
+            orc.gemv(GGML_Q4_0, qw, qs, r, c // 32, xq[c], threads=cores)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 200:
+            break
+    return {"value": round(set_bytes * n / el / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{n} c1 steps in {el:.1f} s, {cores} threads, oracle/amdc_oracle.c row-parallel (bit-identical to cpu_gemv_q4)"}
+
+
 def traffic_from_profiles():
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC summary, if any."""
     p = os.path.join(ROOT, "profiles", "gemv_q4_0_c1_traffic.txt")
@@ -452,6 +477,8 @@ def main():
     if not a.quick and not a.no_cpu:
         cpu = cpu_baseline(a.seed)
         print(f"bench: cpu {json.dumps(cpu)}", file=sys.stderr, flush=True)
+        detail["cpu_all_cores"] = cpu_baseline_rows(a.seed)
+        print(f"bench: cpu_all_cores {json.dumps(detail['cpu_all_cores'])}", file=sys.stderr, flush=True)
     ach = c1["kernel_GBps"]
     out = {
         "metric": METRIC,
