@@ -436,45 +436,30 @@ __device__ __forceinline__ float item_dot(const typename ItemOf<KIND>::type &it,
   return acc;
 }
 
-template <int KIND, bool FQ>
-__device__ __forceinline__ void gemv1_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
-                                           u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 L,
-                                           const float *__restrict__ xf = nullptr, uint8_t *__restrict__ q8out = nullptr) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const u32 ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
-  const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw;
-  const u32 nrg = (rows + rpg - 1u) / rpg, ni = (ng + L - 1u) / L;
-  const u64 RB = amdc_row_bytes(nb);
-  const u32 nblk = 8u * ng;
-  u32x4 *s_lo = (u32x4 *)smem;
-  u32x4 *s_hi = s_lo + nblk;
-  float *s_d = (float *)(s_hi + nblk);
-  u32 *s_as = (u32 *)(s_d + nblk);
-  u32 rg = blockIdx.x, i = 0;
-  if (rg >= nrg) return; // the whole workgroup
-  auto rowp = [&](u32 g_) {
-    const u32 r_ = g_ * rpg + wv * rpw + q;
-    return W + (u64)(r_ < rows ? r_ : rows - 1u) * RB;
-  };
-  // Fused quantization (the arithmetic of amdc_quant_q8): 8 lanes per block,
-  // 4 values per lane, 32 blocks per pass of the workgroup. The activation
-  // loads of up to QCH passes are issued before the first weight item's, so
-  // that the quantization runs while the weights are in flight (loads count
-  // down in issue order); they are unconditional (a block past nb reads the
-  // last block again and takes zeros), so that no branch joins them. The max
-  // and the sum of a block's 8 lanes go by DPP (xor 1, xor 2, then the
-  // half-row mirror).
-  const u32 e = tid & 7u;
+// Fused quantization into the staged vector (the arithmetic of
+// amdc_quant_q8): 8 lanes per block, 4 values per lane, 32 blocks per pass of
+// the workgroup; each block goes to the LDS slot of the staged layout
+// (permuted as the weights, p = (b % 8) ng + b / 8) as lo/hi words, d and
+// asum, and, when q8out is given, workgroup 0 also writes the Q8 buffer. The
+// activation loads of up to QCH passes are issued at once (load), so that a
+// kernel can put them ahead of its first weight loads and quantize (quant)
+// while the weights are in flight (loads count down in issue order); they are
+// unconditional (a block past nb reads the last block again and takes zeros),
+// so that no branch joins them. The max and the sum of a block's 8 lanes go
+// by DPP (xor 1, xor 2, then the half-row mirror).
+struct FusedQ8 {
   v4f xv[QCH];
-  auto xload = [&](u32 b0) {
+  __device__ __forceinline__ void load(const float *__restrict__ xf, u32 nb, u32 b0) {
+    const u32 tid = threadIdx.x, e = tid & 7u;
 #pragma unroll
     for (u32 c = 0; c < QCH; c++) {
       const u32 b = b0 + 32u * c + (tid >> 3);
       const v4f v = *(const v4f *)(xf + 32u * (b < nb ? b : nb - 1u) + 4u * e);
       xv[c] = b < nb ? v : (v4f){0.0f, 0.0f, 0.0f, 0.0f};
     }
-  };
-  auto xquant = [&](u32 b0) {
+  }
+  __device__ __forceinline__ void quant(u32 b0, u32 nb, u32 ng, u32x4 *s_lo, u32x4 *s_hi, float *s_d, u32 *s_as, uint8_t *__restrict__ q8out) {
+    const u32 tid = threadIdx.x, e = tid & 7u, nblk = 8u * ng;
 #pragma unroll
     for (u32 c = 0; c < QCH; c++) {
       if (b0 + 32u * c >= nblk) break;
@@ -503,18 +488,41 @@ __device__ __forceinline__ void gemv1_body(const uint8_t *__restrict__ W, const 
         if (e == 0u) ((float *)(q8out + 32u * nb))[b] = d, ((u32 *)(q8out + 36u * nb))[b] = sum;
       }
     }
+  }
+};
+
+template <int KIND, bool FQ>
+__device__ __forceinline__ void gemv1_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
+                                           u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 L,
+                                           const float *__restrict__ xf = nullptr, uint8_t *__restrict__ q8out = nullptr) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const u32 ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw;
+  const u32 nrg = (rows + rpg - 1u) / rpg, ni = (ng + L - 1u) / L;
+  const u64 RB = amdc_row_bytes(nb);
+  const u32 nblk = 8u * ng;
+  u32x4 *s_lo = (u32x4 *)smem;
+  u32x4 *s_hi = s_lo + nblk;
+  float *s_d = (float *)(s_hi + nblk);
+  u32 *s_as = (u32 *)(s_d + nblk);
+  u32 rg = blockIdx.x, i = 0;
+  if (rg >= nrg) return; // the whole workgroup
+  auto rowp = [&](u32 g_) {
+    const u32 r_ = g_ * rpg + wv * rpw + q;
+    return W + (u64)(r_ < rows ? r_ : rows - 1u) * RB;
   };
+  FusedQ8 fq;
   Item cur, nxt;
   if (FQ) {
-    xload(0);
+    fq.load(xf, nb, 0);
     __asm__ volatile("" ::: "memory"); // keep the activation loads ahead of the weight loads
   }
   load_item<KIND>(cur, rowp(rg), ng, l, l < ng);
   if (FQ) {
-    xquant(0);
+    fq.quant(0, nb, ng, s_lo, s_hi, s_d, s_as, q8out);
     for (u32 b0 = 32u * QCH; b0 < nblk; b0 += 32u * QCH) {
-      xload(b0);
-      xquant(b0);
+      fq.load(xf, nb, b0);
+      fq.quant(b0, nb, ng, s_lo, s_hi, s_d, s_as, q8out);
     }
   } else {
     for (u32 j = tid; j < nblk; j += NT) { // stage the whole Q8 vector (permuted)
