@@ -292,11 +292,14 @@ static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
 static int g_open, g_cus;
 static int t_lanes = -1, t_unroll = -1, t_wgs = -1, t_gemm = -1, t_gemm_min = -1, t_ksplit = -1;
-static u32 x_fuse_nb = 128;
-static int t_form = 0; /* decode GEMV: 1 = amdc_gemv_*_p1, 2 = amdc_gemv_*_p2, 0 = by shape */ /* amdc_gemv_q4_x / _q4k_x: the largest nb quantized inside the GEMV */
-/* The GEMM's device workspace (prepared activations, split-K partial sums): grown on demand. */
+static u32 x_fuse_nb = 128; /* amdc_gemv_q4_x / _q4k_x: the largest nb quantized inside the GEMV */
+static int t_form = 0;      /* decode GEMV: 1 = amdc_gemv_*_p1, 2 = amdc_gemv_*_p2, 0 = by shape */
+/* The GEMM's device workspace (prepared activations, split-K partial sums): grown on demand;
+ * the smaller ones it replaced stay allocated until amdc_close (see ws_reserve). */
 static void *g_ws;
 static size_t g_ws_bytes;
+static void *g_ws_old[48];
+static unsigned g_ws_old_n;
 
 #define HIPCALL(x)                                                                               \
   do {                                                                                           \
@@ -401,7 +404,8 @@ static void stage_free(void);
 void amdc_close(void) {
   if (g_open) stage_free();
   if (g_open && g_ws) H.Free(g_ws);
-  g_ws = NULL, g_ws_bytes = 0;
+  for (unsigned i = 0; g_open && i < g_ws_old_n; i++) H.Free(g_ws_old[i]);
+  g_ws = NULL, g_ws_bytes = 0, g_ws_old_n = 0;
   if (g_open && g_mod) H.ModuleUnload(g_mod);
   g_mod = NULL;
   g_open = 0;
@@ -826,13 +830,20 @@ int amdc_gemv_q6k_x(const void *w, const float *x, float *y, uint32_t rows, uint
   return gemv_x(AMDC_KIND_Q6_K, "gemv_q6k_x", w, x, y, rows, nb, bias, res, q8, stream);
 }
 
+/* Grow the workspace to at least n bytes (a power of two, >= 1 MiB). A smaller
+ * workspace is kept, not freed, until amdc_close: a graph captured earlier may
+ * still hold its address, and replays of it must stay valid. */
 static int ws_reserve(size_t n) {
   if (n <= g_ws_bytes) return AMDC_OK;
-  if (g_ws) HIPCALL(H.Free(g_ws));
+  size_t m = (size_t)1 << 20;
+  while (m < n) m <<= 1;
+  if (g_ws) {
+    if (g_ws_old_n == sizeof g_ws_old / sizeof g_ws_old[0]) return fail(AMDC_EINVAL, "workspace: grown too many times");
+    g_ws_old[g_ws_old_n++] = g_ws;
+  }
   g_ws = NULL, g_ws_bytes = 0;
-  n = (n + (1u << 20) - 1u) & ~(size_t)((1u << 20) - 1u);
-  HIPCALL(H.Malloc(&g_ws, n));
-  g_ws_bytes = n;
+  HIPCALL(H.Malloc(&g_ws, m));
+  g_ws_bytes = m;
   return AMDC_OK;
 }
 

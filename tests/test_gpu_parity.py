@@ -347,3 +347,26 @@ def test_verify_splitk(dev, orc, kind):
         if ks in bits:
             assert np.array_equal(u, bits[ks]), ks
         bits[ks] = u
+
+
+def test_graph_survives_workspace_growth(dev, orc):
+    """A graph captured while the library's workspace is small keeps replaying correctly after a larger
+    call has grown the workspace (the smaller allocation stays alive until amdc_close)."""
+    small = Case(dev, orc, 3, 64, 40, 32, seed=31)
+    small.quant()
+    S = dev.Stream()
+    dev.gemm_q4k(small.W, small.Q, small.Y, 64, 40, 32, small.xs, 64)  # sizes the workspace for this call
+    dev.sync()
+    want = small.Y.download(np.uint32)
+    g = dev.Graph(S, lambda s: dev.gemm_q4k(small.W, small.Q, small.Y, 64, 40, 32, small.xs, 64, stream=s))
+    big = Case(dev, orc, 3, 300, 544, 256, seed=32)
+    big.quant()
+    dev.gemm_q4k(big.W, big.Q, big.Y, 300, 544, 256, big.xs, 300)  # grows the workspace
+    dev.sync()
+    for _ in range(3):
+        small.Y.fill(0)
+        g.launch()
+        S.sync()
+        assert np.array_equal(small.Y.download(np.uint32), want)
+    y = big.y_gpu()
+    assert rel_err(y[255], big.y_oracle(255), big.mag(255)) < TOL
