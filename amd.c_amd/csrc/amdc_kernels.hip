@@ -6,13 +6,30 @@
 //
 // Kernels (grid x = workgroups, 256 threads each):
 //   amdc_quant_q8      Q8 activation quantization (src/cpu.c:36-53)
-//   amdc_gemv_{q4_0,q4_k}_t{1,8,16}
-//                      y = W x for T <= 1/8/16 Q8 vectors, the weights read
-//                      once per launch (ie_gemv_q4q8, ie_gemv_q4kq8, _tr8, _tr)
+//   amdc_rmsnorm_q8, amdc_swiglu_q8
+//                      the Q8 producers (the float op and its Q8 copy)
+//   amdc_gemv_{q4_0,q4_k}_p1, _x1, {q4_0,q4_k,q8_0,q6_k}_p2
+//                      the decode GEMV (T = 1): short rows (_p1; _x1 with the
+//                      quantization fused), long rows and the Q8_0 / Q6_K kinds
+//                      (_p2) (ie_gemv_q4q8, ie_gemv_q4kq8, ie_gemv_q8q8,
+//                      ie_gemv_q6kq8)
+//   amdc_gemv_{q4_0,q4_k,q8_0,q6_k}_v8, amdc_gemm_reduce
+//                      the verify GEMV, T <= 8 vectors on int8 MFMA, K split
+//                      over workgroups and reduced in split order
+//                      (ie_gemv_q4kq8_tr8 / _tr / _ts2, ie_gemv_q6kq8_tr8, ...)
+//   amdc_gemv_{q4_0,q4_k}_t{1,8,16}, _t1u1
+//                      dot4 multi-vector GEMVs (a tuning alternative)
+//   amdc_q8_prep, amdc_gemmh_m64_n{64,128}, amdc_gemmh_{q4_0,q8_0,q6_k}_m64_n{64,128}
+//                      the prefill chunk GEMM on the f16 MFMA with exact
+//                      integer block sums (ie_gemm_q4kr, ie_gemm_q8r, ie_gemm_q6kr)
 //   amdc_gemm_q4_k_n{64,128}
-//                      the prefill chunk GEMM on int8 MFMA (ie_gemm_q4kr)
-//   amdc_dots_{q4_0,q4_k}
+//                      the same on int8 MFMA (a tuning alternative)
+//   amdc_chain         a list of quantize / decode-GEMV operations in one
+//                      persistent launch (the megakernel's GEMV chain)
+//   amdc_dots_{q4_0,q4_k,q8_0,q6_k}
 //                      the per-block int32 dot products (parity check)
+//   amdc_probe_read, amdc_probe_copy
+//                      plain streams (bandwidth and counter calibration)
 // The weight layout is amdc_layout.h. The Q8 buffer is the reference's:
 // [int8 q[32 nb] | f32 d[nb] | u32 asum[nb]] (src/common.h:25-29).
 #include <hip/hip_runtime.h>
