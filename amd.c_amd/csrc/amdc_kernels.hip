@@ -1626,53 +1626,89 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *
 // block arithmetic (src/cpu.c:81, 111-112, 168):
 //   Q4_0: acc += (d_w d_a) (dq - 8 asum); Q8_0: acc += (d_w d_a) dq
 //   Q4_K: acc = fma(s dq, d_a, acc), s = d sc; the min term - sum (dmin mn)
-//         (d_a asum) of every block on v_mfma_f32_16x16x4_f32 (column pp = 0).
+//         (d_a asum) of every block on v_mfma_f32_16x16x4_f32 (column pp = 0),
+//         its A operand formed from the header registers (K index 4 q + h:
+//         the lane's own super-groups h, h + 4, sub-block q % 8).
 // The columns pp = 0 and 1 of a token hold the sums of alternate blocks; a
 // DPP add joins them at the end.
 // Workgroup: 4 waves, wave w: rows 16 w .. 16 w + 15 of a 64-row tile; K in
 // tiles of 8 super-groups (64 blocks): the tile's activations are staged in
 // LDS, B-ready (the zero halves written once), with d_a, d_a asum (or asum)
-// per (block, token); each wave builds its rows' scale table (and Q4_K min
-// table) from the headers; the weights come straight from memory, plane k of
-// the tile is 4 loads of 32 contiguous bytes per row, one plane ahead.
+// per (block, token); each wave builds its rows' scale table from the headers.
+// The weights go from memory straight into LDS (buffer_load ... lds) in whole
+// 128-byte lines: plane k of a tile is 128 contiguous bytes of a row, and each
+// load instruction moves 8 rows x 128 bytes (register loads in the MFMA's lane
+// order touch 16 rows x 32 bytes per instruction, which held the vector memory
+// pipeline to about 2.5 TB/s); the A operand is then read from LDS in lane
+// order. Per wave a ring of NS plane steps (Q4: one plane of its 16 rows, 2 KB;
+// Q8_0: the two half planes of a block, 4 KB), one LDS array per slot so that
+// the waits for each step's loads are counted separately; within a wave's
+// plane, row i's 16-byte column c holds super-group c ^ v8_swz(i), so that the
+// A reads (16 rows, one column pair) fall on distinct banks.
 // Split K over gridDim.y (tiles [t0, t1) per split, partial sums to part).
-template <int KIND>
+__device__ __forceinline__ u32 v8_swz(u32 i) { return (i & 7u) ^ ((i >> 3) & 1u); }
+// A workgroup barrier for LDS written with ds_write only: the waves' LDS
+// writes are complete (lgkmcnt 0), the compiler keeps memory accesses on their
+// side; unlike __syncthreads it does not wait for the loads into LDS in
+// flight (each wave's weight ring is its own).
+__device__ __forceinline__ void v8_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <int KIND, int NS>
 __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
                                            u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 xs, u32 ys,
                                            u32 rs, float *__restrict__ part) {
+  constexpr u32 SC = KIND == AMDC_Q8_0 ? 2u : 1u; // 2 KB chunks (planes of 16 rows) per step
+  typedef __attribute__((address_space(3))) void lds_t;
+  __shared__ __attribute__((aligned(16))) u32x4 sw0[4][SC * 128u];
+  __shared__ __attribute__((aligned(16))) u32x4 sw1[4][SC * 128u];
+  __shared__ __attribute__((aligned(16))) u32x4 sw2[NS > 2 ? 4 : 1][NS > 2 ? SC * 128u : 1u];
+  __shared__ __attribute__((aligned(16))) u32x4 sw3[NS > 2 ? 4 : 1][NS > 2 ? SC * 128u : 1u];
   __shared__ __attribute__((aligned(16))) u32x4 sB[32][2][16]; // [pair p + 4 k][quarter & 1][column]: a column's nonzero half of K
   __shared__ __attribute__((aligned(16))) float sda[64][8];    // d_a [block of tile][token]
   __shared__ __attribute__((aligned(16))) float sxa[64][8];    // Q4_K: d_a asum; Q4_0: asum (as int bits)
-  __shared__ __attribute__((aligned(16))) float ssc[4][64][16]; // per wave: s (Q4_K d sc, Q4_0 d) [block][row]
-  __shared__ __attribute__((aligned(16))) float smn[4][64][16]; // per wave, Q4_K: -(dmin mn) [block][row]
+  __shared__ __attribute__((aligned(16))) float ssc[4][64][16]; // per wave: s (Q4_K d sc, Q4_0 / Q8_0 d) [block][row]
   const u32 ng = amdc_ngroups(nb), nt = (ng + 7u) >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
   const u32 i16 = lane & 15u, h = lane >> 4, n = i16, tk = n & 7u, pp = n >> 3;
   const u32 RB = (u32)amdc_row_bytes_k(KIND, nb);
-  const u32 rt0 = blockIdx.x * 64u, r0 = rt0 + 16u * w, ra = r0 + i16 < rows ? r0 + i16 : rows - 1u; // A row of this lane
-  // a workgroup-uniform resource over the tile's rows; the lane's row in the 32-bit offset
+  const u32 rt0 = blockIdx.x * 64u, r0 = rt0 + 16u * w;
+  auto clamp_row = [&](u32 r) { return (r < rows ? r : rows - 1u) - rt0; };
+  // a workgroup-uniform resource over the tile's rows; a lane's row in the 32-bit offset
   const __amdgpu_buffer_rsrc_t rw = rsrc(W + (u64)rt0 * RB, (u32)min((u64)(rows - rt0) * RB, (u64)0xFFFFFFF0u));
-  const u32 wo = (ra - rt0) * RB;
+  const u32 wo = clamp_row(r0 + i16) * RB;                                    // row i16 (headers)
+  const u32 wl0 = clamp_row(r0 + (lane >> 3)) * RB, wl1 = clamp_row(r0 + 8u + (lane >> 3)) * RB; // the plane loads' rows
+  const u32 lcol = lane & 7u, g0 = lcol ^ v8_swz(lane >> 3), g1 = lcol ^ v8_swz(8u + (lane >> 3));
   const u32 xn = (u32)min((u64)T * xs, (u64)0xFFFFFFF0u);
   const __amdgpu_buffer_rsrc_t rxq = rsrc(xq, xn); // the T Q8 rows
   constexpr u32 OOB = 0xFFFFFFF0u;                 // an offset past every resource: the load returns zeros
   const u32 ks = blockIdx.y, nks = gridDim.y, t0 = nt * ks / nks, t1 = nt * (ks + 1u) / nks;
   auto gtile = [&](u32 t) { return ng - 8u * t < 8u ? ng - 8u * t : 8u; };
-  // the weights of plane k of tile t: this lane's 16 bytes of the 4 pairs
-  // (every load unconditional: out-of-range ones read as zeros, so the
-  // compiler can count the loads in flight instead of draining them)
-  auto load_plane = [&](u32 t, u32 k, u32x4 (&wq)[4]) {
-    const u32 gt = gtile(t);
+  auto slot = [&](u32 s) -> u32x4 * {
+    if (s == 0u) return sw0[w];
+    if (s == 1u) return sw1[w];
+    if (s == 2u) return sw2[NS > 2 ? w : 0u];
+    return sw3[NS > 2 ? w : 0u];
+  };
+  // step k of tile t into slot s: chunk c = plane k (Q4) or 2k + c (Q8_0); rows 8j + lane / 8, column lane & 7
+  auto issue = [&](u32 t, u32 k, u32 s, bool on) {
+    const u32 gt = on ? gtile(t) : 0u; // off: every load out of range (zeros into the slot)
 #pragma unroll
-    for (u32 p = 0; p < 4u; p++) {
-      const u32 gl = 2u * p + (h >> 1);
-      const u32 o = KIND == AMDC_Q8_0 ? (u32)amdc_q8_off(ng, 8u * t + gl, 2u * k + (h & 1u)) : (u32)amdc_nib_off(ng, 8u * t + gl, k);
-      wq[p] = __builtin_amdgcn_raw_buffer_load_b128(rw, gl < gt ? wo + o : OOB, 0, 0);
+    for (u32 c = 0; c < SC; c++) {
+      const u32 pl = SC == 1u ? k : 2u * k + c;
+      const u32 base = (KIND == AMDC_Q8_0 ? 2048u : 1024u) * t + 16u * ng + 16u * pl * gt;
+      lds_t *d = (lds_t *)(slot(s) + 128u * c);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, d, 16, g0 < gt ? wl0 + base + 16u * g0 : OOB, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_t *)(slot(s) + 128u * c + 64u), 16, g1 < gt ? wl1 + base + 16u * g1 : OOB, 0, 0, 0);
     }
   };
   // activations of tile t in registers (thread: 2 of the 16-byte halves, 2 of the (block, token) scale pairs)
   u32x4 ra4[4];
   float rd[2];
-  u32 rx[2]; // asum as loaded: d_a asum is formed at the LDS store, so that the fetch does not wait for its loads
+  u32 rx[2];
   u32x4 rh[2];
   auto fetch_tile = [&](u32 t) {
     const u32 gt = gtile(t);
@@ -1695,6 +1731,7 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
       rh[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, gl < gt ? wo + 16u * (8u * t + gl) : OOB, 0, 0);
     }
   };
+  float am[16]; // Q4_K: -(dmin mn) of row i16 for K index 4 q + h of the min-term MFMAs: super-group h + 4 (q / 8), sub-block q % 8
   auto stage_tile = [&]() {
 #pragma unroll
     for (u32 c = 0; c < 4u; c++) {
@@ -1708,7 +1745,7 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
       sxa[bl][tok] = KIND == AMDC_Q4_K ? rd[c] * (float)(int)rx[c] : __builtin_bit_cast(float, rx[c]);
     }
 #pragma unroll
-    for (u32 q = 0; q < 2u; q++) { // this wave's scale tables: row i16, groups h, h + 4
+    for (u32 q = 0; q < 2u; q++) { // this wave's scale table: row i16, groups h, h + 4
       const u32 gl = h + 4u * q;
       const u32x4 hd = rh[q];
 #pragma unroll
@@ -1717,19 +1754,22 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
           ssc[w][8u * gl + k][i16] = h2f(hword(hd, k >> 1) >> (16u * (k & 1u)));
         } else {
           ssc[w][8u * gl + k][i16] = h2f(hd.x) * (float)q4k_sc(hd, k);
-          smn[w][8u * gl + k][i16] = -(h2f(hd.x >> 16) * (float)q4k_mn(hd, k));
+          am[8u * q + k] = -(h2f(hd.x >> 16) * (float)q4k_mn(hd, k));
         }
       }
     }
   };
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  // the MFMAs of plane k (pairs of the tile) with its weights wq
-  auto plane = [&](u32 k, u32 npair, const u32x4 (&wq)[4]) {
+  // the MFMAs of plane step k (pairs of the tile) from slot s
+  auto plane = [&](u32 k, u32 npair, u32 s) {
+    const u32x4 *sl = slot(s);
+    const u32 cs = SC == 2u ? 128u * (h & 1u) : 0u; // Q8_0: lanes h odd read the second half plane
     v4i c[4];
 #pragma unroll
-    for (u32 p = 0; p < 4u; p++) { // the MFMAs of the plane first
+    for (u32 p = 0; p < 4u; p++) {
       if (p < npair) {
-        const u32x4 a = KIND == AMDC_Q8_0 ? wq[p] : (wq[p] >> (4u * (h & 1u))) & 0x0F0F0F0Fu;
+        const u32x4 wq = sl[cs + 8u * i16 + ((2u * p + (h >> 1)) ^ v8_swz(i16))];
+        const u32x4 a = KIND == AMDC_Q8_0 ? wq : (wq >> (4u * (h & 1u))) & 0x0F0F0F0Fu;
         const u32x4 bq = (h >> 1) == pp ? sB[p + 4u * k][h & 1u][n] : (u32x4)(0u); // the other half of K is zero
         c[p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, bq), (v4i){0, 0, 0, 0}, 0, 0, 0);
       }
@@ -1754,37 +1794,36 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
     }
   };
 
-  // software pipeline over (tile, plane): plane k uses ring slot k & 3 and,
-  // once used, the slot is reloaded with plane k + 4 (of this tile or the next)
-  u32x4 wq[4][4];
+  // software pipeline over (tile, step): step k uses slot k % NS and, once
+  // used, the slot is reloaded with step k + NS (of this tile or the next)
   if (t0 < t1) {
     fetch_tile(t0);
 #pragma unroll
-    for (u32 k = 0; k < 4u; k++) load_plane(t0, k, wq[k]);
+    for (u32 k = 0; k < (u32)NS; k++) issue(t0, k, k, true);
   }
   for (u32 t = t0; t < t1; t++) {
     const bool more = t + 1u < t1;
     const u32 npair = (gtile(t) + 1u) >> 1;
-    __syncthreads(); // the previous tile's readers are done
+    v8_barrier(); // the previous tile's readers are done
     stage_tile();
-    __syncthreads();
-    if (more) fetch_tile(t + 1u); // in flight during this tile
-#pragma unroll
-    for (u32 k = 0; k < 8u; k++) {
-      plane(k, npair, wq[k & 3u]);
-      if (k < 4u) load_plane(t, k + 4u, wq[k & 3u]);
-      else if (more) load_plane(t + 1u, k - 4u, wq[k & 3u]);
-    }
+    v8_barrier();
     if (KIND == AMDC_Q4_K) { // the min term of the tile's blocks, into the pp = 0 columns
       v4f m = {acc[0], acc[1], acc[2], acc[3]};
 #pragma unroll
       for (u32 q = 0; q < 16u; q++) {
-        const u32 bl = 4u * q + h; // K index = block of the tile
-        const float am = smn[w][bl][i16];
+        const u32 bl = 8u * (h + 4u * (q >> 3)) + (q & 7u); // K index 4 q + h
         const float bx = pp == 0u ? sxa[bl][tk] : 0.0f;
-        m = __builtin_amdgcn_mfma_f32_16x16x4f32(am, bx, m, 0, 0, 0);
+        m = __builtin_amdgcn_mfma_f32_16x16x4f32(am[q], bx, m, 0, 0, 0);
       }
       acc[0] = m[0], acc[1] = m[1], acc[2] = m[2], acc[3] = m[3];
+    }
+    if (more) fetch_tile(t + 1u); // in flight during this tile
+#pragma unroll
+    for (u32 k = 0; k < 8u; k++) {
+      plane(k, npair, k % (u32)NS);
+      // issued also after the range's last tile (as zeros), so that the waits count statically
+      if (k + (u32)NS < 8u) issue(t, k + (u32)NS, k % (u32)NS, true);
+      else issue(t + 1u, k + (u32)NS - 8u, k % (u32)NS, more);
     }
   }
   // join the two block parities of each token (columns n and n + 8) and store
@@ -1810,17 +1849,17 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_0_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *part) {
-  gemv8_body<AMDC_Q4_0>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+  gemv8_body<AMDC_Q4_0, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
 }
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *part) {
-  gemv8_body<AMDC_Q4_K>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+  gemv8_body<AMDC_Q4_K, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
 }
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *part) {
-  gemv8_body<AMDC_Q8_0>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+  gemv8_body<AMDC_Q8_0, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
 }
 
 // The verify GEMV for Q6_K (T <= 8). A Q6_K weight's scale changes every 16
