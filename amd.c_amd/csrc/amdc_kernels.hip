@@ -1867,8 +1867,8 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v8(const uint8_
 // and each of the 16 columns one (quarter, token) pair:
 //   A (16 rows x 64): lane (row i, h) = q - 32 of the 16 weights of half h & 1
 //     of sub-block (g + h / 2, k) (a pair of super-groups, one plane, as the Q4
-//     pair kernel): its 16 nibble bytes (one 128-bit load) and its half's
-//     high-bit word (one 32-bit load), then ((v | 0x80) - 0x20) ^ 0x80 per byte
+//     pair kernel): its 16 nibble bytes and its half's high-bit word, then
+//     ((v | 0x80) - 0x20) ^ 0x80 per byte
 //   B (64 x 16 columns n = 4 q + t): the 16 activations of quarter q for token
 //     t (4 tokens per MFMA, two MFMAs for 8), zeros in the other quarters (LDS
 //     holds only the nonzero quarter of each column; the other lanes use 0)
@@ -1877,34 +1877,49 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v8(const uint8_
 // reference's fma(fma(s1, d1, s0 d0), d_a, acc), src/cpu.c:142, regrouped);
 // the four quarters of a token are joined at the end (row_ror 8, then 4).
 // Tiles of 8 super-groups as gemv8_body: activations and d_a staged in LDS in
-// B form, each wave's d sc table per (sub-block, half, row); the weights from
-// memory one plane ahead in a ring of 4 planes. Split K over gridDim.y.
+// B form. The weights go into LDS as in gemv8_body, in whole 128-byte lines: a
+// ring step is the nibble planes 2m, 2m + 1 and high-bit plane m of the wave's
+// 16 rows (6 KB), 2 steps per wave. The scales: each wave's table of sc + 128
+// per (sub-block, half, row) in bytes and d per (super-group, row); s = d sc
+// is formed as fma(d, sc + 128, -128 d), the same single rounding as d * sc.
+// Split K over gridDim.y.
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq,
                                                                    float *__restrict__ y, u32 rows, u32 nb, const float *__restrict__ bias,
                                                                    const float *__restrict__ res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *__restrict__ part) {
+  typedef __attribute__((address_space(3))) void lds_t;
+  constexpr u32 CH = 128u; // u32x4 per 2 KB chunk (16 rows x 128 bytes)
+  __shared__ __attribute__((aligned(16))) u32x4 sw0[4][3u * CH]; // per wave: nibble planes 2m, 2m + 1, high plane m
+  __shared__ __attribute__((aligned(16))) u32x4 sw1[4][3u * CH];
   __shared__ __attribute__((aligned(16))) u32x4 sB[2][32][16]; // [token half][pair p + 4 k][column]: the column's nonzero quarter
   __shared__ __attribute__((aligned(16))) float sda[64][8];       // d_a [sub-block][token]
-  __shared__ __attribute__((aligned(16))) float ssc[4][64][2][16]; // per wave: d sc [sub-block][half][row]
+  __shared__ __attribute__((aligned(16))) uint8_t ssc[4][64][2][16]; // per wave: sc + 128 [sub-block][half][row]
+  __shared__ __attribute__((aligned(16))) float sd[4][8][16];        // per wave: d [super-group][row]
   const u32 ng = nb >> 3, nt = (ng + 7u) >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
   const u32 i16 = lane & 15u, h = lane >> 4, n = i16, qn = n >> 2, tq = n & 3u;
-  const u32 RB = (u32)amdc_q6k_row_bytes(nb);
-  const u32 rt0 = blockIdx.x * 64u, r0 = rt0 + 16u * w, ra = r0 + i16 < rows ? r0 + i16 : rows - 1u;
+  const u32 RB = (u32)amdc_q6k_row_bytes(nb), D = amdc_q6k_dpad(ng);
+  const u32 rt0 = blockIdx.x * 64u, r0 = rt0 + 16u * w;
+  auto clamp_row = [&](u32 r) { return (r < rows ? r : rows - 1u) - rt0; };
   const __amdgpu_buffer_rsrc_t rw = rsrc(W + (u64)rt0 * RB, (u32)min((u64)(rows - rt0) * RB, (u64)0xFFFFFFF0u));
-  const u32 wo = (ra - rt0) * RB;
+  const u32 wo = clamp_row(r0 + i16) * RB;
+  const u32 wl0 = clamp_row(r0 + (lane >> 3)) * RB, wl1 = clamp_row(r0 + 8u + (lane >> 3)) * RB; // the plane loads' rows
+  const u32 lcol = lane & 7u, g0 = lcol ^ v8_swz(lane >> 3), g1 = lcol ^ v8_swz(8u + (lane >> 3));
   const __amdgpu_buffer_rsrc_t rxq = rsrc(xq, (u32)min((u64)T * xs, (u64)0xFFFFFFF0u));
   constexpr u32 OOB = 0xFFFFFFF0u;
   const u32 ks = blockIdx.y, nks = gridDim.y, t0 = nt * ks / nks, t1 = nt * (ks + 1u) / nks;
   auto gtile = [&](u32 t) { return ng - 8u * t < 8u ? ng - 8u * t : 8u; };
-  // plane k of tile t: per pair p, the 16 nibble bytes of sub-block (2p + h / 2, k) and the high word of half h & 1
-  auto load_plane = [&](u32 t, u32 k, u32x4 (&wq)[4], u32 (&hq)[4]) {
-    const u32 gt = gtile(t);
+  auto slot = [&](u32 s) -> u32x4 * {
+    if (s == 0u) return sw0[w];
+    return sw1[w];
+  };
+  // step m of tile t into slot s (off: every load out of range)
+  auto issue = [&](u32 t, u32 m, u32 s, bool on) {
+    const u32 gt = on ? gtile(t) : 0u;
 #pragma unroll
-    for (u32 p = 0; p < 4u; p++) {
-      const u32 gl = 2u * p + (h >> 1), g = 8u * t + gl;
-      wq[p] = __builtin_amdgcn_raw_buffer_load_b128(rw, gl < gt ? wo + (u32)amdc_q6k_nib_off(ng, g, k) : OOB, 0, 0);
-      hq[p] = __builtin_amdgcn_raw_buffer_load_b32(rw, gl < gt ? wo + (u32)amdc_q6k_hi_off(ng, g, k >> 1) + 8u * (k & 1u) + 4u * (h & 1u) : OOB,
-                                                   0, 0);
+    for (u32 c = 0; c < 3u; c++) {
+      const u32 base = c < 2u ? 16u * ng + D + 1024u * t + 16u * (2u * m + c) * gt : 144u * ng + D + 512u * t + 16u * m * gt;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_t *)(slot(s) + CH * c), 16, g0 < gt ? wl0 + base + 16u * g0 : OOB, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_t *)(slot(s) + CH * c + 64u), 16, g1 < gt ? wl1 + base + 16u * g1 : OOB, 0, 0, 0);
     }
   };
   u32x4 ra4[4];
@@ -1945,28 +1960,35 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
       sda[i >> 3][i & 7u] = rd[c];
     }
 #pragma unroll
-    for (u32 q = 0; q < 2u; q++) { // this wave's table: row i16, super-groups h, h + 4
+    for (u32 q = 0; q < 2u; q++) { // this wave's tables: row i16, super-groups h, h + 4
       const u32 gl = h + 4u * q;
-      const float d = h2f(rdd[q]);
+      sd[w][gl][i16] = h2f(rdd[q]);
 #pragma unroll
       for (u32 k = 0; k < 8u; k++)
 #pragma unroll
         for (u32 e = 0; e < 2u; e++)
-          ssc[w][8u * gl + k][e][i16] = d * (float)(int)(int8_t)(hword(rh[q], k >> 1) >> (16u * (k & 1u) + 8u * e));
+          ssc[w][8u * gl + k][e][i16] = (uint8_t)((hword(rh[q], k >> 1) >> (16u * (k & 1u) + 8u * e)) + 128u);
     }
   };
   float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
   const u32 nth = T > 4u ? 2u : 1u; // token halves with tokens
-  auto plane = [&](u32 k, u32 npair, const u32x4 (&wq)[4], const u32 (&hq)[4]) {
+  v4f d4[4], n4[4];                 // d and -128 d of this lane's output rows, super-group 2 p + qn / 2
+  // the MFMAs of plane k = 2 m + e from slot s
+  auto plane = [&](u32 m, u32 e, u32 npair, u32 s) {
+    const u32 k = 2u * m + e;
+    const u32x4 *sl = slot(s);
     v4i c[2][4];
     const u32 sft = 4u * (h & 1u);
 #pragma unroll
     for (u32 p = 0; p < 4u; p++) { // the MFMAs of the plane first
       if (p < npair) {
+        const u32 col = (2u * p + (h >> 1)) ^ v8_swz(i16);
+        const u32x4 wq = sl[CH * e + 8u * i16 + col];
+        const u32 hq = ((const u32 *)(sl + 2u * CH + 8u * i16 + col))[2u * e + (h & 1u)];
         u32 a[4];
 #pragma unroll
         for (u32 i = 0; i < 4u; i++) {
-          const u32 v = ((wq[p][i] >> sft) & 0x0F0F0F0Fu) | (((hq[p] >> (2u * i)) & 0x03030303u) << 4);
+          const u32 v = ((wq[i] >> sft) & 0x0F0F0F0Fu) | (((hq >> (2u * i)) & 0x03030303u) << 4);
           a[i] = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
         }
         const v4i av = {(int)a[0], (int)a[1], (int)a[2], (int)a[3]};
@@ -1981,7 +2003,10 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
     for (u32 p = 0; p < 4u; p++) {
       if (p >= npair) break;
       const u32 bl = 8u * (2u * p + (qn >> 1)) + k; // this lane's sub-block (column quarter qn)
-      const v4f s4 = *(const v4f *)&ssc[w][bl][qn & 1u][4u * h];
+      const u32 sc4 = *(const u32 *)&ssc[w][bl][qn & 1u][4u * h];
+      v4f s4;
+#pragma unroll
+      for (u32 v = 0; v < 4u; v++) s4[v] = __builtin_fmaf(d4[p][v], (float)((sc4 >> (8u * v)) & 0xFFu), n4[p][v]); // v_cvt_f32_ubyte<v>
 #pragma unroll
       for (u32 th = 0; th < 2u; th++) {
         if (th >= nth) break;
@@ -1991,25 +2016,30 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
       }
     }
   };
-  u32x4 wq[4][4];
-  u32 hq[4][4];
   if (t0 < t1) {
     fetch_tile(t0);
-#pragma unroll
-    for (u32 k = 0; k < 4u; k++) load_plane(t0, k, wq[k], hq[k]);
+    issue(t0, 0u, 0u, true);
+    issue(t0, 1u, 1u, true);
   }
   for (u32 t = t0; t < t1; t++) {
     const bool more = t + 1u < t1;
     const u32 npair = (gtile(t) + 1u) >> 1;
-    __syncthreads();
+    v8_barrier(); // the previous tile's readers are done
     stage_tile();
-    __syncthreads();
+    v8_barrier();
+#pragma unroll
+    for (u32 p = 0; p < 4u; p++) {
+      d4[p] = *(const v4f *)&sd[w][2u * p + (qn >> 1)][4u * h];
+      n4[p] = -128.0f * d4[p];
+    }
     if (more) fetch_tile(t + 1u);
 #pragma unroll
-    for (u32 k = 0; k < 8u; k++) {
-      plane(k, npair, wq[k & 3u], hq[k & 3u]);
-      if (k < 4u) load_plane(t, k + 4u, wq[k & 3u], hq[k & 3u]);
-      else if (more) load_plane(t + 1u, k - 4u, wq[k & 3u], hq[k & 3u]);
+    for (u32 m = 0; m < 4u; m++) {
+      plane(m, 0u, npair, m & 1u);
+      plane(m, 1u, npair, m & 1u);
+      // issued also after the range's last tile (as zeros), so that the waits count statically
+      if (m < 2u) issue(t, m + 2u, m & 1u, true);
+      else issue(t + 1u, m - 2u, m & 1u, more);
     }
   }
   // join the four quarters of each token (columns t, t + 4, t + 8, t + 12 of a row of 16 lanes)
