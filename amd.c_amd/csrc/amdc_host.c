@@ -274,6 +274,9 @@ enum {
   K_GEMV_Q6K_V8,
   K_GEMMH_Q4_N128,
   K_GEMMH_Q4_N64,
+  K_GEMV_Q4_V16,
+  K_GEMV_Q4K_V16,
+  K_GEMV_Q8_V16,
   K_N
 };
 static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1",  "amdc_gemv_q4_k_t1",  "amdc_gemv_q4_0_t1u1",
@@ -286,7 +289,8 @@ static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1
                                        "amdc_chain",          "amdc_rmsnorm_q8",    "amdc_swiglu_q8",     "amdc_gemv_q8_0_p2",
                                        "amdc_gemv_q6_k_p2",   "amdc_dots_q8_0",     "amdc_dots_q6_k",     "amdc_gemmh_q8_0_m64_n128",
                                        "amdc_gemmh_q8_0_m64_n64", "amdc_gemmh_q6_k_m64_n128", "amdc_gemmh_q6_k_m64_n64",
-                                       "amdc_gemv_q8_0_v8",   "amdc_gemv_q6_k_v8",  "amdc_gemmh_q4_0_m64_n128", "amdc_gemmh_q4_0_m64_n64"};
+                                       "amdc_gemv_q8_0_v8",   "amdc_gemv_q6_k_v8",  "amdc_gemmh_q4_0_m64_n128", "amdc_gemmh_q4_0_m64_n64",
+                                       "amdc_gemv_q4_0_v16",  "amdc_gemv_q4_k_v16", "amdc_gemv_q8_0_v16"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -389,10 +393,8 @@ int amdc_open(const char *hsaco) {
   if (t_gemm < 0) t_gemm = envi("AMDC_GEMM_KERNEL", 0);
   if (t_ksplit < 0) t_ksplit = envi("AMDC_GEMM_KSPLIT", 0);
   /* the token count from which op_gemv runs the prefill GEMM: the reference's IE_GEMM_MIN
-     variable, with a default measured on MI355X (the verify kernels, 8 vectors per launch, are
-     faster up to about 24 tokens: 17408 x 5120 Q4_K, T = 17: 53 us against 67 us for the GEMM;
-     T = 32: 83 against 70) */
-  if (t_gemm_min < 0) t_gemm_min = envi("IE_GEMM_MIN", 25);
+     variable when set; else 0, the MI355X rule of use_gemm */
+  if (t_gemm_min < 0) t_gemm_min = envi("IE_GEMM_MIN", 0);
   x_fuse_nb = (u32)envi("AMDC_GEMVX_FUSE_NB", 128);
   t_form = envi("AMDC_GEMV_FORM", 0);
   g_open = 1;
@@ -598,7 +600,7 @@ static u32 gemv_lanes(u32 ng) {
 
 static int ws_reserve(size_t n);
 
-/* The verify GEMV on int8 MFMA (T <= 8): 64 rows per workgroup, K split
+/* The verify GEMV on int8 MFMA (T <= 16; Q6_K T <= 8): 64 rows per workgroup, K split
  * over tiles of 64 blocks until the workgroups fill the CUs twice. */
 static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                         const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
@@ -616,7 +618,11 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
     part = g_ws;
   }
   void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs, &part};
-  const int k = kind == AMDC_KIND_Q4_K ? K_GEMV_Q4K_V8 : kind == AMDC_KIND_Q8_0 ? K_GEMV_Q8_V8 : kind == AMDC_KIND_Q6_K ? K_GEMV_Q6K_V8 : K_GEMV_Q4_V8;
+  const int v16 = T > 8u; /* the 16-vector form (not for Q6_K: its launches take at most 8) */
+  const int k = kind == AMDC_KIND_Q6_K ? K_GEMV_Q6K_V8
+                : kind == AMDC_KIND_Q4_K ? (v16 ? K_GEMV_Q4K_V16 : K_GEMV_Q4K_V8)
+                : kind == AMDC_KIND_Q8_0 ? (v16 ? K_GEMV_Q8_V16 : K_GEMV_Q8_V8)
+                                         : (v16 ? K_GEMV_Q4_V16 : K_GEMV_Q4_V8);
   HIPCALL(H.ModuleLaunchKernel(g_k[k], wgs, ks, 1, 256, 1, 1, 0, stream, args, NULL));
   if (ks > 1u) {
     const u64 n = (u64)rows * T;
@@ -665,10 +671,12 @@ static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uin
   if ((kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) && (T == 1u || t_unroll > 0))
     return gemv_k8_launch(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
   if (T > 1u && t_unroll <= 0) {
-    /* the int8-MFMA verify kernels, 8 vectors per launch (measured on MI355X, T = 16: 17408 x 5120
-       Q4_K 42.9 us as two such launches against 176 us on the dot4 multi-vector kernel) */
-    for (u32 t0 = 0; t0 < T; t0 += 8u) {
-      const u32 tn = T - t0 < 8u ? T - t0 : 8u;
+    /* the int8-MFMA verify kernels, up to 16 vectors per launch (8 for Q6_K); measured on MI355X,
+       T = 16: 17408 x 5120 Q4_K 42.9 us as two 8-vector launches against 176 us on the dot4
+       multi-vector kernel */
+    const u32 cap = kind == AMDC_KIND_Q6_K ? 8u : 16u;
+    for (u32 t0 = 0; t0 < T; t0 += cap) {
+      const u32 tn = T - t0 < cap ? T - t0 : cap;
       int rc = gemv8_launch(kind, w, xq + (u64)t0 * xs, y + (u64)t0 * ys, rows, nb, bias, res ? res + (u64)t0 * rs : NULL, tn, xs, ys, rs,
                             stream);
       if (rc) return rc;
@@ -929,6 +937,19 @@ int amdc_gemm_q6k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uin
   return gemm_launch(AMDC_KIND_Q6_K, "gemm_q6k", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
 }
 
+/* op_gemv's choice for T > 1: the prefill GEMM or the verify kernels (up to 16 vectors per
+ * launch). IE_GEMM_MIN set (> 0): the reference's rule, T >= IE_GEMM_MIN. Else measured on
+ * MI355X (us per call, verify / GEMM): the verify kernels win up to T = 32 on the 7B-27B layer
+ * shapes (17408 x 5120 Q4_K T = 32: 60 / 70, T = 33: 70 / 70, T = 40: 79 / 71; 4096 x 11008
+ * Q4_0 T = 32: 36 / 43; 5120 x 6144 Q4_K T = 32: 32 / 37), except on matrices of at most 2^24
+ * weights, where the GEMM wins from T = 20 (4096 x 4096 Q4_0 T = 20: 27 / 23, T = 17: 19 / 22;
+ * Q8_0 T = 20: 29 / 27). */
+static int use_gemm(uint32_t T, uint32_t rows, uint32_t nb) {
+  if (t_gemm_min > 0) return (int)T >= t_gemm_min;
+  if (T >= 33u) return 1;
+  return T >= 20u && (u64)rows * nb * 32u <= (1ull << 24);
+}
+
 int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                  const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
   NEED_OPEN();
@@ -936,7 +957,7 @@ int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t 
     int rc = check_mat("op_gemv", kind, w, xq, y, rows, nb);
     return rc ? rc : gemv_launch(kind, w, xq, y, rows, nb, bias, res, 1, 0, 0, 0, stream);
   }
-  if ((int)T >= t_gemm_min) return gemm_launch(kind, "op_gemv", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+  if (use_gemm(T, rows, nb)) return gemm_launch(kind, "op_gemv", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
   return gemv_t(kind, "op_gemv", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
 }
 

@@ -1658,7 +1658,7 @@ __device__ __forceinline__ void v8_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-template <int KIND, int NS>
+template <int KIND, int NS, int NH>
 __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
                                            u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 xs, u32 ys,
                                            u32 rs, float *__restrict__ part) {
@@ -1668,9 +1668,10 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
   __shared__ __attribute__((aligned(16))) u32x4 sw1[4][SC * 128u];
   __shared__ __attribute__((aligned(16))) u32x4 sw2[NS > 2 ? 4 : 1][NS > 2 ? SC * 128u : 1u];
   __shared__ __attribute__((aligned(16))) u32x4 sw3[NS > 2 ? 4 : 1][NS > 2 ? SC * 128u : 1u];
-  __shared__ __attribute__((aligned(16))) u32x4 sB[32][2][16]; // [pair p + 4 k][quarter & 1][column]: a column's nonzero half of K
-  __shared__ __attribute__((aligned(16))) float sda[64][8];    // d_a [block of tile][token]
-  __shared__ __attribute__((aligned(16))) float sxa[64][8];    // Q4_K: d_a asum; Q4_0: asum (as int bits)
+  constexpr u32 NTK = 8u * NH;                                      // tokens per launch: NH halves of 8
+  __shared__ __attribute__((aligned(16))) u32x4 sB[NH][32][2][16]; // [token half][pair p + 4 k][quarter & 1][column]: a column's nonzero half of K
+  __shared__ __attribute__((aligned(16))) float sda[64][NTK];      // d_a [block of tile][token]
+  __shared__ __attribute__((aligned(16))) float sxa[64][NTK];      // Q4_K: d_a asum; Q4_0: asum (as int bits)
   __shared__ __attribute__((aligned(16))) float ssc[4][64][16]; // per wave: s (Q4_K d sc, Q4_0 / Q8_0 d) [block][row]
   const u32 ng = amdc_ngroups(nb), nt = (ng + 7u) >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
   const u32 i16 = lane & 15u, h = lane >> 4, n = i16, tk = n & 7u, pp = n >> 3;
@@ -1705,22 +1706,22 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_t *)(slot(s) + 128u * c + 64u), 16, g1 < gt ? wl1 + base + 16u * g1 : OOB, 0, 0, 0);
     }
   };
-  // activations of tile t in registers (thread: 2 of the 16-byte halves, 2 of the (block, token) scale pairs)
-  u32x4 ra4[4];
-  float rd[2];
-  u32 rx[2];
+  // activations of tile t in registers (thread: 2 NH of the 16-byte halves, 2 NH of the (block, token) scale pairs)
+  u32x4 ra4[4 * NH];
+  float rd[2 * NH];
+  u32 rx[2 * NH];
   u32x4 rh[2];
   auto fetch_tile = [&](u32 t) {
     const u32 gt = gtile(t);
 #pragma unroll
-    for (u32 c = 0; c < 4u; c++) {
+    for (u32 c = 0; c < 4u * NH; c++) {
       const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, gl = bl >> 3, k = bl & 7u, b = 64u * t + 8u * gl + k;
       const bool ok = tok < T && gl < gt && b < nb;
       ra4[c] = __builtin_amdgcn_raw_buffer_load_b128(rxq, ok ? tok * xs + 32u * b + 16u * half : OOB, 0, 0);
     }
 #pragma unroll
-    for (u32 c = 0; c < 2u; c++) {
-      const u32 i = tid + c * NT, tok = i & 7u, bl = i >> 3, b = 64u * t + bl;
+    for (u32 c = 0; c < 2u * NH; c++) {
+      const u32 i = tid + c * NT, tok = i & (NTK - 1u), bl = i / NTK, b = 64u * t + bl;
       const bool ok = tok < T && (bl >> 3) < gt && b < nb;
       rd[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxq, ok ? tok * xs + 32u * nb + 4u * b : OOB, 0, 0));
       rx[c] = __builtin_amdgcn_raw_buffer_load_b32(rxq, ok ? tok * xs + 36u * nb + 4u * b : OOB, 0, 0);
@@ -1734,13 +1735,13 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
   float am[16]; // Q4_K: -(dmin mn) of row i16 for K index 4 q + h of the min-term MFMAs: super-group h + 4 (q / 8), sub-block q % 8
   auto stage_tile = [&]() {
 #pragma unroll
-    for (u32 c = 0; c < 4u; c++) {
+    for (u32 c = 0; c < 4u * NH; c++) {
       const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, gl = bl >> 3, k = bl & 7u;
-      sB[(gl >> 1) + 4u * k][half][tok + 8u * (gl & 1u)] = ra4[c];
+      sB[tok >> 3][(gl >> 1) + 4u * k][half][(tok & 7u) + 8u * (gl & 1u)] = ra4[c];
     }
 #pragma unroll
-    for (u32 c = 0; c < 2u; c++) {
-      const u32 i = tid + c * NT, tok = i & 7u, bl = i >> 3;
+    for (u32 c = 0; c < 2u * NH; c++) {
+      const u32 i = tid + c * NT, tok = i & (NTK - 1u), bl = i / NTK;
       sda[bl][tok] = rd[c];
       sxa[bl][tok] = KIND == AMDC_Q4_K ? rd[c] * (float)(int)rx[c] : __builtin_bit_cast(float, rx[c]);
     }
@@ -1759,19 +1760,22 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
       }
     }
   };
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float acc[NH][4] = {};
   // the MFMAs of plane step k (pairs of the tile) from slot s
   auto plane = [&](u32 k, u32 npair, u32 s) {
     const u32x4 *sl = slot(s);
     const u32 cs = SC == 2u ? 128u * (h & 1u) : 0u; // Q8_0: lanes h odd read the second half plane
-    v4i c[4];
+    v4i c[NH][4];
 #pragma unroll
     for (u32 p = 0; p < 4u; p++) {
       if (p < npair) {
         const u32x4 wq = sl[cs + 8u * i16 + ((2u * p + (h >> 1)) ^ v8_swz(i16))];
         const u32x4 a = KIND == AMDC_Q8_0 ? wq : (wq >> (4u * (h & 1u))) & 0x0F0F0F0Fu;
-        const u32x4 bq = (h >> 1) == pp ? sB[p + 4u * k][h & 1u][n] : (u32x4)(0u); // the other half of K is zero
-        c[p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, bq), (v4i){0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (u32 th = 0; th < (u32)NH; th++) {
+          const u32x4 bq = (h >> 1) == pp ? sB[th][p + 4u * k][h & 1u][n] : (u32x4)(0u); // the other half of K is zero
+          c[th][p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, bq), (v4i){0, 0, 0, 0}, 0, 0, 0);
+        }
       }
     }
 #pragma unroll
@@ -1779,17 +1783,20 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
       if (p >= npair) break;
       const u32 bl = 8u * (2u * p + pp) + k; // this lane's block (column pp)
       const v4f s4 = *(const v4f *)&ssc[w][bl][4u * h];
-      const float da = sda[bl][tk];
-      if (KIND == AMDC_Q4_0) {
-        const u32 as = __builtin_bit_cast(u32, sxa[bl][tk]);
 #pragma unroll
-        for (u32 v = 0; v < 4u; v++) acc[v] += (s4[v] * da) * (float)(int)((u32)c[p][v] - 8u * as);
-      } else if (KIND == AMDC_Q8_0) {
+      for (u32 th = 0; th < (u32)NH; th++) {
+        const float da = sda[bl][tk + 8u * th];
+        if (KIND == AMDC_Q4_0) {
+          const u32 as = __builtin_bit_cast(u32, sxa[bl][tk + 8u * th]);
 #pragma unroll
-        for (u32 v = 0; v < 4u; v++) acc[v] += (s4[v] * da) * (float)c[p][v];
-      } else {
+          for (u32 v = 0; v < 4u; v++) acc[th][v] += (s4[v] * da) * (float)(int)((u32)c[th][p][v] - 8u * as);
+        } else if (KIND == AMDC_Q8_0) {
 #pragma unroll
-        for (u32 v = 0; v < 4u; v++) acc[v] = __builtin_fmaf(s4[v] * (float)c[p][v], da, acc[v]);
+          for (u32 v = 0; v < 4u; v++) acc[th][v] += (s4[v] * da) * (float)c[th][p][v];
+        } else {
+#pragma unroll
+          for (u32 v = 0; v < 4u; v++) acc[th][v] = __builtin_fmaf(s4[v] * (float)c[th][p][v], da, acc[th][v]);
+        }
       }
     }
   };
@@ -1808,14 +1815,17 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
     stage_tile();
     v8_barrier();
     if (KIND == AMDC_Q4_K) { // the min term of the tile's blocks, into the pp = 0 columns
-      v4f m = {acc[0], acc[1], acc[2], acc[3]};
 #pragma unroll
-      for (u32 q = 0; q < 16u; q++) {
-        const u32 bl = 8u * (h + 4u * (q >> 3)) + (q & 7u); // K index 4 q + h
-        const float bx = pp == 0u ? sxa[bl][tk] : 0.0f;
-        m = __builtin_amdgcn_mfma_f32_16x16x4f32(am[q], bx, m, 0, 0, 0);
+      for (u32 th = 0; th < (u32)NH; th++) {
+        v4f m = {acc[th][0], acc[th][1], acc[th][2], acc[th][3]};
+#pragma unroll
+        for (u32 q = 0; q < 16u; q++) {
+          const u32 bl = 8u * (h + 4u * (q >> 3)) + (q & 7u); // K index 4 q + h
+          const float bx = pp == 0u ? sxa[bl][tk + 8u * th] : 0.0f;
+          m = __builtin_amdgcn_mfma_f32_16x16x4f32(am[q], bx, m, 0, 0, 0);
+        }
+        acc[th][0] = m[0], acc[th][1] = m[1], acc[th][2] = m[2], acc[th][3] = m[3];
       }
-      acc[0] = m[0], acc[1] = m[1], acc[2] = m[2], acc[3] = m[3];
     }
     if (more) fetch_tile(t + 1u); // in flight during this tile
 #pragma unroll
@@ -1828,19 +1838,23 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
   }
   // join the two block parities of each token (columns n and n + 8) and store
 #pragma unroll
-  for (u32 v = 0; v < 4u; v++) acc[v] += dpp<0x128>(acc[v]); // row_ror:8
-  if (pp == 0u && tk < T) {
+  for (u32 th = 0; th < (u32)NH; th++) {
 #pragma unroll
-    for (u32 v = 0; v < 4u; v++) {
-      const u32 r = r0 + 4u * h + v;
-      if (r >= rows) continue;
-      if (part) {
-        part[((u64)ks * T + tk) * rows + r] = acc[v];
-      } else {
-        float o = acc[v];
-        if (bias) o = o + bias[r];
-        if (res) o = res[(u64)tk * rs + r] + o;
-        y[(u64)tk * ys + r] = o;
+    for (u32 v = 0; v < 4u; v++) acc[th][v] += dpp<0x128>(acc[th][v]); // row_ror:8
+    const u32 tt = tk + 8u * th;
+    if (pp == 0u && tt < T) {
+#pragma unroll
+      for (u32 v = 0; v < 4u; v++) {
+        const u32 r = r0 + 4u * h + v;
+        if (r >= rows) continue;
+        if (part) {
+          part[((u64)ks * T + tt) * rows + r] = acc[th][v];
+        } else {
+          float o = acc[th][v];
+          if (bias) o = o + bias[r];
+          if (res) o = res[(u64)tt * rs + r] + o;
+          y[(u64)tt * ys + r] = o;
+        }
       }
     }
   }
@@ -1849,17 +1863,33 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_0_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *part) {
-  gemv8_body<AMDC_Q4_0, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+  gemv8_body<AMDC_Q4_0, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
 }
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *part) {
-  gemv8_body<AMDC_Q4_K, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+  gemv8_body<AMDC_Q4_K, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
 }
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *part) {
-  gemv8_body<AMDC_Q8_0, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+  gemv8_body<AMDC_Q8_0, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+}
+// the same for up to 16 vectors (two token halves per MFMA A operand)
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_0_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+                                                                   const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
+                                                                   float *part) {
+  gemv8_body<AMDC_Q4_0, 2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+}
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+                                                                   const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
+                                                                   float *part) {
+  gemv8_body<AMDC_Q4_K, 2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+}
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+                                                                   const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
+                                                                   float *part) {
+  gemv8_body<AMDC_Q8_0, 1, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
 }
 
 // The verify GEMV for Q6_K (T <= 8). A Q6_K weight's scale changes every 16

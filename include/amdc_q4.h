@@ -163,7 +163,7 @@ int amdc_gemv_q6k_x(const void *w, const float *x, float *y, uint32_t rows, uint
                     void *stream);
 
 /* y_t = W x_t for T Q8 vectors (MTP verify, any T >= 1; the weights are
- * read once per 8 vectors, on int8 MFMA, the exact integer dots of
+ * read once per 16 vectors (8 for Q6_K), on int8 MFMA, the exact integer dots of
  * ie_q4q8_block / ie_q4k_dot): x_t at xq + t * xs bytes, y_t at y + t * ys
  * floats, res_t at res + t * rs floats. A library workspace holds split-K
  * partial sums (allocated on the first call of a size: call once outside
@@ -216,10 +216,10 @@ int amdc_gemm_q6k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uin
 
 /* The dispatch of launch_op for OP_GEMV_Q4 / OP_GEMV_Q8 / OP_GEMV_Q4K /
  * OP_GEMV_Q6K over T tokens (src/hip.c:928-1089): T == 1 -> the decode GEMV;
- * T >= IE_GEMM_MIN (env, default 25 on MI355X; the reference's default is
- * 17) -> the GEMM (Q4_0 included, where the
- * reference runs one GEMV per token); else the multi-vector GEMV. kind: any
- * AMDC_KIND_*. */
+ * T >= IE_GEMM_MIN (env) -> the GEMM (Q4_0 included, where the reference
+ * runs one GEMV per token); else the multi-vector GEMV. Without IE_GEMM_MIN
+ * (the reference's default is 17) the MI355X rule: the GEMM for T >= 33, and
+ * for T >= 20 on matrices of at most 2^24 weights. kind: any AMDC_KIND_*. */
 int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                  const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 

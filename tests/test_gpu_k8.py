@@ -184,10 +184,10 @@ def test_gemm_extreme_values(dev, orc, kind):
 
 
 @pytest.mark.parametrize("kind,rows,nb", [(Q8, 200, 544), (Q8, 77, 13), (Q6, 200, 544), (Q6, 70, 24)])
-@pytest.mark.parametrize("T", [1, 2, 7, 8])
+@pytest.mark.parametrize("T", [1, 2, 7, 8, 12, 16])
 def test_verify_splitk(dev, orc, kind, rows, nb, T):
-    """The T <= 8 verify kernels (int8 MFMA; Q6_K one sub-block per MFMA, half dots in separate
-    columns) with K split over workgroups: several splits in a row, with bias and residual, all
+    """The verify kernels (int8 MFMA, T <= 16 per launch, Q6_K T <= 8; Q6_K one half sub-block per
+    K quarter, half dots in separate columns) with K split over workgroups: several splits in a row, with bias and residual, all
     within the bound and a repeated split gives the same bits; the per-vector decode kernel
     (tuning unroll=1) agrees within the bound."""
     c = Case(dev, orc, kind, rows, nb, T, seed=21 + T)

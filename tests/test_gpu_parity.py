@@ -197,7 +197,7 @@ def test_gemm_q4k(dev, orc, rows, nb, T, kern, ks):
 
 def test_op_gemv_dispatch(dev, orc):
     rows, nb = 48, 64
-    for kind, T in ((0, 1), (3, 1), (0, 8), (3, 8), (0, 20), (3, 20), (0, 40), (3, 40)):
+    for kind, T in ((0, 1), (3, 1), (0, 8), (3, 8), (0, 19), (3, 19), (0, 20), (3, 20), (0, 40), (3, 40)):
         c = Case(dev, orc, kind, rows, nb, T, seed=T + kind)
         c.quant()
         dev.op_gemv(kind, c.W, c.Q, c.Y, rows, nb, T, c.xs, rows)
@@ -323,11 +323,12 @@ def test_gemv_fused_quant_special_blocks(dev, orc, kind, nb):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("kind", [0, 3])
-def test_verify_splitk(dev, orc, kind):
-    """The T <= 8 verify kernel with K split over workgroups (partial sums added in split order by the reduce
-    kernel): calls in a row with different splits, bias and residual all match the oracle, and a repeated
-    split gives the same bits."""
-    rows, nb, T = 200, 544, 8
+@pytest.mark.parametrize("T", [8, 11, 16])
+def test_verify_splitk(dev, orc, kind, T):
+    """The verify kernels (T <= 8, and the 16-vector form for T = 9..16) with K split over workgroups
+    (partial sums added in split order by the reduce kernel): calls in a row with different splits, bias
+    and residual all match the oracle, and a repeated split gives the same bits."""
+    rows, nb = 200, 544
     c = Case(dev, orc, kind, rows, nb, T, seed=21)
     c.quant()
     g = np.random.default_rng(3)
@@ -370,3 +371,17 @@ def test_graph_survives_workspace_growth(dev, orc):
         assert np.array_equal(small.Y.download(np.uint32), want)
     y = big.y_gpu()
     assert rel_err(y[255], big.y_oracle(255), big.mag(255)) < TOL
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind,T", [(0, 24), (3, 32), (3, 33)])
+def test_op_gemv_dispatch_large(dev, orc, kind, T):
+    """op_gemv on a matrix of more than 2^24 weights: T = 24 and 32 run the verify kernels (16 + 8,
+    16 + 16 vectors), T = 33 the GEMM; every token matches the oracle."""
+    rows, nb = 1040, 520
+    c = Case(dev, orc, kind, rows, nb, T, seed=T + 7 * kind)
+    c.quant()
+    dev.op_gemv(kind, c.W, c.Q, c.Y, rows, nb, T, c.xs, rows)
+    y = c.y_gpu()
+    for t in range(T):
+        assert rel_err(y[t], c.y_oracle(t), c.mag(t)) < TOL, (kind, T, t)
