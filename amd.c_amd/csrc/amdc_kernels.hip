@@ -13,9 +13,10 @@
 //                      quantization fused), long rows and the Q8_0 / Q6_K kinds
 //                      (_p2) (ie_gemv_q4q8, ie_gemv_q4kq8, ie_gemv_q8q8,
 //                      ie_gemv_q6kq8)
-//   amdc_gemv_{q4_0,q4_k,q8_0,q6_k}_v8, amdc_gemm_reduce
-//                      the verify GEMV, T <= 8 vectors on int8 MFMA, K split
-//                      over workgroups and reduced in split order
+//   amdc_gemv_{q4_0,q4_k,q8_0,q6_k}_v8, amdc_gemv_{q4_0,q4_k,q8_0}_v16,
+//   amdc_gemm_reduce   the verify GEMV, T <= 8 (_v8) or 16 (_v16) vectors on
+//                      int8 MFMA, weights staged through LDS, K split over
+//                      workgroups and reduced in split order
 //                      (ie_gemv_q4kq8_tr8 / _tr / _ts2, ie_gemv_q6kq8_tr8, ...)
 //   amdc_gemv_{q4_0,q4_k}_t{1,8,16}, _t1u1
 //                      dot4 multi-vector GEMVs (a tuning alternative)
