@@ -277,6 +277,7 @@ enum {
   K_GEMV_Q4_V16,
   K_GEMV_Q4K_V16,
   K_GEMV_Q8_V16,
+  K_GEMV_Q6K_V16,
   K_N
 };
 static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1",  "amdc_gemv_q4_k_t1",  "amdc_gemv_q4_0_t1u1",
@@ -290,7 +291,8 @@ static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1
                                        "amdc_gemv_q6_k_p2",   "amdc_dots_q8_0",     "amdc_dots_q6_k",     "amdc_gemmh_q8_0_m64_n128",
                                        "amdc_gemmh_q8_0_m64_n64", "amdc_gemmh_q6_k_m64_n128", "amdc_gemmh_q6_k_m64_n64",
                                        "amdc_gemv_q8_0_v8",   "amdc_gemv_q6_k_v8",  "amdc_gemmh_q4_0_m64_n128", "amdc_gemmh_q4_0_m64_n64",
-                                       "amdc_gemv_q4_0_v16",  "amdc_gemv_q4_k_v16", "amdc_gemv_q8_0_v16"};
+                                       "amdc_gemv_q4_0_v16",  "amdc_gemv_q4_k_v16", "amdc_gemv_q8_0_v16",
+                                       "amdc_gemv_q6_k_v16"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -600,7 +602,7 @@ static u32 gemv_lanes(u32 ng) {
 
 static int ws_reserve(size_t n);
 
-/* The verify GEMV on int8 MFMA (T <= 16; Q6_K T <= 8): 64 rows per workgroup, K split
+/* The verify GEMV on int8 MFMA (T <= 16): 64 rows per workgroup, K split
  * over tiles of 64 blocks until the workgroups fill the CUs twice. */
 static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                         const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
@@ -618,8 +620,8 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
     part = g_ws;
   }
   void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs, &part};
-  const int v16 = T > 8u; /* the 16-vector form (not for Q6_K: its launches take at most 8) */
-  const int k = kind == AMDC_KIND_Q6_K ? K_GEMV_Q6K_V8
+  const int v16 = T > 8u; /* the 16-vector form */
+  const int k = kind == AMDC_KIND_Q6_K ? (v16 ? K_GEMV_Q6K_V16 : K_GEMV_Q6K_V8)
                 : kind == AMDC_KIND_Q4_K ? (v16 ? K_GEMV_Q4K_V16 : K_GEMV_Q4K_V8)
                 : kind == AMDC_KIND_Q8_0 ? (v16 ? K_GEMV_Q8_V16 : K_GEMV_Q8_V8)
                                          : (v16 ? K_GEMV_Q4_V16 : K_GEMV_Q4_V8);
@@ -671,12 +673,11 @@ static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uin
   if ((kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) && (T == 1u || t_unroll > 0))
     return gemv_k8_launch(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
   if (T > 1u && t_unroll <= 0) {
-    /* the int8-MFMA verify kernels, up to 16 vectors per launch (8 for Q6_K); measured on MI355X,
-       T = 16: 17408 x 5120 Q4_K 42.9 us as two 8-vector launches against 176 us on the dot4
+    /* the int8-MFMA verify kernels, up to 16 vectors per launch; measured on MI355X, T = 16:
+       17408 x 5120 Q4_K 30.8 us in one launch, 41 us as two 8-vector launches, 176 us on the dot4
        multi-vector kernel */
-    const u32 cap = kind == AMDC_KIND_Q6_K ? 8u : 16u;
-    for (u32 t0 = 0; t0 < T; t0 += cap) {
-      const u32 tn = T - t0 < cap ? T - t0 : cap;
+    for (u32 t0 = 0; t0 < T; t0 += 16u) {
+      const u32 tn = T - t0 < 16u ? T - t0 : 16u;
       int rc = gemv8_launch(kind, w, xq + (u64)t0 * xs, y + (u64)t0 * ys, rows, nb, bias, res ? res + (u64)t0 * rs : NULL, tn, xs, ys, rs,
                             stream);
       if (rc) return rc;

@@ -13,7 +13,7 @@
 //                      quantization fused), long rows and the Q8_0 / Q6_K kinds
 //                      (_p2) (ie_gemv_q4q8, ie_gemv_q4kq8, ie_gemv_q8q8,
 //                      ie_gemv_q6kq8)
-//   amdc_gemv_{q4_0,q4_k,q8_0,q6_k}_v8, amdc_gemv_{q4_0,q4_k,q8_0}_v16,
+//   amdc_gemv_{q4_0,q4_k,q8_0,q6_k}_v8, amdc_gemv_{q4_0,q4_k,q8_0,q6_k}_v16,
 //   amdc_gemm_reduce   the verify GEMV, T <= 8 (_v8) or 16 (_v16) vectors on
 //                      int8 MFMA, weights staged through LDS, K split over
 //                      workgroups and reduced in split order
@@ -1914,16 +1914,17 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v16(const uint8
 // per (sub-block, half, row) in bytes and d per (super-group, row); s = d sc
 // is formed as fma(d, sc + 128, -128 d), the same single rounding as d * sc.
 // Split K over gridDim.y.
-extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq,
-                                                                   float *__restrict__ y, u32 rows, u32 nb, const float *__restrict__ bias,
-                                                                   const float *__restrict__ res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *__restrict__ part) {
+template <int NQ, int NS>
+__device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y,
+                                               u32 rows, u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T,
+                                               u32 xs, u32 ys, u32 rs, float *__restrict__ part) {
+  constexpr u32 NTK = 4u * NQ; // tokens per launch: NQ groups of 4
   typedef __attribute__((address_space(3))) void lds_t;
   constexpr u32 CH = 128u; // u32x4 per 2 KB chunk (16 rows x 128 bytes)
   __shared__ __attribute__((aligned(16))) u32x4 sw0[4][3u * CH]; // per wave: nibble planes 2m, 2m + 1, high plane m
-  __shared__ __attribute__((aligned(16))) u32x4 sw1[4][3u * CH];
-  __shared__ __attribute__((aligned(16))) u32x4 sB[2][32][16]; // [token half][pair p + 4 k][column]: the column's nonzero quarter
-  __shared__ __attribute__((aligned(16))) float sda[64][8];       // d_a [sub-block][token]
+  __shared__ __attribute__((aligned(16))) u32x4 sw1[NS > 1 ? 4 : 1][NS > 1 ? 3u * CH : 1u];
+  __shared__ __attribute__((aligned(16))) u32x4 sB[NQ][32][16]; // [token group][pair p + 4 k][column]: the column's nonzero quarter
+  __shared__ __attribute__((aligned(16))) float sda[64][NTK];      // d_a [sub-block][token]
   __shared__ __attribute__((aligned(16))) uint8_t ssc[4][64][2][16]; // per wave: sc + 128 [sub-block][half][row]
   __shared__ __attribute__((aligned(16))) float sd[4][8][16];        // per wave: d [super-group][row]
   const u32 ng = nb >> 3, nt = (ng + 7u) >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
@@ -1940,8 +1941,8 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
   const u32 ks = blockIdx.y, nks = gridDim.y, t0 = nt * ks / nks, t1 = nt * (ks + 1u) / nks;
   auto gtile = [&](u32 t) { return ng - 8u * t < 8u ? ng - 8u * t : 8u; };
   auto slot = [&](u32 s) -> u32x4 * {
-    if (s == 0u) return sw0[w];
-    return sw1[w];
+    if (s == 0u || NS == 1) return sw0[w];
+    return sw1[NS > 1 ? w : 0u];
   };
   // step m of tile t into slot s (off: every load out of range)
   auto issue = [&](u32 t, u32 m, u32 s, bool on) {
@@ -1953,21 +1954,21 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_t *)(slot(s) + CH * c + 64u), 16, g1 < gt ? wl1 + base + 16u * g1 : OOB, 0, 0, 0);
     }
   };
-  u32x4 ra4[4];
-  float rd[2];
+  u32x4 ra4[2 * NQ];
+  float rd[NQ];
   u32x4 rh[2];
   u32 rdd[2];
   auto fetch_tile = [&](u32 t) {
     const u32 gt = gtile(t);
 #pragma unroll
-    for (u32 c = 0; c < 4u; c++) {
+    for (u32 c = 0; c < 2u * NQ; c++) {
       const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, b = 64u * t + bl;
       const bool ok = tok < T && (bl >> 3) < gt;
       ra4[c] = __builtin_amdgcn_raw_buffer_load_b128(rxq, ok ? tok * xs + 32u * b + 16u * half : OOB, 0, 0);
     }
 #pragma unroll
-    for (u32 c = 0; c < 2u; c++) {
-      const u32 i = tid + c * NT, tok = i & 7u, bl = i >> 3, b = 64u * t + bl;
+    for (u32 c = 0; c < (u32)NQ; c++) {
+      const u32 i = tid + c * NT, tok = i & (NTK - 1u), bl = i / NTK, b = 64u * t + bl;
       const bool ok = tok < T && (bl >> 3) < gt;
       rd[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxq, ok ? tok * xs + 32u * nb + 4u * b : OOB, 0, 0));
     }
@@ -1980,15 +1981,15 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
   };
   auto stage_tile = [&]() {
 #pragma unroll
-    for (u32 c = 0; c < 4u; c++) { // (half, sub-block (gl, k), token) -> quarter 2 (gl & 1) + half of pair gl / 2
+    for (u32 c = 0; c < 2u * NQ; c++) { // (half, sub-block (gl, k), token) -> quarter 2 (gl & 1) + half of pair gl / 2
       const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, gl = bl >> 3, k = bl & 7u;
       const u32 q = 2u * (gl & 1u) + half;
       sB[tok >> 2][(gl >> 1) + 4u * k][4u * q + (tok & 3u)] = ra4[c];
     }
 #pragma unroll
-    for (u32 c = 0; c < 2u; c++) {
+    for (u32 c = 0; c < (u32)NQ; c++) {
       const u32 i = tid + c * NT;
-      sda[i >> 3][i & 7u] = rd[c];
+      sda[i / NTK][i % NTK] = rd[c];
     }
 #pragma unroll
     for (u32 q = 0; q < 2u; q++) { // this wave's tables: row i16, super-groups h, h + 4
@@ -2001,14 +2002,14 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
           ssc[w][8u * gl + k][e][i16] = (uint8_t)((hword(rh[q], k >> 1) >> (16u * (k & 1u) + 8u * e)) + 128u);
     }
   };
-  float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-  const u32 nth = T > 4u ? 2u : 1u; // token halves with tokens
+  float acc[NQ][4] = {};
+  const u32 nth = (T + 3u) >> 2; // token groups with tokens (group 0 always: T >= 1)
   v4f d4[4], n4[4];                 // d and -128 d of this lane's output rows, super-group 2 p + qn / 2
   // the MFMAs of plane k = 2 m + e from slot s
   auto plane = [&](u32 m, u32 e, u32 npair, u32 s) {
     const u32 k = 2u * m + e;
     const u32x4 *sl = slot(s);
-    v4i c[2][4];
+    v4i c[NQ][4];
     const u32 sft = 4u * (h & 1u);
 #pragma unroll
     for (u32 p = 0; p < 4u; p++) { // the MFMAs of the plane first
@@ -2024,8 +2025,8 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
         }
         const v4i av = {(int)a[0], (int)a[1], (int)a[2], (int)a[3]};
 #pragma unroll
-        for (u32 th = 0; th < 2u; th++)
-          if (th < nth)
+        for (u32 th = 0; th < (u32)NQ; th++)
+          if (th == 0u || th < nth)
             c[th][p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, h == qn ? __builtin_bit_cast(v4i, sB[th][p + 4u * k][n]) : (v4i){0, 0, 0, 0},
                                                              (v4i){0, 0, 0, 0}, 0, 0, 0);
       }
@@ -2039,8 +2040,8 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
 #pragma unroll
       for (u32 v = 0; v < 4u; v++) s4[v] = __builtin_fmaf(d4[p][v], (float)((sc4 >> (8u * v)) & 0xFFu), n4[p][v]); // v_cvt_f32_ubyte<v>
 #pragma unroll
-      for (u32 th = 0; th < 2u; th++) {
-        if (th >= nth) break;
+      for (u32 th = 0; th < (u32)NQ; th++) {
+        if (th > 0u && th >= nth) break;
         const float da = sda[bl][tq + 4u * th];
 #pragma unroll
         for (u32 v = 0; v < 4u; v++) acc[th][v] = __builtin_fmaf(s4[v] * (float)c[th][p][v], da, acc[th][v]);
@@ -2049,8 +2050,8 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
   };
   if (t0 < t1) {
     fetch_tile(t0);
-    issue(t0, 0u, 0u, true);
-    issue(t0, 1u, 1u, true);
+#pragma unroll
+    for (u32 m = 0; m < (u32)NS; m++) issue(t0, m, m, true);
   }
   for (u32 t = t0; t < t1; t++) {
     const bool more = t + 1u < t1;
@@ -2066,16 +2067,16 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
     if (more) fetch_tile(t + 1u);
 #pragma unroll
     for (u32 m = 0; m < 4u; m++) {
-      plane(m, 0u, npair, m & 1u);
-      plane(m, 1u, npair, m & 1u);
+      plane(m, 0u, npair, m % (u32)NS);
+      plane(m, 1u, npair, m % (u32)NS);
       // issued also after the range's last tile (as zeros), so that the waits count statically
-      if (m < 2u) issue(t, m + 2u, m & 1u, true);
-      else issue(t + 1u, m - 2u, m & 1u, more);
+      if (m + (u32)NS < 4u) issue(t, m + (u32)NS, m % (u32)NS, true);
+      else issue(t + 1u, m + (u32)NS - 4u, m % (u32)NS, more);
     }
   }
   // join the four quarters of each token (columns t, t + 4, t + 8, t + 12 of a row of 16 lanes)
 #pragma unroll
-  for (u32 th = 0; th < 2u; th++)
+  for (u32 th = 0; th < (u32)NQ; th++)
 #pragma unroll
     for (u32 v = 0; v < 4u; v++) {
       acc[th][v] += dpp<0x128>(acc[th][v]); // row_ror:8
@@ -2083,7 +2084,7 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
     }
   if (qn == 0u) {
 #pragma unroll
-    for (u32 th = 0; th < 2u; th++) {
+    for (u32 th = 0; th < (u32)NQ; th++) {
       const u32 tk = tq + 4u * th;
       if (tk >= T) continue;
 #pragma unroll
@@ -2101,4 +2102,16 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_
       }
     }
   }
+}
+
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+                                                                   const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
+                                                                   float *part) {
+  gemv8_q6k_body<2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+}
+// up to 16 vectors: four token groups per A operand, a ring of one step (72 KB of LDS, 2 workgroups per CU)
+extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
+                                                                    float *part) {
+  gemv8_q6k_body<4, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
 }

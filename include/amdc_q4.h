@@ -163,7 +163,7 @@ int amdc_gemv_q6k_x(const void *w, const float *x, float *y, uint32_t rows, uint
                     void *stream);
 
 /* y_t = W x_t for T Q8 vectors (MTP verify, any T >= 1; the weights are
- * read once per 16 vectors (8 for Q6_K), on int8 MFMA, the exact integer dots of
+ * read once per 16 vectors, on int8 MFMA, the exact integer dots of
  * ie_q4q8_block / ie_q4k_dot): x_t at xq + t * xs bytes, y_t at y + t * ys
  * floats, res_t at res + t * rs floats. A library workspace holds split-K
  * partial sums (allocated on the first call of a size: call once outside
