@@ -123,7 +123,7 @@ ABI = {
     "amdc_chain_destroy": (C.c_int, [_P]),
 }
 
-CHAIN_QUANT, CHAIN_GEMV = 0, 1
+CHAIN_QUANT, CHAIN_GEMV, CHAIN_GEMV_X = 0, 1, 2
 
 
 class ChainOp(C.Structure):
@@ -428,6 +428,11 @@ def chain_quant(x, q, nb, sync=True):
 def chain_gemv(kind, w, xq, y, rows, nb, bias=None, res=None, sync=True):
     """A decode-GEMV operation of a GEMV chain: w, xq (Q8) -> y."""
     return ChainOp(CHAIN_GEMV, kind, int(sync), rows, nb, _p(w), None, None, _p(xq), _p(y), _p(bias), _p(res))
+
+
+def chain_gemv_x(kind, w, x, y, rows, nb, bias=None, res=None, sync=True):
+    """A decode-GEMV operation on the f32 vector x (quantized inside the operation): w, x -> y."""
+    return ChainOp(CHAIN_GEMV_X, kind, int(sync), rows, nb, _p(w), _p(x), None, None, _p(y), _p(bias), _p(res))
 
 
 class Chain:

@@ -1025,13 +1025,14 @@ int amdc_chain_create(const amdc_chain_op *ops, uint32_t n, void **chain) {
       if (!o->x || !o->q || !o->nb) rc = fail(AMDC_EINVAL, "chain op %u: quantize needs x, q and nb", k);
       else if (!aligned16(o->x)) rc = fail(AMDC_EINVAL, "chain op %u: x must be 16-byte aligned", k);
       e->type = 0, e->a = o->x, e->b = o->q;
-    } else if (o->type == AMDC_CHAIN_GEMV) {
-      rc = check_mat("chain gemv", o->kind, o->w, o->xq, o->y, o->rows, o->nb);
+    } else if (o->type == AMDC_CHAIN_GEMV || o->type == AMDC_CHAIN_GEMV_X) {
+      const int fq = o->type == AMDC_CHAIN_GEMV_X; /* the f32 vector, quantized by every workgroup */
+      rc = check_mat("chain gemv", o->kind, o->w, fq ? (const uint8_t *)o->x : o->xq, o->y, o->rows, o->nb);
       if (!rc && o->kind != AMDC_KIND_Q4_0 && o->kind != AMDC_KIND_Q4_K)
         rc = fail(AMDC_EINVAL, "chain op %u: kind %d (the chain runs Q4_0 and Q4_K GEMVs)", k, o->kind);
       if (!rc && 320u * amdc_ngroups(o->nb) > GEMV_LDS_T1) rc = fail(AMDC_EINVAL, "chain op %u: nb %u too large", k, o->nb);
-      e->type = o->kind == AMDC_KIND_Q4_K ? 2u : 1u, e->rows = o->rows, e->L = gemv_lanes(amdc_ngroups(o->nb));
-      e->a = o->w, e->b = (void *)o->xq, e->y = o->y, e->bias = o->bias, e->res = o->res;
+      e->type = (o->kind == AMDC_KIND_Q4_K ? 2u : 1u) + (fq ? 2u : 0u), e->rows = o->rows, e->L = gemv_lanes(amdc_ngroups(o->nb));
+      e->a = o->w, e->b = fq ? (void *)o->x : (void *)o->xq, e->y = o->y, e->bias = o->bias, e->res = o->res;
       if (!rc && 320u * amdc_ngroups(o->nb) > lds) lds = 320u * amdc_ngroups(o->nb);
     } else {
       rc = fail(AMDC_EINVAL, "chain op %u: type %d", k, o->type);

@@ -787,7 +787,8 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_p2(const uint8_
 // the abort flag, every workgroup leaves, and the host reports the error.
 // The last workgroup to finish sets the counters back to zero.
 struct ChainOp { // the host's amdc_chain_op, resolved (amdc_host.c): 64 bytes
-  u32 type;      // 0: quantize a -> b (nb blocks); 1, 2: GEMV Q4_0 / Q4_K, W a, Q8 vector b -> y
+  u32 type;      // 0: quantize a -> b (nb blocks); 1, 2: GEMV Q4_0 / Q4_K, W a, Q8 vector b -> y;
+                 // 3, 4: the same with the f32 vector b, quantized by every workgroup into its LDS
   u32 sync;      // grid barrier after this operation
   u32 rows, nb, L, pad;
   const void *a;
@@ -849,7 +850,7 @@ __device__ __forceinline__ bool chain_barrier(u32 *sync, u32 nbar, u32 spin_ns) 
 // the last item reads row 0's first super-group again and is not used), then
 // the arithmetic; it[0] of the first batch may already be loaded (pre).
 #define CHI 2u
-template <int KIND>
+template <int KIND, bool FQ>
 __device__ __forceinline__ void chain_gemv(const ChainOp &op, Item (&it)[CHI], bool pre, uint8_t *smem) {
   const uint8_t *W = (const uint8_t *)op.a, *xq = (const uint8_t *)op.b;
   const u32 rows = op.rows, nb = op.nb, L = op.L, ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
@@ -876,8 +877,21 @@ __device__ __forceinline__ void chain_gemv(const ChainOp &op, Item (&it)[CHI], b
   };
   if (nit) load_batch(0u, pre ? 1u : 0u);
   __asm__ volatile("" ::: "memory"); // the weight loads ahead of the activation loads
+  if (FQ) { // the f32 vector (written by other workgroups: coherent loads), quantized as amdc_quant_q8
+    const __amdgpu_buffer_rsrc_t rx = rsrc(xq, 128u * nb);
+    const u32 e = tid & 7u;
+    FusedQ8 fq;
+    for (u32 b0 = 0; b0 < nblk; b0 += 32u * QCH) {
+#pragma unroll
+      for (u32 c = 0; c < QCH; c++) {
+        const u32 b = b0 + 32u * c + (tid >> 3);
+        fq.xv[c] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rx, b < nb ? 128u * b + 16u * e : 0xFFFFFFF0u, 0, CPOL_SC1));
+      }
+      fq.quant(b0, nb, ng, s_lo, s_hi, s_d, s_as, nullptr);
+    }
+  }
   const __amdgpu_buffer_rsrc_t rq = rsrc(xq, 40u * nb);
-  for (u32 j = tid; j < nblk; j += NT) { // the Q8 vector, written by other workgroups: coherent loads
+  for (u32 j = tid; !FQ && j < nblk; j += NT) { // the Q8 vector, written by other workgroups: coherent loads
     const u32 p = (j & 7u) * ng + (j >> 3);
     u32x4 lo = (u32x4)(0u), hi = (u32x4)(0u);
     float d = 0.0f;
@@ -955,7 +969,7 @@ __device__ __forceinline__ bool chain_preload(const ChainOp &op, Item &cur) {
   if (blockIdx.x >= nrg) return false;
   const u32 r = blockIdx.x * rpg + wv * rpw + q;
   const uint8_t *wr = (const uint8_t *)op.a + (u64)(r < op.rows ? r : op.rows - 1u) * amdc_row_bytes(op.nb);
-  if (op.type == 1u) load_item<AMDC_Q4_0>(cur, wr, ng, l, l < ng);
+  if (op.type == 1u || op.type == 3u) load_item<AMDC_Q4_0>(cur, wr, ng, l, l < ng);
   else load_item<AMDC_Q4_K>(cur, wr, ng, l, l < ng);
   return true;
 }
@@ -967,8 +981,10 @@ extern "C" __global__ __launch_bounds__(256) void amdc_chain(const ChainOp *__re
   for (u32 k = 0; k < n; k++) {
     const ChainOp op = ops[k];
     if (op.type == 0u) chain_quant(op);
-    else if (op.type == 1u) chain_gemv<AMDC_Q4_0>(op, it, pre == k, smem);
-    else chain_gemv<AMDC_Q4_K>(op, it, pre == k, smem);
+    else if (op.type == 1u) chain_gemv<AMDC_Q4_0, false>(op, it, pre == k, smem);
+    else if (op.type == 2u) chain_gemv<AMDC_Q4_K, false>(op, it, pre == k, smem);
+    else if (op.type == 3u) chain_gemv<AMDC_Q4_0, true>(op, it, pre == k, smem);
+    else chain_gemv<AMDC_Q4_K, true>(op, it, pre == k, smem);
     if (op.sync && k + 1u < n) {
       // the next GEMV's first weights go out before the wait (quantizations between do not touch it[])
       u32 j = k + 1u;

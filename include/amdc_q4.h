@@ -254,12 +254,15 @@ int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kern
  *   AMDC_CHAIN_QUANT: x (32 nb floats) -> q (Q8 buffer, 40 nb bytes)
  *   AMDC_CHAIN_GEMV:  kind, w (rows x nb), xq (Q8) -> y (rows floats),
  *                     optional bias / res (rows floats) as amdc_gemv_q4
+ *   AMDC_CHAIN_GEMV_X: the same on x (32 nb floats): every workgroup
+ *                     quantizes x into its LDS (as amdc_gemv_q4_x, no Q8
+ *                     buffer, no barrier between quantization and GEMV)
  * An operation that reads what an earlier one writes must come after a sync
  * (the check compares buffer pointers). All workgroups must be resident at
  * once: the grid is what the device holds (at most 2 per CU); nothing else
  * should run on the device meanwhile. A barrier that waits longer than 200 ms
  * aborts the launch (every workgroup leaves); amdc_chain_check reports it. */
-enum { AMDC_CHAIN_QUANT = 0, AMDC_CHAIN_GEMV = 1 };
+enum { AMDC_CHAIN_QUANT = 0, AMDC_CHAIN_GEMV = 1, AMDC_CHAIN_GEMV_X = 2 };
 typedef struct {
   int type, kind, sync;
   uint32_t rows, nb;

@@ -96,3 +96,50 @@ def test_chain_rejects_read_before_sync(dev, orc):
         op = dev.chain_quant(x0, q0, 8)
         op.type = 7
         dev.Chain([op])
+
+
+def test_chain_fused_quant_equals_separate_launches(dev, orc):
+    """GEMV operations on f32 vectors (AMDC_CHAIN_GEMV_X: every workgroup quantizes its input into LDS, no
+    Q8 buffer, no barrier between quantization and GEMV): x0 -> A (Q4_0, nb 13) -> y1 -> B (Q4_K, bias and
+    residual) -> y2 -> C and D (one input, no barrier between them), then E (Q4_0, nb 600: the quantization
+    in two passes) on x0 again. Each output equals amdc_quant_q8 + amdc_gemv with the same lane split, bit
+    for bit, across repeated launches."""
+    g = np.random.default_rng(5)
+    A = Case(dev, orc, 0, 256, 13, seed=11)
+    B = Case(dev, orc, 3, 1024, 8, seed=12)
+    C_ = Case(dev, orc, 0, 77, 32, seed=13)
+    D = Case(dev, orc, 3, 300, 32, seed=14)
+    E = Case(dev, orc, 0, 90, 600, seed=15)
+    x0 = dev.DevBuf.of(A.x[0])
+    xe = dev.DevBuf.of(E.x[0])
+    y1, y2, y3, y4, y5 = (dev.DevBuf(4 * r) for r in (256, 1024, 77, 300, 90))
+    bias = dev.DevBuf.of(g.standard_normal(1024).astype(np.float32))
+    res = dev.DevBuf.of(g.standard_normal(1024).astype(np.float32))
+    ops = [dev.chain_gemv_x(0, A.W, x0, y1, 256, 13),
+           dev.chain_gemv_x(3, B.W, y1, y2, 1024, 8, bias=bias, res=res),
+           dev.chain_gemv_x(0, C_.W, y2, y3, 77, 32, sync=False),
+           dev.chain_gemv_x(3, D.W, y2, y4, 300, 32),
+           dev.chain_gemv_x(0, E.W, xe, y5, 90, 600)]
+    ch = dev.Chain(ops)
+    want = []
+    q = dev.DevBuf(q8_stride(600))
+    z1, z2, z3, z4, z5 = (dev.DevBuf(4 * r) for r in (256, 1024, 77, 300, 90))
+    dev.quant_q8(x0, q, 13)
+    dev.gemv(0, A.W, q, z1, 256, 13)
+    dev.quant_q8(z1, q, 8)
+    dev.gemv(3, B.W, q, z2, 1024, 8, bias=bias, res=res)
+    dev.quant_q8(z2, q, 32)
+    dev.gemv(0, C_.W, q, z3, 77, 32)
+    dev.gemv(3, D.W, q, z4, 300, 32)
+    dev.quant_q8(xe, q, 600)
+    dev.gemv(0, E.W, q, z5, 90, 600)
+    want = [b.download(np.uint32) for b in (z1, z2, z3, z4, z5)]
+    for rep in range(3):
+        for b in (y1, y2, y3, y4, y5):
+            b.fill(0)
+        ch.launch()
+        ch.check()
+        got = [b.download(np.uint32) for b in (y1, y2, y3, y4, y5)]
+        for i, (gt, wt) in enumerate(zip(got, want)):
+            assert np.array_equal(gt, wt), (rep, i)
+    assert rel_err(y5.download(np.float32), E.y_oracle(0), E.mag(0)) < TOL
