@@ -465,12 +465,12 @@ __device__ __forceinline__ float item_dot(const typename ItemOf<KIND>::type &it,
 // unconditional (a block past nb reads the last block again and takes zeros),
 // so that no branch joins them. The max and the sum of a block's 8 lanes go
 // by DPP (xor 1, xor 2, then the half-row mirror).
-struct FusedQ8 {
-  v4f xv[QCH];
+template <u32 NC> struct FusedQ8T {
+  v4f xv[NC];
   __device__ __forceinline__ void load(const float *__restrict__ xf, u32 nb, u32 b0) {
     const u32 tid = threadIdx.x, e = tid & 7u;
 #pragma unroll
-    for (u32 c = 0; c < QCH; c++) {
+    for (u32 c = 0; c < NC; c++) {
       const u32 b = b0 + 32u * c + (tid >> 3);
       const v4f v = *(const v4f *)(xf + 32u * (b < nb ? b : nb - 1u) + 4u * e);
       xv[c] = b < nb ? v : (v4f){0.0f, 0.0f, 0.0f, 0.0f};
@@ -508,6 +508,7 @@ struct FusedQ8 {
     }
   }
 };
+typedef FusedQ8T<QCH> FusedQ8;
 
 template <int KIND, bool FQ>
 __device__ __forceinline__ void gemv1_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
@@ -880,10 +881,10 @@ __device__ __forceinline__ void chain_gemv(const ChainOp &op, Item (&it)[CHI], b
   if (FQ) { // the f32 vector (written by other workgroups: coherent loads), quantized as amdc_quant_q8
     const __amdgpu_buffer_rsrc_t rx = rsrc(xq, 128u * nb);
     const u32 e = tid & 7u;
-    FusedQ8 fq;
-    for (u32 b0 = 0; b0 < nblk; b0 += 32u * QCH) {
+    FusedQ8T<4> fq; // 4 passes of 32 blocks in flight: the chain kernel keeps 2 workgroups per CU
+    for (u32 b0 = 0; b0 < nblk; b0 += 32u * 4u) {
 #pragma unroll
-      for (u32 c = 0; c < QCH; c++) {
+      for (u32 c = 0; c < 4u; c++) {
         const u32 b = b0 + 32u * c + (tid >> 3);
         fq.xv[c] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rx, b < nb ? 128u * b + 16u * e : 0xFFFFFFF0u, 0, CPOL_SC1));
       }
@@ -974,7 +975,7 @@ __device__ __forceinline__ bool chain_preload(const ChainOp &op, Item &cur) {
   return true;
 }
 
-extern "C" __global__ __launch_bounds__(256) void amdc_chain(const ChainOp *__restrict__ ops, u32 n, u32 *sync, u32 spin_ns) {
+extern "C" __global__ __launch_bounds__(256, 2) void amdc_chain(const ChainOp *__restrict__ ops, u32 n, u32 *sync, u32 spin_ns) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   u32 nbar = 0, pre = 0xFFFFFFFFu; // pre: the operation whose first item it[0] holds
   Item it[CHI];

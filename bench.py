@@ -177,12 +177,18 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
     graphs = [timer.graph(lambda s, ci=ci: step(ci, s)) for ci in range(G.copies)]
     ms_launches = timer.replay_ms(graphs, steps, warmup)
     del graphs
-    # the same step as one GEMV chain launch per weight copy: each GEMV quantizes its f32 input in
-    # every workgroup (as amdc_gemv_q4_x), a grid barrier after each GEMV (the next one waits for it,
-    # as the launches wait for each other)
+    # the same step as one GEMV chain launch per weight copy, a grid barrier after each operation
+    # (the next one waits for it, as the launches wait for each other); as amdc_gemv_q4_x, a GEMV
+    # quantizes its f32 input in every workgroup for nb <= 128, else after a quantize operation
+    Qc = amdc.DevBuf(q8_stride(cols_max // 32))
     chains = []
     for ci in range(G.copies):
-        ops = [amdc.chain_gemv_x(kind, G.dev[ci][gi], X, Y, r, c // 32) for gi, (name, r, c, _) in enumerate(groups)]
+        ops = []
+        for gi, (name, r, c, _) in enumerate(groups):
+            if c // 32 <= 128:
+                ops.append(amdc.chain_gemv_x(kind, G.dev[ci][gi], X, Y, r, c // 32))
+            else:
+                ops += [amdc.chain_quant(X, Qc, c // 32), amdc.chain_gemv(kind, G.dev[ci][gi], Qc, Y, r, c // 32)]
         chains.append(amdc.Chain(ops))
     chains[0].launch()
     chains[0].check()
