@@ -219,7 +219,8 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
 
 
 def verify_set(steps, seed, timer):
-    """c3: T = 8 vectors against each matrix (weights read once per launch)."""
+    """c3: T = 8 vectors against each matrix (weights read once per launch); also T = 16 (the
+    16-vector kernels, one launch)."""
     cfg = synth.CONFIGS["c3"]
     T = cfg["T"]
     out = {}
@@ -227,15 +228,19 @@ def verify_set(steps, seed, timer):
         M = Mats(kind, [(name, r, c)], seed + i, min_bytes=1 << 30)
         nb = c // 32
         xs = q8_stride(nb)
-        X = amdc.DevBuf.of(synth.activations(T, c, seed + 50 + i))
-        Q = amdc.DevBuf(T * xs)
-        Y = amdc.DevBuf(4 * T * r)
-        amdc.quant_q8(X, Q, nb, T, 4 * c, xs)
-        amdc.gemv_t(kind, M.dev[0][0], Q, Y, r, nb, T, xs, r)  # sizes the library's workspace before the capture
-        t = timer.per_launch_ms(lambda j, s: amdc.gemv_t(kind, M.dev[j % M.copies][0], Q, Y, r, nb, T, xs, r, stream=s), M.copies)
+        X = amdc.DevBuf.of(synth.activations(16, c, seed + 50 + i))
+        Q = amdc.DevBuf(16 * xs)
+        Y = amdc.DevBuf(4 * 16 * r)
+        amdc.quant_q8(X, Q, nb, 16, 4 * c, xs)
+        ts = {}
+        for tn in (T, 16):
+            amdc.gemv_t(kind, M.dev[0][0], Q, Y, r, nb, tn, xs, r)  # sizes the library's workspace before the capture
+            ts[tn] = timer.per_launch_ms(lambda j, s: amdc.gemv_t(kind, M.dev[j % M.copies][0], Q, Y, r, nb, tn, xs, r, stream=s),
+                                         M.copies)
+        t = ts[T]
         b = wbytes(r, c)
         out[name] = {"rows": r, "cols": c, "T": T, "us": round(t * 1e3, 3), "GB/s": round(b / t / 1e6, 1),
-                     "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4)}
+                     "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4), "T16_us": round(ts[16] * 1e3, 3)}
         del M
     return out
 
