@@ -1663,6 +1663,8 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *
 // the waits for each step's loads are counted separately; within a wave's
 // plane, row i's 16-byte column c holds super-group c ^ v8_swz(i), so that the
 // A reads (16 rows, one column pair) fall on distinct banks.
+// NH token halves of 8 (T <= 8 NH): the _v16 kernels take two, each A operand
+// then feeds two MFMAs.
 // Split K over gridDim.y (tiles [t0, t1) per split, partial sums to part).
 __device__ __forceinline__ u32 v8_swz(u32 i) { return (i & 7u) ^ ((i >> 3) & 1u); }
 // A workgroup barrier for LDS written with ds_write only: the waves' LDS
