@@ -1027,13 +1027,26 @@ int amdc_chain_create(const amdc_chain_op *ops, uint32_t n, void **chain) {
       e->type = 0, e->a = o->x, e->b = o->q;
     } else if (o->type == AMDC_CHAIN_GEMV || o->type == AMDC_CHAIN_GEMV_X) {
       const int fq = o->type == AMDC_CHAIN_GEMV_X; /* the f32 vector, quantized by every workgroup */
+      const int k8 = o->kind == AMDC_KIND_Q8_0 || o->kind == AMDC_KIND_Q6_K;
+      const u32 ng = amdc_ngroups(o->nb), need = (o->kind == AMDC_KIND_Q6_K ? 352u : 320u) * ng;
       rc = check_mat("chain gemv", o->kind, o->w, fq ? (const uint8_t *)o->x : o->xq, o->y, o->rows, o->nb);
-      if (!rc && o->kind != AMDC_KIND_Q4_0 && o->kind != AMDC_KIND_Q4_K)
-        rc = fail(AMDC_EINVAL, "chain op %u: kind %d (the chain runs Q4_0 and Q4_K GEMVs)", k, o->kind);
-      if (!rc && 320u * amdc_ngroups(o->nb) > GEMV_LDS_T1) rc = fail(AMDC_EINVAL, "chain op %u: nb %u too large", k, o->nb);
-      e->type = (o->kind == AMDC_KIND_Q4_K ? 2u : 1u) + (fq ? 2u : 0u), e->rows = o->rows, e->L = gemv_lanes(amdc_ngroups(o->nb));
-      e->a = o->w, e->b = fq ? (void *)o->x : (void *)o->xq, e->y = o->y, e->bias = o->bias, e->res = o->res;
-      if (!rc && 320u * amdc_ngroups(o->nb) > lds) lds = 320u * amdc_ngroups(o->nb);
+      if (!rc && fq && k8) rc = fail(AMDC_EINVAL, "chain op %u: the f32-input GEMV takes Q4_0 and Q4_K (quantize Q8_0 / Q6_K inputs first)", k);
+      if (!rc && k8 && (u64)o->rows * amdc_row_bytes_k(o->kind, o->nb) + amdc_row_bytes_k(o->kind, o->nb) >= (1ull << 32))
+        rc = fail(AMDC_EINVAL, "chain op %u: the matrix must be under 4 GiB", k);
+      if (!rc && need > GEMV_LDS_T1) rc = fail(AMDC_EINVAL, "chain op %u: nb %u too large", k, o->nb);
+      if (k8) {
+        /* the lanes per row of the decode launch (gemv_k8_launch): bit-equal results */
+        const u32 cus = g_cus > 0 ? (u32)g_cus : 256u;
+        u32 L = 4u;
+        while (L < 64u && 3u * L < ng) L <<= 1;
+        while (L < 64u && L < ng && (o->rows + 4u * (64u / L) - 1u) / (4u * (64u / L)) < 2u * cus) L <<= 1;
+        if (t_lanes > 0) L = (u32)t_lanes;
+        e->type = o->kind == AMDC_KIND_Q6_K ? 6u : 5u, e->L = L;
+      } else {
+        e->type = (o->kind == AMDC_KIND_Q4_K ? 2u : 1u) + (fq ? 2u : 0u), e->L = gemv_lanes(ng);
+      }
+      e->rows = o->rows, e->a = o->w, e->b = fq ? (void *)o->x : (void *)o->xq, e->y = o->y, e->bias = o->bias, e->res = o->res;
+      if (!rc && need > lds) lds = need;
     } else {
       rc = fail(AMDC_EINVAL, "chain op %u: type %d", k, o->type);
     }

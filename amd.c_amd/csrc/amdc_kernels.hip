@@ -620,6 +620,31 @@ struct Item2 {
   float b, r;
 };
 
+// The loads of super-group g of the row at byte base of resource rw (base past
+// the resource: every load returns zeros), cache policy COH.
+template <int KIND, int COH>
+__device__ __forceinline__ void item_load(typename ItemOf<KIND>::type &w, __amdgpu_buffer_rsrc_t rw, u32 base, u32 g, u32 ng) {
+  const u32 t = g >> 3, gt = ng - 8u * t < 8u ? ng - 8u * t : 8u;
+  w.h = __builtin_amdgcn_raw_buffer_load_b128(rw, base + 16u * g, 0, COH);
+  if constexpr (KIND == AMDC_Q8_0) {
+    const u32 o0 = base + 16u * ng + 2048u * t + 16u * (g & 7u);
+#pragma unroll
+    for (u32 k = 0; k < 16u; k++) w.n[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, o0 + 16u * gt * k, 0, COH);
+  } else if constexpr (KIND == AMDC_Q6_K) {
+    const u32 D = amdc_q6k_dpad(ng), o0 = base + 16u * ng + D + 1024u * t + 16u * (g & 7u);
+    const u32 o1 = base + 144u * ng + D + 512u * t + 16u * (g & 7u);
+#pragma unroll
+    for (u32 k = 0; k < 8u; k++) w.n[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, o0 + 16u * gt * k, 0, COH);
+#pragma unroll
+    for (u32 k = 0; k < 4u; k++) w.x[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, o1 + 16u * gt * k, 0, COH);
+    w.d = __builtin_amdgcn_raw_buffer_load_b16(rw, base + 16u * ng + 2u * g, 0, COH);
+  } else {
+    const u32 o0 = base + 16u * ng + 1024u * t + 16u * (g & 7u);
+#pragma unroll
+    for (u32 k = 0; k < 8u; k++) w.n[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, o0 + 16u * gt * k, 0, COH);
+  }
+}
+
 template <int KIND>
 __device__ __forceinline__ void gemv2_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
                                            u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 L) {
@@ -642,26 +667,7 @@ __device__ __forceinline__ void gemv2_body(const uint8_t *__restrict__ W, const 
   auto load = [&](Item2<KIND> &it, u32 f, u32 j, u32 i) {
     const u32 r = (blockIdx.x + j * gridDim.x) * rpg + rbase, g = l + L * i;
     const bool ok = f < n && g < ng && r < rows;
-    const u32 t = g >> 3, gt = ng - 8u * t < 8u ? ng - 8u * t : 8u;
-    const u32 base = ok ? r * RB : NR;
-    it.w.h = __builtin_amdgcn_raw_buffer_load_b128(rw, base + 16u * g, 0, 0);
-    if constexpr (KIND == AMDC_Q8_0) {
-      const u32 o0 = base + 16u * ng + 2048u * t + 16u * (g & 7u);
-#pragma unroll
-      for (u32 k = 0; k < 16u; k++) it.w.n[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, o0 + 16u * gt * k, 0, 0);
-    } else if constexpr (KIND == AMDC_Q6_K) {
-      const u32 D = amdc_q6k_dpad(ng), o0 = base + 16u * ng + D + 1024u * t + 16u * (g & 7u);
-      const u32 o1 = base + 144u * ng + D + 512u * t + 16u * (g & 7u);
-#pragma unroll
-      for (u32 k = 0; k < 8u; k++) it.w.n[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, o0 + 16u * gt * k, 0, 0);
-#pragma unroll
-      for (u32 k = 0; k < 4u; k++) it.w.x[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, o1 + 16u * gt * k, 0, 0);
-      it.w.d = __builtin_amdgcn_raw_buffer_load_b16(rw, base + 16u * ng + 2u * g, 0, 0);
-    } else {
-      const u32 o0 = base + 16u * ng + 1024u * t + 16u * (g & 7u);
-#pragma unroll
-      for (u32 k = 0; k < 8u; k++) it.w.n[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, o0 + 16u * gt * k, 0, 0);
-    }
+    item_load<KIND, 0>(it.w, rw, ok ? r * RB : NR, g, ng);
     const u32 ro = f < n && r < rows ? 4u * r : 0xFFFFFFF0u;
     it.b = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, ro, 0, 0));
     it.r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, ro, 0, 0));
@@ -789,7 +795,8 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_p2(const uint8_
 // The last workgroup to finish sets the counters back to zero.
 struct ChainOp { // the host's amdc_chain_op, resolved (amdc_host.c): 64 bytes
   u32 type;      // 0: quantize a -> b (nb blocks); 1, 2: GEMV Q4_0 / Q4_K, W a, Q8 vector b -> y;
-                 // 3, 4: the same with the f32 vector b, quantized by every workgroup into its LDS
+                 // 3, 4: the same with the f32 vector b, quantized by every workgroup into its LDS;
+                 // 5, 6: GEMV Q8_0 / Q6_K, W a, Q8 vector b -> y
   u32 sync;      // grid barrier after this operation
   u32 rows, nb, L, pad;
   const void *a;
@@ -934,6 +941,71 @@ __device__ __forceinline__ void chain_gemv(const ChainOp &op, Item (&it)[CHI], b
 // the quantization of op.a (nb blocks of 32 floats) into the Q8 buffer op.b,
 // blocks 32 p .. 32 p + 31 by workgroup p, + 32 gridDim.x, ... (8 lanes per
 // block, 4 values per lane; the arithmetic of amdc_quant_q8)
+// A Q8_0 / Q6_K GEMV operation of the chain: the decode kernel's item loads
+// and arithmetic (gemv2_body, the same lanes per row: bit-equal results), one
+// item at a time, the Q8 vector written by other workgroups (coherent loads),
+// the rows of the workgroup as the GEMV operations above; no weight preload
+// before a barrier.
+template <int KIND>
+__device__ __forceinline__ void chain_gemv_k8(const ChainOp &op, uint8_t *smem) {
+  const uint8_t *W = (const uint8_t *)op.a, *xq = (const uint8_t *)op.b;
+  const u32 rows = op.rows, nb = op.nb, L = op.L, ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw;
+  const u32 nrg = (rows + rpg - 1u) / rpg, ni = (ng + L - 1u) / L, nblk = 8u * ng;
+  const u32 mine = blockIdx.x < nrg ? (nrg - blockIdx.x + gridDim.x - 1u) / gridDim.x : 0u, nit = mine * ni;
+  const u32 RB = (u32)amdc_row_bytes_k(KIND, nb), NR = rows * RB; // the host checks NR + RB < 2^32
+  u32x4 *s_lo = (u32x4 *)smem;
+  u32x4 *s_hi = s_lo + nblk;
+  float *s_d = (float *)(s_hi + nblk);
+  u32 *s_as = (u32 *)(s_d + nblk);
+  const __amdgpu_buffer_rsrc_t rw = rsrc(W, NR);
+  typename ItemOf<KIND>::type A;
+  auto ld = [&](typename ItemOf<KIND>::type &it, u32 f) {
+    const u32 j = f / ni, i = f - j * ni, g = l + L * i, r = (blockIdx.x + j * gridDim.x) * rpg + wv * rpw + q;
+    item_load<KIND, 0>(it, rw, f < nit && g < ng && r < rows ? r * RB : NR, g, ng);
+  };
+  if (nit) ld(A, 0u);
+  __asm__ volatile("" ::: "memory"); // the weight loads ahead of the activation loads
+  const __amdgpu_buffer_rsrc_t rq = rsrc(xq, 40u * nb);
+  for (u32 j = tid; j < nblk; j += NT) { // the Q8 vector, written by other workgroups: coherent loads
+    const u32 p = (j & 7u) * ng + (j >> 3);
+    u32x4 lo = (u32x4)(0u), hi = (u32x4)(0u);
+    float d = 0.0f;
+    if (j < nb) {
+      lo = __builtin_amdgcn_raw_buffer_load_b128(rq, 32u * j, 0, CPOL_SC1);
+      hi = __builtin_amdgcn_raw_buffer_load_b128(rq, 32u * j + 16u, 0, CPOL_SC1);
+      d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, 32u * nb + 4u * j, 0, CPOL_SC1));
+    }
+    s_lo[p] = lo, s_hi[p] = hi, s_d[p] = d;
+    if constexpr (KIND == AMDC_Q6_K) // 32 x the sum of each half of the block, as gemv2_body stages it
+      ((u32x2 *)s_as)[p] = (u32x2){32u * (u32)hsum16(lo), 32u * (u32)hsum16(hi)};
+  }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t ry = rsrc(op.y, 4u * rows), rb = rsrc(op.bias, 4u * rows), rr = rsrc(op.res, 4u * rows);
+  float acc = 0.0f;
+  auto comp = [&](const typename ItemOf<KIND>::type &it, u32 f) {
+    const u32 j = f / ni, i = f - j * ni, g = l + L * i;
+    const float a2 = item_dot<KIND>(it, g < ng ? g : 0u, ng, s_lo, s_hi, s_d, s_as, acc);
+    acc = g < ng ? a2 : acc;
+    if (i == ni - 1u) {
+      const float v = seg_sum(acc, L);
+      const u32 r = (blockIdx.x + j * gridDim.x) * rpg + wv * rpw + q;
+      if (l == 0u && r < rows) {
+        float o = v;
+        if (op.bias) o = o + __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, 4u * r, 0, CPOL_SC1));
+        if (op.res) o = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, 4u * r, 0, CPOL_SC1)) + o;
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(u32, o), ry, 4u * r, 0, CPOL_SC1);
+      }
+      acc = 0.0f;
+    }
+  };
+  for (u32 f = 0; f < nit; f++) { // one item at a time (the chain kernel's registers hold no second Q8_0 item)
+    comp(A, f);
+    if (f + 1u < nit) ld(A, f + 1u);
+  }
+  __syncthreads(); // the LDS vector is free for the next operation
+}
+
 __device__ __forceinline__ void chain_quant(const ChainOp &op) {
   const u32 nb = op.nb, tid = threadIdx.x, e = tid & 7u;
   const __amdgpu_buffer_rsrc_t rx = rsrc(op.a, 128u * nb), rq = rsrc(op.b, 40u * nb);
@@ -967,7 +1039,7 @@ __device__ __forceinline__ void chain_quant(const ChainOp &op) {
 __device__ __forceinline__ bool chain_preload(const ChainOp &op, Item &cur) {
   const u32 L = op.L, ng = amdc_ngroups(op.nb), lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
   const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw, nrg = (op.rows + rpg - 1u) / rpg;
-  if (blockIdx.x >= nrg) return false;
+  if (blockIdx.x >= nrg || op.type > 4u) return false; // Q8_0 / Q6_K operations load their own first items
   const u32 r = blockIdx.x * rpg + wv * rpw + q;
   const uint8_t *wr = (const uint8_t *)op.a + (u64)(r < op.rows ? r : op.rows - 1u) * amdc_row_bytes(op.nb);
   if (op.type == 1u || op.type == 3u) load_item<AMDC_Q4_0>(cur, wr, ng, l, l < ng);
@@ -985,7 +1057,9 @@ extern "C" __global__ __launch_bounds__(256, 2) void amdc_chain(const ChainOp *_
     else if (op.type == 1u) chain_gemv<AMDC_Q4_0, false>(op, it, pre == k, smem);
     else if (op.type == 2u) chain_gemv<AMDC_Q4_K, false>(op, it, pre == k, smem);
     else if (op.type == 3u) chain_gemv<AMDC_Q4_0, true>(op, it, pre == k, smem);
-    else chain_gemv<AMDC_Q4_K, true>(op, it, pre == k, smem);
+    else if (op.type == 4u) chain_gemv<AMDC_Q4_K, true>(op, it, pre == k, smem);
+    else if (op.type == 5u) chain_gemv_k8<AMDC_Q8_0>(op, smem);
+    else chain_gemv_k8<AMDC_Q6_K>(op, smem);
     if (op.sync && k + 1u < n) {
       // the next GEMV's first weights go out before the wait (quantizations between do not touch it[])
       u32 j = k + 1u;

@@ -252,9 +252,11 @@ int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kern
  * separate launches bit for bit (amdc_quant_q8; amdc_gemv_q4 / _q4k with
  * the same lane split).
  *   AMDC_CHAIN_QUANT: x (32 nb floats) -> q (Q8 buffer, 40 nb bytes)
- *   AMDC_CHAIN_GEMV:  kind, w (rows x nb), xq (Q8) -> y (rows floats),
- *                     optional bias / res (rows floats) as amdc_gemv_q4
- *   AMDC_CHAIN_GEMV_X: the same on x (32 nb floats): every workgroup
+ *   AMDC_CHAIN_GEMV:  kind (any), w (rows x nb), xq (Q8) -> y (rows
+ *                     floats), optional bias / res (rows floats) as
+ *                     amdc_gemv_q4; Q8_0 / Q6_K as amdc_gemv_q8 / _q6k
+ *                     (bit-equal to them)
+ *   AMDC_CHAIN_GEMV_X: Q4_0 / Q4_K on x (32 nb floats): every workgroup
  *                     quantizes x into its LDS (as amdc_gemv_q4_x, no Q8
  *                     buffer, no barrier between quantization and GEMV)
  * An operation that reads what an earlier one writes must come after a sync

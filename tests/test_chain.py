@@ -143,3 +143,62 @@ def test_chain_fused_quant_equals_separate_launches(dev, orc):
         for i, (gt, wt) in enumerate(zip(got, want)):
             assert np.array_equal(gt, wt), (rep, i)
     assert rel_err(y5.download(np.float32), E.y_oracle(0), E.mag(0)) < TOL
+
+
+def test_chain_q8_0_q6_k_equals_separate_launches(dev, orc):
+    """Q8_0 and Q6_K GEMV operations in a chain (the matrices of a Q4_K_M file besides Q4_K): x0 -> Q8 ->
+    GEMV A (Q8_0, nb 13) -> y1 -> Q8 -> GEMV B (Q6_K, bias and residual) -> y2 -> Q8 -> GEMV C (Q4_K) and D
+    (Q8_0) on one input. Each output equals amdc_quant_q8 + amdc_gemv of the kind, bit for bit, across
+    repeated launches; A and B match the oracle."""
+    g = np.random.default_rng(9)
+    Q8, Q6 = synth.KIND_Q8_0, synth.KIND_Q6_K
+    A = Case(dev, orc, Q8, 256, 13, seed=21)
+    B = Case(dev, orc, Q6, 1024, 8, seed=22)
+    C_ = Case(dev, orc, 3, 300, 32, seed=23)
+    D = Case(dev, orc, Q8, 77, 32, seed=24)
+    x0 = dev.DevBuf.of(A.x[0])
+    q0, q1, q2 = dev.DevBuf(q8_stride(13)), dev.DevBuf(q8_stride(8)), dev.DevBuf(q8_stride(32))
+    y1, y2, y3, y4 = (dev.DevBuf(4 * r) for r in (256, 1024, 300, 77))
+    bias = dev.DevBuf.of(g.standard_normal(1024).astype(np.float32))
+    res = dev.DevBuf.of(g.standard_normal(1024).astype(np.float32))
+    ops = [dev.chain_quant(x0, q0, 13),
+           dev.chain_gemv(Q8, A.W, q0, y1, 256, 13),
+           dev.chain_quant(y1, q1, 8),
+           dev.chain_gemv(Q6, B.W, q1, y2, 1024, 8, bias=bias, res=res),
+           dev.chain_quant(y2, q2, 32),
+           dev.chain_gemv(3, C_.W, q2, y3, 300, 32, sync=False),
+           dev.chain_gemv(Q8, D.W, q2, y4, 77, 32)]
+    ch = dev.Chain(ops)
+    r0, r1, r2 = dev.DevBuf(q8_stride(13)), dev.DevBuf(q8_stride(8)), dev.DevBuf(q8_stride(32))
+    z1, z2, z3, z4 = (dev.DevBuf(4 * r) for r in (256, 1024, 300, 77))
+    dev.quant_q8(x0, r0, 13)
+    dev.gemv(Q8, A.W, r0, z1, 256, 13)
+    dev.quant_q8(z1, r1, 8)
+    dev.gemv(Q6, B.W, r1, z2, 1024, 8, bias=bias, res=res)
+    dev.quant_q8(z2, r2, 32)
+    dev.gemv(3, C_.W, r2, z3, 300, 32)
+    dev.gemv(Q8, D.W, r2, z4, 77, 32)
+    want = [b.download(np.uint32) for b in (z1, z2, z3, z4)]
+    for rep in range(3):
+        for b in (y1, y2, y3, y4):
+            b.fill(0)
+        ch.launch()
+        ch.check()
+        got = [b.download(np.uint32) for b in (y1, y2, y3, y4)]
+        for i, (gt, wt) in enumerate(zip(got, want)):
+            assert np.array_equal(gt, wt), (rep, i)
+    assert rel_err(y1.download(np.float32), A.y_oracle(0), A.mag(0)) < TOL
+    # B's input is the quantized y1 (not B's own activations): check it through the oracle on that input
+    xq1 = r1.download(np.uint8)[:40 * 8]
+    yb = orc.gemv(synth.GGML[Q6], B.qw, B.qs, 1024, 8, xq1)
+    mag = orc.gemv_f64(synth.GGML[Q6], B.src, 1024, 8, xq1)[1]
+    yb = orc.epilogue(yb, bias.download(np.float32), res.download(np.float32))
+    assert rel_err(y2.download(np.float32), yb, mag + np.abs(bias.download(np.float32)) + np.abs(res.download(np.float32))) < TOL
+
+
+def test_chain_rejects_f32_input_for_q8_0(dev, orc):
+    A = Case(dev, orc, synth.KIND_Q8_0, 64, 8, seed=5)
+    x0 = dev.DevBuf.of(A.x[0])
+    y = dev.DevBuf(4 * 64)
+    with pytest.raises(dev.AmdcError):
+        dev.Chain([dev.chain_gemv_x(synth.KIND_Q8_0, A.W, x0, y, 64, 8)])
