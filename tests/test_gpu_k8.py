@@ -124,7 +124,7 @@ def test_errors_do_not_launch(dev, orc):
     with pytest.raises(dev.AmdcError):
         dev.gemv_q8(c.W.ptr + 4, c.Q, c.Y, 8, 16)  # misaligned weights
     with pytest.raises(dev.AmdcError):
-        dev.Chain([dev.chain_gemv(Q6, c.W, c.Q, c.Y, 8, 16)])  # the chain runs the Q4 kinds only
+        dev.Chain([dev.chain_gemv_x(Q6, c.W, c.X, c.Y, 8, 16)])  # f32-input chain GEMVs take the Q4 kinds only
 
 
 @pytest.mark.parametrize("kind,rows,nb,T", [(Q8, 1, 1, 17), (Q8, 63, 13, 64), (Q8, 130, 128, 65), (Q8, 70, 344, 33), (Q8, 300, 40, 256),
