@@ -1,7 +1,7 @@
 """The GEMV chain (amdc_chain_*): a list of quantize and decode-GEMV operations in one persistent launch
 with grid barriers. Every result equals the separate launches (amdc_quant_q8, then amdc_gemv_q4 / _q4k with
-the same lane split) bit for bit, across repeated launches and graph replays, and the GEMVs match the oracle
-to the GEMV tolerance."""
+the same lane split, amdc_gemv_q8 / _q6k) bit for bit, across repeated launches and graph replays, and the
+GEMVs match the oracle to the GEMV tolerance."""
 import numpy as np
 import pytest
 
