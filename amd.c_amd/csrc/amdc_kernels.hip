@@ -1694,7 +1694,7 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *
   const u64 step = (u64)rows * T;
   float v[16];
 #pragma unroll
-  for (u32 k = 0; k < 16u; k++) v[k] = part[(k < nks ? k : 0u) * step + i];
+  for (u32 k = 0; k < 16u; k++) v[k] = k < nks ? part[k * step + i] : 0.0f; // nks is uniform: no divergence
   float o = v[0];
 #pragma unroll
   for (u32 k = 1; k < 16u; k++) o = k < nks ? o + v[k] : o;
