@@ -18,7 +18,11 @@
  * Every function returns 0 on success, else an AMDC_E* code; amdc_last_error()
  * then says why (the reference instead prints and exit(1)s: src/common.c:6-14;
  * a host that wants that calls ie_die(amdc_last_error())).
- * Not re-entrant: one thread drives the library (as src/hip.c). */
+ * Not re-entrant: one thread drives the library (as src/hip.c). The operators
+ * that use the library's device workspace (the GEMMs, the split-K multi-vector
+ * GEMV, amdc_gemv_*_x with q8 NULL above the fused size) share it: work of
+ * theirs queued on different streams, or in graphs replayed on them, must be
+ * ordered (one stream, or an event between), or their results race. */
 #ifndef AMDC_Q4_H
 #define AMDC_Q4_H
 
