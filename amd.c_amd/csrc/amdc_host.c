@@ -613,6 +613,7 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
   u32 ks = 1;
   while (ks < nt && ks < 16u && (u64)wgs * (ks + 1u) <= 4u * cus) ks++;
   if (t_ksplit > 0) ks = (u32)t_ksplit < nt ? (u32)t_ksplit : nt;
+  if (ks > 16u) ks = 16u; /* amdc_gemm_reduce adds at most 16 splits (AMDC_GEMM_KSPLIT is not range-checked) */
   float *part = NULL;
   if (ks > 1u) {
     int rc = ws_reserve((size_t)ks * T * rows * 4u);
@@ -892,6 +893,7 @@ static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *x
     while (ks < 16u && tiles * ks < 3u * cus && ng >= 4u * ks) ks <<= 1;
   }
   if (ks > ng) ks = ng;
+  if (ks > 16u) ks = 16u; /* amdc_gemm_reduce adds at most 16 splits */
   const u32 Tp = (T + 127u) / 128u * 128u, K = 32u * nb;
   const size_t xh_b = (size_t)Tp * K * 2u, sc_b = (size_t)nb * Tp * 4u, part_b = ks > 1u ? (size_t)ks * T * rows * 4u : 0u;
   rc = ws_reserve(xh_b + 2u * sc_b + part_b);

@@ -1685,6 +1685,17 @@ GEMMH_KERNEL(amdc_gemmh_q4_0_m64_n64, 2, AMDC_Q4_0)
 // The split-K sums: y[t][r] = part[0][t][r] + part[1][t][r] + ... (in split
 // order), then the epilogue. All nks (<= 16) loads are issued before the
 // first add (a split past nks reads split 0 again and is not added).
+// the partial sums of element i over N splits, in split order: N loads in flight, then the adds
+template <u32 N> __device__ __forceinline__ float split_sum(const float *__restrict__ part, u64 step, u64 i) {
+  float v[N];
+#pragma unroll
+  for (u32 k = 0; k < N; k++) v[k] = part[k * step + i];
+  float o = v[0];
+#pragma unroll
+  for (u32 k = 1; k < N; k++) o = o + v[k];
+  return o;
+}
+
 extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *__restrict__ part, u32 nks, float *__restrict__ y, u32 rows,
                                                                    u32 T, const float *__restrict__ bias, const float *__restrict__ res,
                                                                    u32 ys, u32 rs) {
@@ -1692,12 +1703,25 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *
   if (i >= (u64)rows * T) return;
   const u32 t = (u32)(i / rows), r = (u32)(i - (u64)t * rows);
   const u64 step = (u64)rows * T;
-  float v[16];
-#pragma unroll
-  for (u32 k = 0; k < 16u; k++) v[k] = k < nks ? part[k * step + i] : 0.0f; // nks is uniform: no divergence
-  float o = v[0];
-#pragma unroll
-  for (u32 k = 1; k < 16u; k++) o = k < nks ? o + v[k] : o;
+  float o; // nks (1..16) is uniform: one branch, then a constant number of loads
+  switch (nks) {
+  case 1: o = split_sum<1>(part, step, i); break;
+  case 2: o = split_sum<2>(part, step, i); break;
+  case 3: o = split_sum<3>(part, step, i); break;
+  case 4: o = split_sum<4>(part, step, i); break;
+  case 5: o = split_sum<5>(part, step, i); break;
+  case 6: o = split_sum<6>(part, step, i); break;
+  case 7: o = split_sum<7>(part, step, i); break;
+  case 8: o = split_sum<8>(part, step, i); break;
+  case 9: o = split_sum<9>(part, step, i); break;
+  case 10: o = split_sum<10>(part, step, i); break;
+  case 11: o = split_sum<11>(part, step, i); break;
+  case 12: o = split_sum<12>(part, step, i); break;
+  case 13: o = split_sum<13>(part, step, i); break;
+  case 14: o = split_sum<14>(part, step, i); break;
+  case 15: o = split_sum<15>(part, step, i); break;
+  default: o = split_sum<16>(part, step, i); break;
+  }
   if (bias) o = o + bias[r];
   if (res) o = res[(u64)t * rs + r] + o;
   y[(u64)t * ys + r] = o;
