@@ -233,14 +233,6 @@ static struct {
 /* The kernels of amdc_kernels.hip. */
 enum {
   K_QUANT,
-  K_GEMV_Q4_T1,
-  K_GEMV_Q4K_T1,
-  K_GEMV_Q4_T1U1,
-  K_GEMV_Q4K_T1U1,
-  K_GEMV_Q4_T8,
-  K_GEMV_Q4K_T8,
-  K_GEMV_Q4_T16,
-  K_GEMV_Q4K_T16,
   K_DOTS_Q4,
   K_DOTS_Q4K,
   K_GEMM_N128,
@@ -280,19 +272,17 @@ enum {
   K_GEMV_Q6K_V16,
   K_N
 };
-static const char *const kname[K_N] = {"amdc_quant_q8",       "amdc_gemv_q4_0_t1",  "amdc_gemv_q4_k_t1",  "amdc_gemv_q4_0_t1u1",
-                                       "amdc_gemv_q4_k_t1u1", "amdc_gemv_q4_0_t8",  "amdc_gemv_q4_k_t8",  "amdc_gemv_q4_0_t16",
-                                       "amdc_gemv_q4_k_t16",  "amdc_dots_q4_0",     "amdc_dots_q4_k",     "amdc_gemm_q4_k_n128",
-                                       "amdc_gemm_q4_k_n64",  "amdc_gemv_q4_0_p1",  "amdc_gemv_q4_k_p1",  "amdc_probe_read",
-                                       "amdc_probe_copy",     "amdc_q8_prep",       "amdc_gemmh_m64_n128", "amdc_gemmh_m64_n64",
-                                       "amdc_gemm_reduce",    "amdc_gemv_q4_0_v8",  "amdc_gemv_q4_k_v8",
-                                       "amdc_gemv_q4_0_x1",   "amdc_gemv_q4_k_x1",  "amdc_gemv_q4_0_p2",  "amdc_gemv_q4_k_p2",
-                                       "amdc_chain",          "amdc_rmsnorm_q8",    "amdc_swiglu_q8",     "amdc_gemv_q8_0_p2",
-                                       "amdc_gemv_q6_k_p2",   "amdc_dots_q8_0",     "amdc_dots_q6_k",     "amdc_gemmh_q8_0_m64_n128",
-                                       "amdc_gemmh_q8_0_m64_n64", "amdc_gemmh_q6_k_m64_n128", "amdc_gemmh_q6_k_m64_n64",
-                                       "amdc_gemv_q8_0_v8",   "amdc_gemv_q6_k_v8",  "amdc_gemmh_q4_0_m64_n128", "amdc_gemmh_q4_0_m64_n64",
-                                       "amdc_gemv_q4_0_v16",  "amdc_gemv_q4_k_v16", "amdc_gemv_q8_0_v16",
-                                       "amdc_gemv_q6_k_v16"};
+static const char *const kname[K_N] = {
+    "amdc_quant_q8",           "amdc_dots_q4_0",          "amdc_dots_q4_k",          "amdc_gemm_q4_k_n128",
+    "amdc_gemm_q4_k_n64",      "amdc_gemv_q4_0_p1",       "amdc_gemv_q4_k_p1",       "amdc_probe_read",
+    "amdc_probe_copy",         "amdc_q8_prep",            "amdc_gemmh_m64_n128",     "amdc_gemmh_m64_n64",
+    "amdc_gemm_reduce",        "amdc_gemv_q4_0_v8",       "amdc_gemv_q4_k_v8",       "amdc_gemv_q4_0_x1",
+    "amdc_gemv_q4_k_x1",       "amdc_gemv_q4_0_p2",       "amdc_gemv_q4_k_p2",       "amdc_chain",
+    "amdc_rmsnorm_q8",         "amdc_swiglu_q8",          "amdc_gemv_q8_0_p2",       "amdc_gemv_q6_k_p2",
+    "amdc_dots_q8_0",          "amdc_dots_q6_k",          "amdc_gemmh_q8_0_m64_n128", "amdc_gemmh_q8_0_m64_n64",
+    "amdc_gemmh_q6_k_m64_n128", "amdc_gemmh_q6_k_m64_n64", "amdc_gemv_q8_0_v8",       "amdc_gemv_q6_k_v8",
+    "amdc_gemmh_q4_0_m64_n128", "amdc_gemmh_q4_0_m64_n64", "amdc_gemv_q4_0_v16",      "amdc_gemv_q4_k_v16",
+    "amdc_gemv_q8_0_v16",      "amdc_gemv_q6_k_v16"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -580,47 +570,74 @@ int amdc_swiglu_q8(float *a, const float *b, uint32_t n, uint8_t *q, uint32_t T,
 static int check_mat(const char *op, int kind, const void *w, const uint8_t *xq, const float *y, uint32_t rows, uint32_t nb) {
   if (!kind_ok(kind)) return fail(AMDC_EINVAL, "%s: kind %d", op, kind);
   if (!w || !xq || !y) return fail(AMDC_EINVAL, "%s: null pointer", op);
-  if (!rows || !nb || rows >= (1u << 24) || nb >= (1u << 16)) return fail(AMDC_EINVAL, "%s: size %u rows x %u blocks", op, rows, nb);
+  if (!rows || !nb || rows >= (1u << 24) || nb > 2048u)
+    return fail(AMDC_EINVAL, "%s: size %u rows x %u blocks (at most 2^24 - 1 rows and 2048 blocks)", op, rows, nb);
   if ((kind == AMDC_KIND_Q4_K || kind == AMDC_KIND_Q6_K) && nb % 8u)
     return fail(AMDC_EINVAL, "%s: %s needs nb %% 8 == 0 (nb %u)", op, kind == AMDC_KIND_Q4_K ? "Q4_K" : "Q6_K", nb);
   if (!aligned16(w) || !aligned16(xq)) return fail(AMDC_EINVAL, "%s: w and xq must be 16-byte aligned", op);
   return AMDC_OK;
 }
 
+/* A lane of the decode kernels holds at most 4 super-groups of its row (its
+ * items enter the kernels' ItemTree): L raised until ceil(ng / L) <= 4 (ng <=
+ * 256, checked by check_mat). */
+static u32 lanes_fit(u32 L, u32 ng) {
+  while (L < 64u && (ng + L - 1u) / L > 4u) L <<= 1;
+  return L;
+}
+
 /* Lanes per row: the smallest power of two >= the super-groups of a row
  * (one super-group per lane), 4..64. */
 static u32 gemv_lanes(u32 ng) {
-  if (t_lanes > 0) return (u32)t_lanes;
+  if (t_lanes > 0) return lanes_fit((u32)t_lanes, ng);
   u32 L = 4;
   while (L < ng && L < 64u) L <<= 1;
   return L;
 }
 
+/* Lanes per row of the second decode form: up to 3 super-groups each; for the
+ * Q8_0 / Q6_K kinds (k8) then, while the grid has under 2 row groups per CU,
+ * more lanes per row and fewer rows per workgroup (measured on MI355X: 1024 x
+ * 5120 Q6_K 5.2 us at 32 lanes against 8.6 at 8; 11008 x 4096 Q8_0 11.4 at 16
+ * against 12.5 at 8). */
+static u32 gemv2_lanes(u32 ng, u32 rows, int k8) {
+  const u32 cus = g_cus > 0 ? (u32)g_cus : 256u;
+  u32 L = 4u;
+  while (L < 64u && 3u * L < ng) L <<= 1;
+  while (k8 && L < 64u && L < ng && (rows + 4u * (64u / L) - 1u) / (4u * (64u / L)) < 2u * cus) L <<= 1;
+  return t_lanes > 0 ? lanes_fit((u32)t_lanes, ng) : L;
+}
+
 /* LDS of the GEMV: 320 bytes per super-group and vector (amdc_kernels.hip). */
 #define GEMV_LDS_T1 (150u * 1024u)
-#define GEMV_LDS_TN (64u * 1024u)
 
 static int ws_reserve(size_t n);
 
 /* The verify GEMV on int8 MFMA (T <= 16): 64 rows per workgroup, K split
- * over tiles of 64 blocks until the workgroups fill the CUs twice. */
+ * over aligned ranges of tiles (64 blocks each) until the workgroups fill the
+ * CUs four times. A range holds S tiles, S a power of two <= 4, so that its
+ * sum is a subtree of the super-group tree (the kernels' order, equal to the
+ * decode GEMV's) and amdc_gemm_reduce's tree over the ranges completes it. */
 static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                         const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
   const u32 nt = (amdc_ngroups(nb) + 7u) / 8u, wgs = (rows + 63u) / 64u, cus = g_cus > 0 ? (u32)g_cus : 256u;
   /* split K up to one tile of 8 super-groups per workgroup while the grid is under 4 workgroups
      per CU: each workgroup's tile is a chain of dependent loads, so more of them in flight win
      (MI355X, T = 8: 5120 x 17408 Q4_K 23.6 us at 9 splits against 29.7 at 4) */
-  u32 ks = 1;
-  while (ks < nt && ks < 16u && (u64)wgs * (ks + 1u) <= 4u * cus) ks++;
-  if (t_ksplit > 0) ks = (u32)t_ksplit < nt ? (u32)t_ksplit : nt;
-  if (ks > 16u) ks = 16u; /* amdc_gemm_reduce adds at most 16 splits (AMDC_GEMM_KSPLIT is not range-checked) */
+  u32 want = 1;
+  while (want < nt && (u64)wgs * (want + 1u) <= 4u * cus) want++;
+  if (t_ksplit > 0) want = (u32)t_ksplit < nt ? (u32)t_ksplit : nt;
+  if (want > 16u) want = 16u; /* amdc_gemm_reduce adds at most 16 ranges */
+  u32 tps = 1;
+  while (tps < 4u && tps * want < nt) tps <<= 1; /* the smallest S with ceil(nt / S) <= want (nt <= 32: S <= 2 for 16) */
+  const u32 ks = (nt + tps - 1u) / tps;
   float *part = NULL;
   if (ks > 1u) {
     int rc = ws_reserve((size_t)ks * T * rows * 4u);
     if (rc) return rc;
     part = g_ws;
   }
-  void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs, &part};
+  void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs, &part, &tps};
   const int v16 = T > 8u; /* the 16-vector form */
   const int k = kind == AMDC_KIND_Q6_K ? (v16 ? K_GEMV_Q6K_V16 : K_GEMV_Q6K_V8)
                 : kind == AMDC_KIND_Q4_K ? (v16 ? K_GEMV_Q4K_V16 : K_GEMV_Q4K_V8)
@@ -629,7 +646,7 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
   HIPCALL(H.ModuleLaunchKernel(g_k[k], wgs, ks, 1, 256, 1, 1, 0, stream, args, NULL));
   if (ks > 1u) {
     const u64 n = (u64)rows * T;
-    void *ra[] = {&part, &ks, &y, &rows, &T, &bias, &res, &ys, &rs};
+    void *ra[] = {&part, (void *)&ks, &y, &rows, &T, &bias, &res, &ys, &rs};
     return launch(K_GEMM_REDUCE, (unsigned)((n + 255u) / 256u), 1, 0, stream, ra);
   }
   return AMDC_OK;
@@ -646,14 +663,7 @@ static int gemv_k8_launch(int kind, const void *w, const uint8_t *xq, float *y, 
   const u64 rb = amdc_row_bytes_k(kind, nb);
   if ((u64)rows * rb + rb >= (1ull << 32))
     return fail(AMDC_EINVAL, "gemv: %u rows of %llu bytes: the matrix must be under 4 GiB (split the rows)", rows, (unsigned long long)rb);
-  /* lanes per row: up to 3 super-groups each; then, while the grid has under 2 row groups per CU,
-     more lanes per row and fewer rows per workgroup (measured on MI355X: 1024 x 5120 Q6_K 5.2 us
-     at 32 lanes against 8.6 at 8; 11008 x 4096 Q8_0 11.4 at 16 against 12.5 at 8) */
-  const u32 cus = g_cus > 0 ? (u32)g_cus : 256u;
-  u32 L = 4u;
-  while (L < 64u && 3u * L < ng) L <<= 1;
-  while (L < 64u && L < ng && (rows + 4u * (64u / L) - 1u) / (4u * (64u / L)) < 2u * cus) L <<= 1;
-  if (t_lanes > 0) L = (u32)t_lanes;
+  const u32 cus = g_cus > 0 ? (u32)g_cus : 256u, L = gemv2_lanes(ng, rows, 1);
   const u32 rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg, cap = 2u * cus;
   const unsigned g = t_wgs > 0 && (u32)t_wgs < nrg ? (unsigned)t_wgs : nrg < cap ? nrg : cap;
   const u32 lds = bpb * 8u * ng + 4u * rpg * ((nrg + g - 1u) / g);
@@ -671,9 +681,16 @@ static int gemv_k8_launch(int kind, const void *w, const uint8_t *xq, float *y, 
 
 static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                        const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
-  if ((kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) && (T == 1u || t_unroll > 0))
-    return gemv_k8_launch(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
-  if (T > 1u && t_unroll <= 0) {
+  if (kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) {
+    if (T == 1u || t_unroll > 0) return gemv_k8_launch(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+  } else if (T > 1u && t_unroll > 0) { /* tuning: one decode launch per vector */
+    for (u32 t = 0; t < T; t++) {
+      int rc = gemv_launch(kind, w, xq + (u64)t * xs, y + (u64)t * ys, rows, nb, bias, res ? res + (u64)t * rs : NULL, 1u, 0u, 0u, 0u, stream);
+      if (rc) return rc;
+    }
+    return AMDC_OK;
+  }
+  if (T > 1u) {
     /* the int8-MFMA verify kernels, up to 16 vectors per launch; measured on MI355X, T = 16:
        17408 x 5120 Q4_K 30.8 us in one launch, 41 us as two 8-vector launches, 176 us on the dot4
        multi-vector kernel */
@@ -686,39 +703,24 @@ static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uin
     return AMDC_OK;
   }
   const u32 ng = amdc_ngroups(nb), L = gemv_lanes(ng), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
-  const u32 TT = T == 1u ? 1u : T <= 8u ? 8u : 16u;
-  u32 GC = (TT == 1u ? GEMV_LDS_T1 : GEMV_LDS_TN) / (320u * TT);
-  if (GC > ng) GC = ng;
-  const u32 lds = 320u * TT * GC;
-  const unsigned grid = t_wgs > 0 && (u32)t_wgs < nrg ? (unsigned)t_wgs : nrg;
   const int form = t_form > 0 ? t_form : ng > 32u ? 2 : 1;
-  if (TT == 1u && t_unroll <= 0 && form == 2 && (u64)rows * 144u * ng + 144u * ng < (1ull << 32)) {
-    /* the decode kernel with buffer loads, for long rows: up to 3 super-groups per lane (it keeps
-       the next one in flight), at most 2 workgroups per CU; LDS for the vector and the
-       workgroup's results. Measured on MI355X: 4096 x 11008 Q4_0 8.6 us (9.5 with the
+  if (form == 2 && (u64)rows * 144u * ng + 144u * ng < (1ull << 32)) {
+    /* the decode kernel with buffer loads (32-bit offsets: matrices under 4 GiB), for long rows: up
+       to 3 super-groups per lane (it keeps the next one in flight), at most 2 workgroups per CU; LDS
+       for the vector and the workgroup's results. Measured on MI355X: 4096 x 11008 Q4_0 8.6 us (9.5 with the
        amdc_gemv_*_p1 split), 5120 x 17408 Q4_K 14.7 (15.8). */
-    u32 L2 = 4u;
-    while (L2 < 64u && 3u * L2 < ng) L2 <<= 1;
-    if (t_lanes > 0) L2 = (u32)t_lanes;
+    const u32 L2 = gemv2_lanes(ng, rows, 0);
     const u32 rpg2 = 4u * (64u / L2), nrg2 = (rows + rpg2 - 1u) / rpg2, cap = 2u * (g_cus > 0 ? (u32)g_cus : 256u);
     const unsigned g2 = t_wgs > 0 && (u32)t_wgs < nrg2 ? (unsigned)t_wgs : nrg2 < cap ? nrg2 : cap;
     const u32 lds2 = 320u * ng + 4u * rpg2 * ((nrg2 + g2 - 1u) / g2);
-    if (lds2 <= GEMV_LDS_T1) {
-      void *a2[] = {&w, &xq, &y, &rows, &nb, &bias, &res, (void *)&L2};
-      return launch(kind == AMDC_KIND_Q4_K ? K_GEMV_Q4K_P2 : K_GEMV_Q4_P2, g2, 1, lds2, stream, a2);
-    }
+    if (lds2 > GEMV_LDS_T1) return fail(AMDC_EINVAL, "gemv: %u rows x %u blocks: %u bytes of LDS (more workgroups)", rows, nb, lds2);
+    void *a2[] = {&w, &xq, &y, &rows, &nb, &bias, &res, (void *)&L2};
+    return launch(kind == AMDC_KIND_Q4_K ? K_GEMV_Q4K_P2 : K_GEMV_Q4_P2, g2, 1, lds2, stream, a2);
   }
-  if (TT == 1u && t_unroll <= 0 && 320u * ng <= GEMV_LDS_T1) { /* the pipelined decode kernel */
-    const unsigned g1 = t_wgs > 0 && (u32)t_wgs < nrg ? (unsigned)t_wgs : nrg;
-    void *a1[] = {&w, &xq, &y, &rows, &nb, &bias, &res, (void *)&L};
-    return launch(kind == AMDC_KIND_Q4_K ? K_GEMV_Q4K_P1 : K_GEMV_Q4_P1, g1, 1, 320u * ng, stream, a1);
-  }
-  int k;
-  const int k4 = kind == AMDC_KIND_Q4_K;
-  if (TT == 1u) k = t_unroll == 1 ? (k4 ? K_GEMV_Q4K_T1U1 : K_GEMV_Q4_T1U1) : (k4 ? K_GEMV_Q4K_T1 : K_GEMV_Q4_T1);
-  else k = TT == 8u ? (k4 ? K_GEMV_Q4K_T8 : K_GEMV_Q4_T8) : (k4 ? K_GEMV_Q4K_T16 : K_GEMV_Q4_T16);
-  void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs, (void *)&L, &GC};
-  return launch(k, grid, 1, lds, stream, args);
+  /* the pipelined decode kernel (320 ng bytes of LDS: ng <= 256 fits) */
+  const unsigned g1 = t_wgs > 0 && (u32)t_wgs < nrg ? (unsigned)t_wgs : nrg;
+  void *a1[] = {&w, &xq, &y, &rows, &nb, &bias, &res, (void *)&L};
+  return launch(kind == AMDC_KIND_Q4_K ? K_GEMV_Q4K_P1 : K_GEMV_Q4_P1, g1, 1, 320u * ng, stream, a1);
 }
 
 int amdc_gemv_q4(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
@@ -1037,13 +1039,8 @@ int amdc_chain_create(const amdc_chain_op *ops, uint32_t n, void **chain) {
         rc = fail(AMDC_EINVAL, "chain op %u: the matrix must be under 4 GiB", k);
       if (!rc && need > GEMV_LDS_T1) rc = fail(AMDC_EINVAL, "chain op %u: nb %u too large", k, o->nb);
       if (k8) {
-        /* the lanes per row of the decode launch (gemv_k8_launch): bit-equal results */
-        const u32 cus = g_cus > 0 ? (u32)g_cus : 256u;
-        u32 L = 4u;
-        while (L < 64u && 3u * L < ng) L <<= 1;
-        while (L < 64u && L < ng && (o->rows + 4u * (64u / L) - 1u) / (4u * (64u / L)) < 2u * cus) L <<= 1;
-        if (t_lanes > 0) L = (u32)t_lanes;
-        e->type = o->kind == AMDC_KIND_Q6_K ? 6u : 5u, e->L = L;
+        /* the lanes per row of the decode launch (gemv_k8_launch) */
+        e->type = o->kind == AMDC_KIND_Q6_K ? 6u : 5u, e->L = gemv2_lanes(ng, o->rows, 1);
       } else {
         e->type = (o->kind == AMDC_KIND_Q4_K ? 2u : 1u) + (fq ? 2u : 0u), e->L = gemv_lanes(ng);
       }

@@ -77,6 +77,28 @@ __device__ __forceinline__ float seg_sum(float v, u32 L) {
   return v;
 }
 
+// The summation order of a row (every GEMV form, decode and verify, follows
+// it, so that their results are equal bit for bit): the leaf of super-group g
+// is its 8 block terms added in block order from +0.0; the row sum is the
+// pairwise tree over the leaves g = 0, 1, ..., ng - 1 (adjacent pairs first),
+// padded with +0.0 leaves to a power of two. A leaf is never -0.0 (every
+// chain starts at +0.0), so x + 0.0 = x and the padding width does not
+// matter. seg_sum over L lanes holding leaves l (lane l) is that tree.
+//
+// A lane that holds the super-groups g = l + L i of its row (items i = 0 ..
+// ni - 1, L lanes per row) gives each item's leaf to seg_sum and then adds
+// the sums of the items in a pairwise tree over i: ItemTree, ni <= 4.
+struct ItemTree {
+  float a = 0.0f, b = 0.0f;
+  __device__ __forceinline__ void add(float v, u32 i) {
+    if (i == 0u) a = v;
+    else if (i == 1u) a = a + v;
+    else if (i == 2u) b = v;
+    else b = b + v;
+  }
+  __device__ __forceinline__ float sum(u32 ni) const { return ni > 2u ? a + b : a; }
+};
+
 __device__ __forceinline__ int sdot4(u32 a, u32 b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 
 // Sum over j < 32 of nibble_j * a_j: the 16 nibble bytes w (byte j: weight j
@@ -244,147 +266,29 @@ extern "C" __global__ __launch_bounds__(256) void amdc_swiglu_q8(float *__restri
 
 // ------------------------------------------------------------------ GEMV
 
-// y[t][r] = sum over blocks of W[r] . x_t for the T (<= TT) Q8 vectors x_t
-// (xq + t * xs bytes), then the reference's epilogue (src/cpu.c:513-520):
-// y (+ bias[r]) then (res[t * rs + r] +) y. y[t][r] at y + t * ys.
+// The decode GEMV: y[r] = sum over blocks of W[r] . x, then the reference's
+// epilogue (src/cpu.c:513-520): y (+ bias[r]) then (res[r] +) y.
 //
 // Work split: a wave holds 64 / L rows, L lanes per row (L = 4..64, a power
-// of two); lane l of a row owns the super-groups g = l, l + L, ... and for each
-// reads its 16-byte header and its 8 nibble blocks (9 loads of 128 bits). The
-// L lane sums of a row are added by seg_sum. A workgroup (4 waves) takes
-// 4 * 64 / L rows per pass and loops over row groups (blockIdx.x, + gridDim.x).
+// of two); lane l of a row owns the super-groups g = l + L i (its items) and
+// for each reads its 16-byte header and its 8 nibble blocks (9 loads of 128
+// bits). A workgroup (4 waves) takes 4 * 64 / L rows per pass and loops over
+// row groups (blockIdx.x, + gridDim.x). The row sum follows the super-group
+// tree order (ItemTree above).
 //
-// The activations of GC super-groups (8 GC blocks) of all T vectors sit in
-// LDS, permuted as the weights (block 8g + k at k GC + g - g0), so that the
-// lanes of a row read consecutive 16-byte words: q low half, q high half, d,
-// asum: 40 bytes x 8 GC x T. When GC >= ng they are staged once per
-// workgroup; else once per chunk of GC super-groups and row group.
+// The Q8 vector sits in LDS, permuted as the weights (block 8g + k at
+// k ng + g), so that the lanes of a row read consecutive 16-byte words: q low
+// half, q high half, d, asum (320 ng bytes).
 //
 // Per block: Q4_0: dot = sum (q - 8) a = nib_dot - 8 asum (u32 wrap as the
 //   reference), acc += (d_w d_a) dot;
 // Q4_K: dq = nib_dot; acc = fma(-(dmin mn), d_a asum, fma((d sc) dq, d_a,
 //   acc)), the operations of src/cpu.c:111-112.
-template <int KIND, int TT, int U>
-__device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
-                                          u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 xs, u32 ys,
-                                          u32 rs, u32 L, u32 GC) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const u32 ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
-  const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw;
-  const u32 nrg = (rows + rpg - 1u) / rpg;
-  const u64 RB = amdc_row_bytes(nb);
-  const u32 nblk = 8u * GC; // LDS blocks per vector
-  u32x4 *s_lo = (u32x4 *)smem;
-  u32x4 *s_hi = s_lo + (u64)TT * nblk;
-  float *s_d = (float *)(s_hi + (u64)TT * nblk);
-  u32 *s_as = (u32 *)(s_d + (u64)TT * nblk);
-
-  // stage the blocks of super-groups [g0, g1) of the T vectors
-  auto stage = [&](u32 g0, u32 g1) {
-    const u32 n = 8u * (g1 - g0), tot = T * n;
-    for (u32 i = tid; i < tot; i += NT) {
-      const u32 t = i / n, bl = i - t * n, b = 8u * g0 + bl;
-      const u32 p = t * nblk + (bl & 7u) * GC + (bl >> 3);
-      const uint8_t *xt = xq + (u64)t * xs;
-      u32x4 lo = (u32x4)(0u), hi = (u32x4)(0u);
-      float d = 0.0f;
-      u32 as = 0;
-      if (b < nb) {
-        lo = *(const u32x4 *)(xt + 32u * b);
-        hi = *(const u32x4 *)(xt + 32u * b + 16u);
-        d = ((const float *)(xt + 32u * nb))[b];
-        as = ((const u32 *)(xt + 36u * nb))[b];
-      }
-      s_lo[p] = lo;
-      s_hi[p] = hi;
-      s_d[p] = d;
-      s_as[p] = as;
-    }
-  };
-
-  const bool one = GC >= ng;
-  if (one) {
-    stage(0, ng);
-    __syncthreads();
-  }
-  for (u32 rg = blockIdx.x; rg < nrg; rg += gridDim.x) {
-    const u32 r = rg * rpg + wv * rpw + q;
-    const uint8_t *wr = W + (u64)(r < rows ? r : rows - 1u) * RB;
-    float acc[TT];
-#pragma unroll
-    for (int t = 0; t < TT; t++) acc[t] = 0.0f;
-    for (u32 g0 = 0; g0 < ng; g0 += GC) {
-      const u32 g1 = g0 + GC < ng ? g0 + GC : ng;
-      if (!one) {
-        __syncthreads();
-        stage(g0, g1);
-        __syncthreads();
-      }
-      for (u32 g = g0 + l; g < g1; g += U * L) {
-        u32x4 hd[U], nbk[U][8];
-        bool ok[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) { // all loads of the step first
-          const u32 gu = g + (u32)u * L;
-          ok[u] = gu < g1;
-          const u32 gc = ok[u] ? gu : g;
-          hd[u] = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_header_off(gc)));
-#pragma unroll
-          for (u32 k = 0; k < 8u; k++) nbk[u][k] = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_nib_off(ng, gc, k)));
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-          if (!ok[u]) continue;
-          const u32 gl = g + (u32)u * L - g0;
-          float dmn = 0.0f, dsc = 0.0f;
-          if (KIND == AMDC_Q4_K) dsc = h2f(hd[u].x), dmn = h2f(hd[u].x >> 16);
-#pragma unroll
-          for (u32 k = 0; k < 8u; k++) {
-            const u32 p = k * GC + gl;
-            float sw, mm = 0.0f;
-            if (KIND == AMDC_Q4_0) sw = h2f(hword(hd[u], k >> 1) >> (16u * (k & 1u)));
-            else sw = dsc * (float)q4k_sc(hd[u], k), mm = dmn * (float)q4k_mn(hd[u], k);
-#pragma unroll
-            for (int t = 0; t < TT; t++) {
-              if ((u32)t < T) {
-                const u32 pt = (u32)t * nblk + p;
-                const int dq = nib_dot(nbk[u][k], s_lo[pt], s_hi[pt]);
-                const float da = s_d[pt];
-                const u32 as = s_as[pt];
-                if (KIND == AMDC_Q4_0) {
-                  const int dot = (int)((u32)dq - 8u * as);
-                  acc[t] += (sw * da) * (float)dot;
-                } else {
-                  const float xa = da * (float)(int)as;
-                  acc[t] = __builtin_fmaf(-mm, xa, __builtin_fmaf(sw * (float)dq, da, acc[t]));
-                }
-              }
-            }
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < TT; t++) {
-      if ((u32)t < T) {
-        const float v = seg_sum(acc[t], L);
-        if (l == 0u && r < rows) {
-          float o = v;
-          if (bias) o = o + bias[r];
-          if (res) o = res[(u64)t * rs + r] + o;
-          y[(u64)t * ys + r] = o;
-        }
-      }
-    }
-  }
-}
-
-// The decode GEMV (one vector), software-pipelined: each lane walks its
+//
+// First form (amdc_gemv_*_p1, _x1), software-pipelined: each lane walks its
 // (row group, super-group) items in order and issues the 9 loads of the next
 // item before it computes the current one, across row groups too; the first
-// item's loads are issued before the activations are staged. The same lane
-// split, LDS layout and per-block arithmetic as gemv_body (the activations
-// must fit in LDS at once: 320 ng bytes).
+// item's loads are issued before the activations are staged.
 struct Item {
   u32x4 h, n[8];
 };
@@ -559,16 +463,17 @@ __device__ __forceinline__ void gemv1_body(const uint8_t *__restrict__ W, const 
     }
   }
   __syncthreads();
-  float acc = 0.0f;
+  ItemTree tr;
   for (;;) {
     u32 rg2 = rg, i2 = i + 1u;
     if (i2 == ni) i2 = 0, rg2 += gridDim.x;
     const bool more = rg2 < nrg;
     if (more) load_item<KIND>(nxt, rowp(rg2), ng, l + L * i2, l + L * i2 < ng);
     const u32 g = l + L * i;
-    if (g < ng) acc = item_dot<KIND>(cur, g, ng, s_lo, s_hi, s_d, s_as, acc);
+    const float leaf = item_dot<KIND>(cur, g < ng ? g : 0u, ng, s_lo, s_hi, s_d, s_as, 0.0f);
+    tr.add(seg_sum(g < ng ? leaf : 0.0f, L), i);
     if (i2 == 0u) { // the row group is done
-      const float v = seg_sum(acc, L);
+      const float v = tr.sum(ni);
       const u32 r = rg * rpg + wv * rpw + q;
       if (l == 0u && r < rows) {
         float o = v;
@@ -576,7 +481,6 @@ __device__ __forceinline__ void gemv1_body(const uint8_t *__restrict__ W, const 
         if (res) o = res[r] + o;
         y[r] = o;
       }
-      acc = 0.0f;
     }
     if (!more) break;
     cur = nxt, rg = rg2, i = i2;
@@ -717,17 +621,16 @@ __device__ __forceinline__ void gemv2_body(const uint8_t *__restrict__ W, const 
   // vector) and go out after the loop: a store inside the loop would make the
   // reuse of its registers wait for every load in flight
   float *s_y = (float *)(s_as + (KIND == AMDC_Q6_K ? 2u : 1u) * nblk);
-  float acc = 0.0f;
+  ItemTree tr;
   auto comp = [&](const Item2<KIND> &it, u32 j, u32 i) {
     const u32 g = l + L * i;
-    const float a2 = item_dot<KIND>(it.w, g < ng ? g : 0u, ng, s_lo, s_hi, s_d, s_as, acc);
-    acc = g < ng ? a2 : acc;
+    const float leaf = item_dot<KIND>(it.w, g < ng ? g : 0u, ng, s_lo, s_hi, s_d, s_as, 0.0f);
+    tr.add(seg_sum(g < ng ? leaf : 0.0f, L), i);
     if (i == ni - 1u) { // the row group is done
-      const float v = seg_sum(acc, L);
+      const float v = tr.sum(ni);
       float o = bias ? v + it.b : v;
       o = res ? it.r + o : o;
       if (l == 0u) s_y[j * rpg + rbase] = o;
-      acc = 0.0f;
     }
   };
   u32 cj = 0, ci = 0, lj = 0, li = 0; // compute / load positions
@@ -914,16 +817,17 @@ __device__ __forceinline__ void chain_gemv(const ChainOp &op, Item (&it)[CHI], b
   }
   __syncthreads();
   const __amdgpu_buffer_rsrc_t ry = rsrc(op.y, 4u * rows), rb = rsrc(op.bias, 4u * rows), rr = rsrc(op.res, 4u * rows);
-  float acc = 0.0f;
+  ItemTree tr;
   for (u32 f0 = 0; f0 < nit; f0 += CHI) {
     if (f0) load_batch(f0, 0u);
 #pragma unroll
     for (u32 u = 0; u < CHI; u++) {
       const u32 f = f0 + u, j = f / ni, i = f - j * ni, g = l + L * i;
       if (f >= nit) break;
-      if (g < ng) acc = item_dot<KIND>(it[u], g, ng, s_lo, s_hi, s_d, s_as, acc);
+      const float leaf = item_dot<KIND>(it[u], g < ng ? g : 0u, ng, s_lo, s_hi, s_d, s_as, 0.0f);
+      tr.add(seg_sum(g < ng ? leaf : 0.0f, L), i);
       if (i == ni - 1u) {
-        const float v = seg_sum(acc, L);
+        const float v = tr.sum(ni);
         const u32 r = (blockIdx.x + j * gridDim.x) * rpg + wv * rpw + q;
         if (l == 0u && r < rows) {
           float o = v;
@@ -931,7 +835,6 @@ __device__ __forceinline__ void chain_gemv(const ChainOp &op, Item (&it)[CHI], b
           if (op.res) o = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, 4u * r, 0, CPOL_SC1)) + o;
           __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(u32, o), ry, 4u * r, 0, CPOL_SC1);
         }
-        acc = 0.0f;
       }
     }
   }
@@ -982,13 +885,13 @@ __device__ __forceinline__ void chain_gemv_k8(const ChainOp &op, uint8_t *smem) 
   }
   __syncthreads();
   const __amdgpu_buffer_rsrc_t ry = rsrc(op.y, 4u * rows), rb = rsrc(op.bias, 4u * rows), rr = rsrc(op.res, 4u * rows);
-  float acc = 0.0f;
+  ItemTree tr;
   auto comp = [&](const typename ItemOf<KIND>::type &it, u32 f) {
     const u32 j = f / ni, i = f - j * ni, g = l + L * i;
-    const float a2 = item_dot<KIND>(it, g < ng ? g : 0u, ng, s_lo, s_hi, s_d, s_as, acc);
-    acc = g < ng ? a2 : acc;
+    const float leaf = item_dot<KIND>(it, g < ng ? g : 0u, ng, s_lo, s_hi, s_d, s_as, 0.0f);
+    tr.add(seg_sum(g < ng ? leaf : 0.0f, L), i);
     if (i == ni - 1u) {
-      const float v = seg_sum(acc, L);
+      const float v = tr.sum(ni);
       const u32 r = (blockIdx.x + j * gridDim.x) * rpg + wv * rpw + q;
       if (l == 0u && r < rows) {
         float o = v;
@@ -996,7 +899,6 @@ __device__ __forceinline__ void chain_gemv_k8(const ChainOp &op, uint8_t *smem) 
         if (op.res) o = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, 4u * r, 0, CPOL_SC1)) + o;
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(u32, o), ry, 4u * r, 0, CPOL_SC1);
       }
-      acc = 0.0f;
     }
   };
   for (u32 f = 0; f < nit; f++) { // one item at a time (the chain kernel's registers hold no second Q8_0 item)
@@ -1099,21 +1001,6 @@ extern "C" __global__ __launch_bounds__(256) void amdc_probe_copy(const u32x4 *_
   const u64 stride = (u64)gridDim.x * NT;
   for (u64 i = (u64)blockIdx.x * NT + threadIdx.x; i < n; i += stride) dst[i] = src[i];
 }
-
-#define GEMV_KERNEL(NAME, KIND, TT, U)                                                                                              \
-  extern "C" __global__ __launch_bounds__(256) void NAME(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,          \
-                                                         const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs, u32 L, \
-                                                         u32 GC) {                                                                  \
-    gemv_body<KIND, TT, U>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, L, GC);                                                    \
-  }
-GEMV_KERNEL(amdc_gemv_q4_0_t1, AMDC_Q4_0, 1, 2)
-GEMV_KERNEL(amdc_gemv_q4_k_t1, AMDC_Q4_K, 1, 2)
-GEMV_KERNEL(amdc_gemv_q4_0_t1u1, AMDC_Q4_0, 1, 1)
-GEMV_KERNEL(amdc_gemv_q4_k_t1u1, AMDC_Q4_K, 1, 1)
-GEMV_KERNEL(amdc_gemv_q4_0_t8, AMDC_Q4_0, 8, 1)
-GEMV_KERNEL(amdc_gemv_q4_k_t8, AMDC_Q4_K, 8, 1)
-GEMV_KERNEL(amdc_gemv_q4_0_t16, AMDC_Q4_0, 16, 1)
-GEMV_KERNEL(amdc_gemv_q4_k_t16, AMDC_Q4_K, 16, 1)
 
 // ------------------------------------------------------------------ block dots (parity)
 
@@ -1682,18 +1569,24 @@ GEMMH_KERNEL(amdc_gemmh_q6_k_m64_n64, 2, AMDC_Q6_K)
 GEMMH_KERNEL(amdc_gemmh_q4_0_m64_n128, 4, AMDC_Q4_0)
 GEMMH_KERNEL(amdc_gemmh_q4_0_m64_n64, 2, AMDC_Q4_0)
 
-// The split-K sums: y[t][r] = part[0][t][r] + part[1][t][r] + ... (in split
-// order), then the epilogue. All nks (<= 16) loads are issued before the
-// first add (a split past nks reads split 0 again and is not added).
-// the partial sums of element i over N splits, in split order: N loads in flight, then the adds
+// The split-K sums: y[t][r] = the pairwise tree (adjacent splits first, a
+// split past nks counting as +0.0) of part[0][t][r], part[1][t][r], ...,
+// then the epilogue. nks (1..16) is uniform: one branch on it, then nks loads
+// in flight, then the adds. The host clamps the split count to 16 (the
+// default case reads 16 splits). The verify kernels' K ranges are aligned
+// subtrees of their tile tree, so this tree completes it; for the GEMM any
+// fixed order would do.
 template <u32 N> __device__ __forceinline__ float split_sum(const float *__restrict__ part, u64 step, u64 i) {
   float v[N];
 #pragma unroll
   for (u32 k = 0; k < N; k++) v[k] = part[k * step + i];
-  float o = v[0];
 #pragma unroll
-  for (u32 k = 1; k < N; k++) o = o + v[k];
-  return o;
+  for (u32 m = N; m > 1u; m = (m + 1u) / 2u) {
+#pragma unroll
+    for (u32 k = 0; k < m / 2u; k++) v[k] = v[2u * k] + v[2u * k + 1u];
+    if (m & 1u) v[m / 2u] = v[m - 1u]; // an odd one out pairs with +0.0
+  }
+  return v[0];
 }
 
 extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *__restrict__ part, u32 nks, float *__restrict__ y, u32 rows,
@@ -1703,7 +1596,7 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *
   if (i >= (u64)rows * T) return;
   const u32 t = (u32)(i / rows), r = (u32)(i - (u64)t * rows);
   const u64 step = (u64)rows * T;
-  float o; // nks (1..16) is uniform: one branch, then a constant number of loads
+  float o;
   switch (nks) {
   case 1: o = split_sum<1>(part, step, i); break;
   case 2: o = split_sum<2>(part, step, i); break;
@@ -1738,19 +1631,26 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *
 //     nonzero half of each column; the lanes of the other half use 0)
 // so that C[r][t + 8 pp] is the exact integer dot of block (g + pp, k) with
 // vector t (Q4_K: sum q a; Q4_0: sum q a, then - 8 asum; Q8_0: the int8
-// weights of planes 2k, 2k + 1 as A, sum w a). Per element the reference's
-// block arithmetic (src/cpu.c:81, 111-112, 168):
-//   Q4_0: acc += (d_w d_a) (dq - 8 asum); Q8_0: acc += (d_w d_a) dq
-//   Q4_K: acc = fma(s dq, d_a, acc), s = d sc; the min term - sum (dmin mn)
-//         (d_a asum) of every block on v_mfma_f32_16x16x4_f32 (column pp = 0),
-//         its A operand formed from the header registers (K index 4 q + h:
-//         the lane's own super-groups h, h + 4, sub-block q % 8).
-// The columns pp = 0 and 1 of a token hold the sums of alternate blocks; a
-// DPP add joins them at the end.
+// weights of planes 2k, 2k + 1 as A, sum w a).
+//
+// The float steps are the decode GEMV's, in its order (the super-group tree
+// order above), so that y_t equals the decode GEMV of vector t bit for bit
+// (the reference's guarantee for its multi-token kernels,
+// kernels/ie_kernels.c:481-482): each lane keeps the leaf of each super-group
+// of its column (pair p: super-group 2 p + pp of the tile), and per block
+//   Q4_0: leaf += (d_w d_a) (dq - 8 asum); Q8_0: leaf += (d_w d_a) dq
+//   Q4_K: leaf = fma(-(dmin mn), d_a asum, fma((d sc) dq, d_a, leaf))
+// After the tile's 8 planes the leaves of a pair are joined across the two
+// columns (a DPP row_ror:8: super-groups 2p, 2p + 1), then the pairs
+// ((0 + 1) + (2 + 3)): the tile's subtree of 8 leaves. The tiles of a
+// workgroup's K range (an aligned range of S <= 4 tiles, S a power of two) go
+// into a pairwise tree kept as a stack (ItemTree's tree, over tiles); the
+// ranges' sums are added by amdc_gemm_reduce in the same tree.
+//
 // Workgroup: 4 waves, wave w: rows 16 w .. 16 w + 15 of a 64-row tile; K in
 // tiles of 8 super-groups (64 blocks): the tile's activations are staged in
 // LDS, B-ready (the zero halves written once), with d_a, d_a asum (or asum)
-// per (block, token); each wave builds its rows' scale table from the headers.
+// per (block, token); each wave builds its rows' scale tables from the headers.
 // The weights go from memory straight into LDS (buffer_load ... lds) in whole
 // 128-byte lines: plane k of a tile is 128 contiguous bytes of a row, and each
 // load instruction moves 8 rows x 128 bytes (register loads in the MFMA's lane
@@ -1763,7 +1663,8 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *
 // A reads (16 rows, one column pair) fall on distinct banks.
 // NH token halves of 8 (T <= 8 NH): the _v16 kernels take two, each A operand
 // then feeds two MFMAs.
-// Split K over gridDim.y (tiles [t0, t1) per split, partial sums to part).
+// Split K over gridDim.y: split ks takes tiles [ks S, ks S + S) (S = tps, at
+// most 4), partial sums to part.
 __device__ __forceinline__ u32 v8_swz(u32 i) { return (i & 7u) ^ ((i >> 3) & 1u); }
 // A workgroup barrier for LDS written with ds_write only: the waves' LDS
 // writes are complete (lgkmcnt 0), the compiler keeps memory accesses on their
@@ -1779,8 +1680,9 @@ __device__ __forceinline__ void v8_barrier() {
 template <int KIND, int NS, int NH>
 __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
                                            u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 xs, u32 ys,
-                                           u32 rs, float *__restrict__ part) {
+                                           u32 rs, float *__restrict__ part, u32 tps) {
   constexpr u32 SC = KIND == AMDC_Q8_0 ? 2u : 1u; // 2 KB chunks (planes of 16 rows) per step
+  constexpr bool K4 = KIND == AMDC_Q4_K;
   typedef __attribute__((address_space(3))) void lds_t;
   __shared__ __attribute__((aligned(16))) u32x4 sw0[4][SC * 128u];
   __shared__ __attribute__((aligned(16))) u32x4 sw1[4][SC * 128u];
@@ -1790,7 +1692,9 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
   __shared__ __attribute__((aligned(16))) u32x4 sB[NH][32][2][16]; // [token half][pair p + 4 k][quarter & 1][column]: a column's nonzero half of K
   __shared__ __attribute__((aligned(16))) float sda[64][NTK];      // d_a [block of tile][token]
   __shared__ __attribute__((aligned(16))) float sxa[64][NTK];      // Q4_K: d_a asum; Q4_0: asum (as int bits)
-  __shared__ __attribute__((aligned(16))) float ssc[4][64][16]; // per wave: s (Q4_K d sc, Q4_0 / Q8_0 d) [block][row]
+  // per wave and plane (double-buffered): s (Q4_K d sc, Q4_0 / Q8_0 d) and Q4_K -(dmin mn) [super-group of tile][row]
+  __shared__ __attribute__((aligned(16))) float ssc[4][2][8][16];
+  __shared__ __attribute__((aligned(16))) float smn[K4 ? 4 : 1][2][8][16];
   const u32 ng = amdc_ngroups(nb), nt = (ng + 7u) >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
   const u32 i16 = lane & 15u, h = lane >> 4, n = i16, tk = n & 7u, pp = n >> 3;
   const u32 RB = (u32)amdc_row_bytes_k(KIND, nb);
@@ -1804,7 +1708,7 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
   const u32 xn = (u32)min((u64)T * xs, (u64)0xFFFFFFF0u);
   const __amdgpu_buffer_rsrc_t rxq = rsrc(xq, xn); // the T Q8 rows
   constexpr u32 OOB = 0xFFFFFFF0u;                 // an offset past every resource: the load returns zeros
-  const u32 ks = blockIdx.y, nks = gridDim.y, t0 = nt * ks / nks, t1 = nt * (ks + 1u) / nks;
+  const u32 ks = blockIdx.y, t0 = ks * tps, t1 = t0 + tps < nt ? t0 + tps : nt;
   auto gtile = [&](u32 t) { return ng - 8u * t < 8u ? ng - 8u * t : 8u; };
   auto slot = [&](u32 s) -> u32x4 * {
     if (s == 0u) return sw0[w];
@@ -1828,7 +1732,7 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
   u32x4 ra4[4 * NH];
   float rd[2 * NH];
   u32 rx[2 * NH];
-  u32x4 rh[2];
+  u32x4 rh[2]; // the next tile's headers of row i16, super-groups h, h + 4
   auto fetch_tile = [&](u32 t) {
     const u32 gt = gtile(t);
 #pragma unroll
@@ -1850,7 +1754,22 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
       rh[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, gl < gt ? wo + 16u * (8u * t + gl) : OOB, 0, 0);
     }
   };
-  float am[16]; // Q4_K: -(dmin mn) of row i16 for K index 4 q + h of the min-term MFMAs: super-group h + 4 (q / 8), sub-block q % 8
+  u32x4 hc[2];   // the current tile's headers (rh is refilled with the next tile's during this one)
+  float dd[2][2]; // Q4_K: d, dmin of hc[q]
+  // the scale table of plane k into buffer k & 1: this lane's entries (super-groups h, h + 4 of row i16);
+  // the same products as the decode GEMV's (exact: an f16 times a 6-bit integer)
+  auto scales = [&](u32 k) {
+#pragma unroll
+    for (u32 q = 0; q < 2u; q++) {
+      const u32 gl = h + 4u * q;
+      if (K4) {
+        ssc[w][k & 1u][gl][i16] = dd[q][0] * (float)q4k_sc(hc[q], k);
+        smn[K4 ? w : 0u][k & 1u][gl][i16] = -(dd[q][1] * (float)q4k_mn(hc[q], k));
+      } else {
+        ssc[w][k & 1u][gl][i16] = h2f(hword(hc[q], k >> 1) >> (16u * (k & 1u)));
+      }
+    }
+  };
   auto stage_tile = [&]() {
 #pragma unroll
     for (u32 c = 0; c < 4u * NH; c++) {
@@ -1861,63 +1780,67 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
     for (u32 c = 0; c < 2u * NH; c++) {
       const u32 i = tid + c * NT, tok = i & (NTK - 1u), bl = i / NTK;
       sda[bl][tok] = rd[c];
-      sxa[bl][tok] = KIND == AMDC_Q4_K ? rd[c] * (float)(int)rx[c] : __builtin_bit_cast(float, rx[c]);
+      sxa[bl][tok] = K4 ? rd[c] * (float)(int)rx[c] : __builtin_bit_cast(float, rx[c]);
     }
 #pragma unroll
-    for (u32 q = 0; q < 2u; q++) { // this wave's scale table: row i16, groups h, h + 4
-      const u32 gl = h + 4u * q;
-      const u32x4 hd = rh[q];
-#pragma unroll
-      for (u32 k = 0; k < 8u; k++) {
-        if (KIND == AMDC_Q4_0 || KIND == AMDC_Q8_0) {
-          ssc[w][8u * gl + k][i16] = h2f(hword(hd, k >> 1) >> (16u * (k & 1u)));
-        } else {
-          ssc[w][8u * gl + k][i16] = h2f(hd.x) * (float)q4k_sc(hd, k);
-          am[8u * q + k] = -(h2f(hd.x >> 16) * (float)q4k_mn(hd, k));
-        }
-      }
+    for (u32 q = 0; q < 2u; q++) {
+      hc[q] = rh[q];
+      if (K4) dd[q][0] = h2f(hc[q].x), dd[q][1] = h2f(hc[q].x >> 16);
     }
+    scales(0u);
   };
-  float acc[NH][4] = {};
-  // the MFMAs of plane step k (pairs of the tile) from slot s
+  float lf[NH][4][4]; // the leaves: [token half][pair p: super-group 2 p + pp][row 4 h + v]
+  // the MFMAs of plane step k (pairs of the tile) from slot s: pair p + 1's MFMAs go out before pair
+  // p's results are used (two result sets live)
   auto plane = [&](u32 k, u32 npair, u32 s) {
     const u32x4 *sl = slot(s);
     const u32 cs = SC == 2u ? 128u * (h & 1u) : 0u; // Q8_0: lanes h odd read the second half plane
-    v4i c[NH][4];
+    v4i c[NH][2];
+    auto mfma = [&](u32 p) {
+      const u32x4 wq = sl[cs + 8u * i16 + ((2u * p + (h >> 1)) ^ v8_swz(i16))];
+      const u32x4 a = KIND == AMDC_Q8_0 ? wq : (wq >> (4u * (h & 1u))) & 0x0F0F0F0Fu;
 #pragma unroll
-    for (u32 p = 0; p < 4u; p++) {
-      if (p < npair) {
-        const u32x4 wq = sl[cs + 8u * i16 + ((2u * p + (h >> 1)) ^ v8_swz(i16))];
-        const u32x4 a = KIND == AMDC_Q8_0 ? wq : (wq >> (4u * (h & 1u))) & 0x0F0F0F0Fu;
-#pragma unroll
-        for (u32 th = 0; th < (u32)NH; th++) {
-          const u32x4 bq = (h >> 1) == pp ? sB[th][p + 4u * k][h & 1u][n] : (u32x4)(0u); // the other half of K is zero
-          c[th][p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, bq), (v4i){0, 0, 0, 0}, 0, 0, 0);
-        }
+      for (u32 th = 0; th < (u32)NH; th++) {
+        const u32x4 bq = (h >> 1) == pp ? sB[th][p + 4u * k][h & 1u][n] : (u32x4)(0u); // the other half of K is zero
+        c[th][p & 1u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, bq), (v4i){0, 0, 0, 0}, 0, 0, 0);
       }
-    }
+    };
+    mfma(0u); // npair >= 1
 #pragma unroll
     for (u32 p = 0; p < 4u; p++) {
       if (p >= npair) break;
-      const u32 bl = 8u * (2u * p + pp) + k; // this lane's block (column pp)
-      const v4f s4 = *(const v4f *)&ssc[w][bl][4u * h];
+      if (p + 1u < npair) mfma(p + 1u);
+      if (p == 0u && k + 1u < 8u) scales(k + 1u); // the next plane's table, while the MFMAs run
+      const u32 gl = 2u * p + pp, bl = 8u * gl + k; // this lane's super-group and block (column pp)
+      const v4f s4 = *(const v4f *)&ssc[w][k & 1u][gl][4u * h];
+      v4f m4 = {};
+      if (K4) m4 = *(const v4f *)&smn[K4 ? w : 0u][k & 1u][gl][4u * h];
 #pragma unroll
       for (u32 th = 0; th < (u32)NH; th++) {
+        const v4i cp = c[th][p & 1u];
         const float da = sda[bl][tk + 8u * th];
         if (KIND == AMDC_Q4_0) {
           const u32 as = __builtin_bit_cast(u32, sxa[bl][tk + 8u * th]);
 #pragma unroll
-          for (u32 v = 0; v < 4u; v++) acc[th][v] += (s4[v] * da) * (float)(int)((u32)c[th][p][v] - 8u * as);
+          for (u32 v = 0; v < 4u; v++) lf[th][p][v] += (s4[v] * da) * (float)(int)((u32)cp[v] - 8u * as);
         } else if (KIND == AMDC_Q8_0) {
 #pragma unroll
-          for (u32 v = 0; v < 4u; v++) acc[th][v] += (s4[v] * da) * (float)c[th][p][v];
+          for (u32 v = 0; v < 4u; v++) lf[th][p][v] += (s4[v] * da) * (float)cp[v];
         } else {
+          const float xa = sxa[bl][tk + 8u * th];
 #pragma unroll
-          for (u32 v = 0; v < 4u; v++) acc[th][v] = __builtin_fmaf(s4[v] * (float)c[th][p][v], da, acc[th][v]);
+          for (u32 v = 0; v < 4u; v++) lf[th][p][v] = __builtin_fmaf(m4[v], xa, __builtin_fmaf(s4[v] * (float)cp[v], da, lf[th][p][v]));
         }
       }
     }
   };
+
+  // the tree over the range's tiles: st[j] holds a pending subtree of 2^j tiles, out the range's sum
+  float st[2][NH][4], out[NH][4];
+#pragma unroll
+  for (u32 th = 0; th < (u32)NH; th++)
+#pragma unroll
+    for (u32 v = 0; v < 4u; v++) out[th][v] = 0.0f, st[0][th][v] = st[1][th][v] = 0.0f;
 
   // software pipeline over (tile, step): step k uses slot k % NS and, once
   // used, the slot is reloaded with step k + NS (of this tile or the next)
@@ -1932,19 +1855,12 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
     v8_barrier(); // the previous tile's readers are done
     stage_tile();
     v8_barrier();
-    if (KIND == AMDC_Q4_K) { // the min term of the tile's blocks, into the pp = 0 columns
 #pragma unroll
-      for (u32 th = 0; th < (u32)NH; th++) {
-        v4f m = {acc[th][0], acc[th][1], acc[th][2], acc[th][3]};
+    for (u32 th = 0; th < (u32)NH; th++)
 #pragma unroll
-        for (u32 q = 0; q < 16u; q++) {
-          const u32 bl = 8u * (h + 4u * (q >> 3)) + (q & 7u); // K index 4 q + h
-          const float bx = pp == 0u ? sxa[bl][tk + 8u * th] : 0.0f;
-          m = __builtin_amdgcn_mfma_f32_16x16x4f32(am[q], bx, m, 0, 0, 0);
-        }
-        acc[th][0] = m[0], acc[th][1] = m[1], acc[th][2] = m[2], acc[th][3] = m[3];
-      }
-    }
+      for (u32 p = 0; p < 4u; p++)
+#pragma unroll
+        for (u32 v = 0; v < 4u; v++) lf[th][p][v] = 0.0f;
     if (more) fetch_tile(t + 1u); // in flight during this tile
 #pragma unroll
     for (u32 k = 0; k < 8u; k++) {
@@ -1953,12 +1869,37 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
       if (k + (u32)NS < 8u) issue(t, k + (u32)NS, k % (u32)NS, true);
       else issue(t + 1u, k + (u32)NS - 8u, k % (u32)NS, more);
     }
+    // the tile's subtree: super-groups (2p, 2p + 1) across the two columns, then ((0 + 1) + (2 + 3)),
+    // then into the tree over tiles (c: the tiles before this one in the range)
+    const u32 c = t - t0;
+#pragma unroll
+    for (u32 th = 0; th < (u32)NH; th++) {
+#pragma unroll
+      for (u32 v = 0; v < 4u; v++) {
+        float pr[4];
+#pragma unroll
+        for (u32 p = 0; p < 4u; p++) pr[p] = lf[th][p][v] + dpp<0x128>(lf[th][p][v]); // row_ror:8
+        float x = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+        if (c & 1u) {
+          x = st[0][th][v] + x;
+          if (c & 2u) out[th][v] = st[1][th][v] + x; // a range of 4 tiles is complete
+          else st[1][th][v] = x;
+        } else {
+          st[0][th][v] = x;
+        }
+      }
+    }
   }
-  // join the two block parities of each token (columns n and n + 8) and store
+  // a range of fewer than 4 tiles: its pending subtrees, from the lowest level up (zero tiles past the range)
+  const u32 cnt = t1 > t0 ? t1 - t0 : 0u;
+  if (cnt < 4u) {
+#pragma unroll
+    for (u32 th = 0; th < (u32)NH; th++)
+#pragma unroll
+      for (u32 v = 0; v < 4u; v++) out[th][v] = cnt == 3u ? st[1][th][v] + st[0][th][v] : cnt == 2u ? st[1][th][v] : st[0][th][v];
+  }
 #pragma unroll
   for (u32 th = 0; th < (u32)NH; th++) {
-#pragma unroll
-    for (u32 v = 0; v < 4u; v++) acc[th][v] += dpp<0x128>(acc[th][v]); // row_ror:8
     const u32 tt = tk + 8u * th;
     if (pp == 0u && tt < T) {
 #pragma unroll
@@ -1966,9 +1907,9 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
         const u32 r = r0 + 4u * h + v;
         if (r >= rows) continue;
         if (part) {
-          part[((u64)ks * T + tt) * rows + r] = acc[th][v];
+          part[((u64)ks * T + tt) * rows + r] = out[th][v];
         } else {
-          float o = acc[th][v];
+          float o = out[th][v];
           if (bias) o = o + bias[r];
           if (res) o = res[(u64)tt * rs + r] + o;
           y[(u64)tt * ys + r] = o;
@@ -1980,34 +1921,34 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
 
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_0_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *part) {
-  gemv8_body<AMDC_Q4_0, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+                                                                   float *part, u32 tps) {
+  gemv8_body<AMDC_Q4_0, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
 }
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *part) {
-  gemv8_body<AMDC_Q4_K, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+                                                                   float *part, u32 tps) {
+  gemv8_body<AMDC_Q4_K, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
 }
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *part) {
-  gemv8_body<AMDC_Q8_0, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+                                                                   float *part, u32 tps) {
+  gemv8_body<AMDC_Q8_0, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
 }
 // the same for up to 16 vectors (two token halves per MFMA A operand)
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_0_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *part) {
-  gemv8_body<AMDC_Q4_0, 2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+                                                                   float *part, u32 tps) {
+  gemv8_body<AMDC_Q4_0, 2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
 }
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *part) {
-  gemv8_body<AMDC_Q4_K, 2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+                                                                   float *part, u32 tps) {
+  gemv8_body<AMDC_Q4_K, 2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
 }
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *part) {
-  gemv8_body<AMDC_Q8_0, 1, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+                                                                   float *part, u32 tps) {
+  gemv8_body<AMDC_Q8_0, 1, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
 }
 
 // The verify GEMV for Q6_K (T <= 8). A Q6_K weight's scale changes every 16
@@ -2034,7 +1975,7 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v16(const uint8
 template <int NQ, int NS>
 __device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y,
                                                u32 rows, u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T,
-                                               u32 xs, u32 ys, u32 rs, float *__restrict__ part) {
+                                               u32 xs, u32 ys, u32 rs, float *__restrict__ part, u32 tps) {
   constexpr u32 NTK = 4u * NQ; // tokens per launch: NQ groups of 4
   typedef __attribute__((address_space(3))) void lds_t;
   constexpr u32 CH = 128u; // u32x4 per 2 KB chunk (16 rows x 128 bytes)
@@ -2055,7 +1996,7 @@ __device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, co
   const u32 lcol = lane & 7u, g0 = lcol ^ v8_swz(lane >> 3), g1 = lcol ^ v8_swz(8u + (lane >> 3));
   const __amdgpu_buffer_rsrc_t rxq = rsrc(xq, (u32)min((u64)T * xs, (u64)0xFFFFFFF0u));
   constexpr u32 OOB = 0xFFFFFFF0u;
-  const u32 ks = blockIdx.y, nks = gridDim.y, t0 = nt * ks / nks, t1 = nt * (ks + 1u) / nks;
+  const u32 ks = blockIdx.y, t0 = ks * tps, t1 = t0 + tps < nt ? t0 + tps : nt;
   auto gtile = [&](u32 t) { return ng - 8u * t < 8u ? ng - 8u * t : 8u; };
   auto slot = [&](u32 s) -> u32x4 * {
     if (s == 0u || NS == 1) return sw0[w];
@@ -2223,12 +2164,12 @@ __device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, co
 
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *part) {
-  gemv8_q6k_body<2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+                                                                   float *part, u32 tps) {
+  gemv8_q6k_body<2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
 }
 // up to 16 vectors: four token groups per A operand, a ring of one step (72 KB of LDS, 2 workgroups per CU)
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                     const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                    float *part) {
-  gemv8_q6k_body<4, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part);
+                                                                    float *part, u32 tps) {
+  gemv8_q6k_body<4, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
 }

@@ -534,3 +534,32 @@ void or_gemv_q8_mt(const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32
 void or_gemv_q6k_mt(const uint32_t *qw, const uint16_t *qs, uint32_t rows, uint32_t nb, const uint8_t *xq, float *y, int nthreads) {
   gemv_mt(4, qw, qs, rows, nb, xq, y, nthreads);
 }
+
+/* or_dequant over up to 256 threads, each a range of whole 256-weight groups. */
+typedef struct {
+  int kind;
+  const uint8_t *src;
+  uint64_t first, n;
+  float *out;
+} dq_job;
+
+static void *run_dq(void *p) {
+  const dq_job *j = p;
+  or_dequant(j->kind, j->src, j->first, j->n, j->out + j->first);
+  return NULL;
+}
+
+void or_dequant_mt(int kind, const uint8_t *src, uint64_t n, float *out, int nt) {
+  if (nt < 1) nt = 1;
+  if (nt > 256) nt = 256;
+  pthread_t th[256];
+  dq_job jb[256];
+  const uint64_t groups = (n + 255u) / 256u;
+  for (int i = 0; i < nt; i++) {
+    const uint64_t a = groups * (uint64_t)i / (uint64_t)nt * 256u, b = groups * (uint64_t)(i + 1) / (uint64_t)nt * 256u;
+    jb[i] = (dq_job){kind, src, a < n ? a : n, (b < n ? b : n) - (a < n ? a : n), out};
+    if (i > 0) pthread_create(&th[i], NULL, run_dq, &jb[i]);
+  }
+  run_dq(&jb[0]);
+  for (int i = 1; i < nt; i++) pthread_join(th[i], NULL);
+}

@@ -90,6 +90,8 @@ void or_block_dots_gguf(int kind, const uint8_t *src, uint32_t rows, uint32_t nb
  * for Q8_0, :98-107 for Q4_0, :108-140 for Q6_K, :142-171 for Q4_K). kind:
  * the GGML id (2, 8, 12, 14). */
 void or_dequant(int kind, const uint8_t *src, uint64_t first, uint64_t n, float *out);
+/* the same for weights 0 .. n - 1 on nthreads threads */
+void or_dequant_mt(int kind, const uint8_t *src, uint64_t n, float *out, int nthreads);
 
 /* A double-precision reference of y = W x straight from the GGUF bytes, and
  * the sum of |terms| of each row (tests/kernel_test.c:59-80): y_ref, mag. */

@@ -55,6 +55,7 @@ class Oracle:
             f.argtypes = [_P, _U32, _U32, _P, _P]
         L.or_block_dots_gguf.argtypes = [C.c_int, _P, _U32, _U32, _P, _P]
         L.or_dequant.argtypes = [C.c_int, _P, C.c_uint64, C.c_uint64, _P]
+        L.or_dequant_mt.argtypes = [C.c_int, _P, C.c_uint64, _P, C.c_int]
         L.or_gemv_f64.argtypes = [C.c_int, _P, _U32, _U32, _P, _P, _P]
         L.or_q4k_qs_n.restype = C.c_size_t
         L.or_q4k_qs_n.argtypes = [_U32, _U32]
@@ -136,9 +137,12 @@ class Oracle:
         self.lib.or_block_dots_gguf(kind, _ptr(np.ascontiguousarray(src)), rows, nb, _ptr(np.ascontiguousarray(xq)), _ptr(out))
         return out.reshape((rows, nb, 2) if h == 2 else (rows, nb))
 
-    def dequant(self, kind, src, n):
+    def dequant(self, kind, src, n, threads=1):
         out = np.zeros(n, dtype=np.float32)
-        self.lib.or_dequant(kind, _ptr(np.ascontiguousarray(src)), 0, n, _ptr(out))
+        if threads > 1:
+            self.lib.or_dequant_mt(kind, _ptr(np.ascontiguousarray(src)), n, _ptr(out), threads)
+        else:
+            self.lib.or_dequant(kind, _ptr(np.ascontiguousarray(src)), 0, n, _ptr(out))
         return out
 
     def gemv_f64(self, kind, src, rows, nb, xq):

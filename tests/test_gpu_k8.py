@@ -35,7 +35,7 @@ def test_block_dots_bitexact(dev, orc, kind, rows, nb):
     assert np.array_equal(got, orc.block_dots_gguf(ttype(kind), c.src, rows, nb, c.xq[0]))
 
 
-SHAPES_Q8 = [(1, 1), (7, 3), (9, 11), (8, 32), (13, 33), (17, 36), (3, 100), (2, 511), (64, 128), (33, 344), (5, 3000)]
+SHAPES_Q8 = [(1, 1), (7, 3), (9, 11), (8, 32), (13, 33), (17, 36), (3, 100), (2, 511), (64, 128), (33, 344), (5, 2048)]
 SHAPES_Q6 = [(1, 8), (7, 16), (9, 40), (3, 64), (37, 160), (19, 544), (8, 192), (3, 1792)]
 
 
@@ -261,11 +261,12 @@ def test_graph_replay_matches_eager(dev, orc):
         assert rel_err(y[c.T - 1], c.y_oracle(c.T - 1), c.mag(c.T - 1)) < TOL
 
 
-@pytest.mark.parametrize("kind,nb", [(0, 511), (0, 3000), (synth.KIND_Q4_K, 2040), (Q8, 2047), (Q6, 2040)])
+@pytest.mark.parametrize("kind,nb", [(0, 511), (0, 2048), (synth.KIND_Q4_K, 2040), (Q8, 2047), (Q6, 2040)])
 def test_max_sizes(dev, orc, kind, nb):
     """The largest rows the reference's loader accepts for each kind (core/ie_core.h:60, 187, 258-260:
     Q4_0 nb < 512, Q8_0 nb < 2048, Q4_K / Q6_K nb < 2048 with nb % 8 == 0; Q4_0 also past the
-    reference's limit, where it would switch to Q8_0): decode, verify (T = 8) and GEMM (T = 32)."""
+    reference's limit, up to this library's 2048 blocks): decode, verify (T = 8) and GEMM (T = 32).
+    2049 blocks are refused before any launch."""
     rows = 37
     c = Case(dev, orc, kind, rows, nb, 32, seed=nb)
     c.quant()
@@ -279,3 +280,5 @@ def test_max_sizes(dev, orc, kind, nb):
     y = c.y_gpu()
     for t in (0, 31):
         assert rel_err(y[t], c.y_oracle(t), c.mag(t)) < TOL, t
+    with pytest.raises(dev.AmdcError, match="2048 blocks"):
+        dev.gemv(kind, c.W, c.Q, c.Y, rows, 2056)

@@ -118,7 +118,7 @@ def test_gemv_t1(dev, orc, kind, rows, nb):
 
 
 @pytest.mark.parametrize("lanes", [4, 8, 16, 32, 64])
-@pytest.mark.parametrize("unroll,form", [(0, 1), (0, 2), (1, 0), (2, 0)])
+@pytest.mark.parametrize("unroll,form", [(0, 0), (0, 1), (0, 2)])
 @pytest.mark.parametrize("wgs", [0, 3])  # 3 workgroups: each loops over several row groups
 @pytest.mark.parametrize("kind,rows,nb", [(0, 70, 344), (0, 33, 300), (3, 45, 160), (3, 6, 544)])
 def test_gemv_t1_tunings(dev, orc, kind, rows, nb, lanes, unroll, form, wgs):
@@ -154,7 +154,7 @@ def test_gemv_epilogue_bias_res(dev, orc, kind, form):
 
 # ---------------------------------------------------------------- multi-vector GEMV (verify)
 
-@pytest.mark.parametrize("path", [0, 1])  # 0: int8-MFMA verify kernels, 8 vectors per launch; 1: the dot4 kernels
+@pytest.mark.parametrize("path", [0, 1])  # 0: the int8-MFMA verify kernels (16 vectors per launch); 1: a decode launch per vector
 @pytest.mark.parametrize("T", [2, 5, 8, 9, 16, 19])
 @pytest.mark.parametrize("kind,rows,nb", [(0, 40, 128), (0, 130, 43), (3, 33, 160), (3, 21, 544), (3, 200, 72)])
 def test_gemv_multi(dev, orc, kind, rows, nb, T, path):
@@ -165,14 +165,14 @@ def test_gemv_multi(dev, orc, kind, rows, nb, T, path):
     R = dev.DevBuf.of(res)
     dev.gemv_t(kind, c.W, c.Q, c.Y, rows, nb, T, c.xs, rows, rows, res=R)
     y = c.y_gpu()
-    # and the single-vector kernel per token: the same values within the bound
+    # and the single-vector kernel per token: within the bound of the oracle, and the same bits
     Y1 = dev.DevBuf(rows * 4)
     for t in range(T):
         want = orc.epilogue(c.y_oracle(t), None, res[t])
         mag = c.mag(t) + np.abs(res[t])
         assert rel_err(y[t], want, mag) < TOL, t
         dev.gemv(kind, c.W, c.Q.ptr + t * c.xs, Y1, rows, nb, res=R.ptr + 4 * t * rows)
-        assert rel_err(Y1.download(np.float32), want, mag) < TOL, t
+        assert np.array_equal(Y1.download(np.uint32), y[t].view(np.uint32)), t
 
 
 # ---------------------------------------------------------------- prefill GEMM
@@ -326,8 +326,8 @@ def test_gemv_fused_quant_special_blocks(dev, orc, kind, nb):
 @pytest.mark.parametrize("T", [8, 11, 16])
 def test_verify_splitk(dev, orc, kind, T):
     """The verify kernels (T <= 8, and the 16-vector form for T = 9..16) with K split over workgroups
-    (partial sums added in split order by the reduce kernel): calls in a row with different splits, bias
-    and residual all match the oracle, and a repeated split gives the same bits."""
+    (aligned tile ranges, their sums added in a tree by the reduce kernel): calls in a row with different
+    splits, bias and residual all match the oracle, and every split gives the same bits."""
     rows, nb = 200, 544
     c = Case(dev, orc, kind, rows, nb, T, seed=21)
     c.quant()
@@ -345,8 +345,8 @@ def test_verify_splitk(dev, orc, kind, T):
             want = orc.epilogue(c.y_oracle(t), bias, res[t])
             assert rel_err(y[t], want, c.mag(t) + np.abs(bias) + np.abs(res[t])) < TOL, (ks, t)
         u = y.view(np.uint32).copy()
-        if ks in bits:
-            assert np.array_equal(u, bits[ks]), ks
+        for k, b in bits.items():
+            assert np.array_equal(u, b), (ks, k)
         bits[ks] = u
 
 
