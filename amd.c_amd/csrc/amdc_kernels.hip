@@ -1689,7 +1689,9 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
   __shared__ __attribute__((aligned(16))) u32x4 sw2[NS > 2 ? 4 : 1][NS > 2 ? SC * 128u : 1u];
   __shared__ __attribute__((aligned(16))) u32x4 sw3[NS > 2 ? 4 : 1][NS > 2 ? SC * 128u : 1u];
   constexpr u32 NTK = 8u * NH;                                      // tokens per launch: NH halves of 8
-  __shared__ __attribute__((aligned(16))) u32x4 sB[NH][32][2][16]; // [token half][pair p + 4 k][quarter & 1][column]: a column's nonzero half of K
+  // [token half][pair p + 4 k][K quarter][column]: the B operands, read by every lane as they are (the
+  // quarters outside a column's half of K hold zeros, written once)
+  __shared__ __attribute__((aligned(16))) u32x4 sB[NH][32][4][16];
   __shared__ __attribute__((aligned(16))) float sda[64][NTK];      // d_a [block of tile][token]
   __shared__ __attribute__((aligned(16))) float sxa[64][NTK];      // Q4_K: d_a asum; Q4_0: asum (as int bits)
   // per wave and plane (double-buffered): s (Q4_K d sc, Q4_0 / Q8_0 d) and Q4_K -(dmin mn) [super-group of tile][row]
@@ -1728,30 +1730,41 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_t *)(slot(s) + 128u * c + 64u), 16, g1 < gt ? wl1 + base + 16u * g1 : OOB, 0, 0, 0);
     }
   };
-  // activations of tile t in registers (thread: 2 NH of the 16-byte halves, 2 NH of the (block, token) scale pairs)
+  // activations of tile t in registers (thread: 2 NH of the 16-byte halves, 2 NH of the (block, token) scale
+  // pairs); the lane offsets of tile 0 computed once: tile t adds 2048 t (halves), 4 t (scales), 128 t
+  // (headers), and a load is valid while its block of the tile is under lim(t)
   u32x4 ra4[4 * NH];
   float rd[2 * NH];
   u32 rx[2 * NH];
   u32x4 rh[2]; // the next tile's headers of row i16, super-groups h, h + 4
-  auto fetch_tile = [&](u32 t) {
-    const u32 gt = gtile(t);
+  u32 xo[4 * NH], xb[4 * NH], so[2 * NH], sbl[2 * NH];
 #pragma unroll
-    for (u32 c = 0; c < 4u * NH; c++) {
-      const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, gl = bl >> 3, k = bl & 7u, b = 64u * t + 8u * gl + k;
-      const bool ok = tok < T && gl < gt && b < nb;
-      ra4[c] = __builtin_amdgcn_raw_buffer_load_b128(rxq, ok ? tok * xs + 32u * b + 16u * half : OOB, 0, 0);
-    }
+  for (u32 c = 0; c < 4u * NH; c++) {
+    const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7;
+    xo[c] = tok < T ? tok * xs + 32u * bl + 16u * half : OOB;
+    xb[c] = tok < T ? bl : 64u;
+  }
+#pragma unroll
+  for (u32 c = 0; c < 2u * NH; c++) {
+    const u32 i = tid + c * NT, tok = i & (NTK - 1u), bl = i / NTK;
+    so[c] = tok * xs + 4u * bl;
+    sbl[c] = tok < T ? bl : 64u;
+  }
+  auto fetch_tile = [&](u32 t) {
+    const u32 lim = min(8u * gtile(t), nb - 64u * t); // blocks of tile t
+#pragma unroll
+    for (u32 c = 0; c < 4u * NH; c++)
+      ra4[c] = __builtin_amdgcn_raw_buffer_load_b128(rxq, xb[c] < lim ? xo[c] + 2048u * t : OOB, 0, 0);
 #pragma unroll
     for (u32 c = 0; c < 2u * NH; c++) {
-      const u32 i = tid + c * NT, tok = i & (NTK - 1u), bl = i / NTK, b = 64u * t + bl;
-      const bool ok = tok < T && (bl >> 3) < gt && b < nb;
-      rd[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxq, ok ? tok * xs + 32u * nb + 4u * b : OOB, 0, 0));
-      rx[c] = __builtin_amdgcn_raw_buffer_load_b32(rxq, ok ? tok * xs + 36u * nb + 4u * b : OOB, 0, 0);
+      const bool ok = sbl[c] < lim;
+      rd[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxq, ok ? so[c] + 32u * nb + 256u * t : OOB, 0, 0));
+      rx[c] = __builtin_amdgcn_raw_buffer_load_b32(rxq, ok ? so[c] + 36u * nb + 256u * t : OOB, 0, 0);
     }
 #pragma unroll
     for (u32 q = 0; q < 2u; q++) {
       const u32 gl = h + 4u * q;
-      rh[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, gl < gt ? wo + 16u * (8u * t + gl) : OOB, 0, 0);
+      rh[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, 8u * gl < lim ? wo + 16u * (8u * t + gl) : OOB, 0, 0);
     }
   };
   u32x4 hc[2];   // the current tile's headers (rh is refilled with the next tile's during this one)
@@ -1772,9 +1785,9 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
   };
   auto stage_tile = [&]() {
 #pragma unroll
-    for (u32 c = 0; c < 4u * NH; c++) {
+    for (u32 c = 0; c < 4u * NH; c++) { // block (gl, k) of token tok: quarter 2 (gl & 1) + half of column tok % 8 + 8 (gl & 1)
       const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, gl = bl >> 3, k = bl & 7u;
-      sB[tok >> 3][(gl >> 1) + 4u * k][half][(tok & 7u) + 8u * (gl & 1u)] = ra4[c];
+      sB[tok >> 3][(gl >> 1) + 4u * k][2u * (gl & 1u) + half][(tok & 7u) + 8u * (gl & 1u)] = ra4[c];
     }
 #pragma unroll
     for (u32 c = 0; c < 2u * NH; c++) {
@@ -1801,7 +1814,7 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
       const u32x4 a = KIND == AMDC_Q8_0 ? wq : (wq >> (4u * (h & 1u))) & 0x0F0F0F0Fu;
 #pragma unroll
       for (u32 th = 0; th < (u32)NH; th++) {
-        const u32x4 bq = (h >> 1) == pp ? sB[th][p + 4u * k][h & 1u][n] : (u32x4)(0u); // the other half of K is zero
+        const u32x4 bq = sB[th][p + 4u * k][h][n];
         c[th][p & 1u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, bq), (v4i){0, 0, 0, 0}, 0, 0, 0);
       }
     };
@@ -1844,6 +1857,12 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
 
   // software pipeline over (tile, step): step k uses slot k % NS and, once
   // used, the slot is reloaded with step k + NS (of this tile or the next)
+  // the zero quarters of the B operands (column n: the quarters of the other block's half of K)
+#pragma unroll
+  for (u32 c = 0; c < 4u * NH; c++) {
+    const u32 i = tid + c * NT, n_ = i & 15u, qz = (i >> 4) & 1u, pk = (i >> 5) & 31u, th = i >> 10;
+    sB[th][pk][2u * (1u - (n_ >> 3)) + qz][n_] = (u32x4)(0u);
+  }
   if (t0 < t1) {
     fetch_tile(t0);
 #pragma unroll
