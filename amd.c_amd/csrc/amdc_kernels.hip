@@ -52,7 +52,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, u32 n) { r
 
 #define NT 256u
 #define SCH 3u  // Q8 blocks per thread whose staging loads are in flight together (decode GEMV)
-#define QCH 17u // passes of 32 blocks whose activation loads are in flight together (fused quantization)
+#define QCH 4u // passes of 32 blocks whose activation loads are in flight together (fused quantization: 128 blocks)
 
 // ------------------------------------------------------------------ helpers
 
@@ -363,7 +363,7 @@ __device__ __forceinline__ float item_dot(const typename ItemOf<KIND>::type &it,
 // the workgroup; each block goes to the LDS slot of the staged layout
 // (permuted as the weights, p = (b % 8) ng + b / 8) as lo/hi words, d and
 // asum, and, when q8out is given, workgroup 0 also writes the Q8 buffer. The
-// activation loads of up to QCH passes are issued at once (load), so that a
+// activation loads of NC passes are issued at once (load), so that a
 // kernel can put them ahead of its first weight loads and quantize (quant)
 // while the weights are in flight (loads count down in issue order); they are
 // unconditional (a block past nb reads the last block again and takes zeros),
@@ -383,7 +383,7 @@ template <u32 NC> struct FusedQ8T {
   __device__ __forceinline__ void quant(u32 b0, u32 nb, u32 ng, u32x4 *s_lo, u32x4 *s_hi, float *s_d, u32 *s_as, uint8_t *__restrict__ q8out) {
     const u32 tid = threadIdx.x, e = tid & 7u, nblk = 8u * ng;
 #pragma unroll
-    for (u32 c = 0; c < QCH; c++) {
+    for (u32 c = 0; c < NC; c++) {
       if (b0 + 32u * c >= nblk) break;
       const u32 b = b0 + 32u * c + (tid >> 3);
       float a = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(xv[c].x), __builtin_fabsf(xv[c].y)),
