@@ -7,7 +7,7 @@ are loaded as one matrix (wqkv = [wq; wk; wv], wgu = [wgate; wup], as
 src/model.c:696, 955 concat_mats), so a step is x -> qkv, o, gate_up, down,
 lm_head: 5 GEMVs, each on an f32 vector quantized to Q8 first (inside the
 GEMV's own launch where nb <= 128, else by a separate amdc_quant_q8 launch:
-7 launches). The same set as 8 separate GEMVs with 5 separate quantizations
+6 launches). The same set as 8 separate GEMVs with 5 separate quantizations
 is timed too (ms_per_step_unmerged). Weight copies are rotated so that the
 weights streamed per step come from HBM (the copies total >= 2 GB, far above
 the 256 MB Infinity Cache). value = weight bytes of the step (the reference's
@@ -15,19 +15,25 @@ rows * nb * 18, src/hip.c:1831) / step time, inputs resident in HBM.
 
 The step is captured once per weight copy as a HIP graph and the graphs are
 replayed back to back (no host launch per kernel), timed by HIP events on
-their stream; each GEMV's own duration comes from a graph of that GEMV
-launched back to back over the weight copies (the roofline's "achieved").
-Also measured, in "detail": c0 (one 4096x4096 Q4_0 GEMV), c2 (Q4_K 27B
-shapes), c3 (T = 8 verify GEMV, weights counted once) and c4 (the T = 256
-prefill GEMM, TOPS = 2 T rows cols / time), each from HIP events around every
-launch on the stream the kernels run on (graphs of back-to-back launches over
-rotating weight copies, averaged).
+their stream. roofline describes the step's own launches: each launch of the
+step (the same call, the same kernel) timed alone by HIP events on the
+stream it runs on, in a graph of that launch repeated over the weight
+copies; "achieved" is the algorithmic bytes over the summed durations of the
+step's dominant kernel (amdc_gemv_q4_0_x1, 4 of its 6 launches), and
+"traffic" the HBM bytes per launch of that kernel read live from rocprofv3
+FETCH_SIZE / WRITE_SIZE counter passes over the same launches (a child
+process under rocprofv3, one pass per counter), scaled by what the counters
+read for a copy kernel of known size. Also measured, in "detail": c0 (one
+4096x4096 Q4_0 GEMV), c2 (Q4_K 27B shapes), c3 (T = 8 verify GEMV, weights
+counted once) and c4 (the T = 256 prefill GEMM on the f16 MFMA and on the
+int8 MFMA, TOPS = 2 T rows cols / time), from HIP events around graphs of
+back-to-back launches over rotating weight copies.
 
 CPU baseline: the reference's own cpu_gemv_q4 (oracle/_ref/libref_cpu.so,
 compiled from hanw/amd.c src/cpu.c), one core, on a bounded sample of the
 same c1 step (else the C restatement in oracle/, kind "port").
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-traffic]
 """
 import argparse
 import json
@@ -98,6 +104,18 @@ class Timer:
         self.S.sync()
         return e0.elapsed_ms(e1) / reps
 
+    def step_ms(self, step, copies, set_bytes, steps, warmup):
+        """ms per step: graphs of m consecutive steps (weight copies ci .. ci + m - 1, m chosen so that a
+        graph holds about 150 us of GPU work and the host's graph launches stay ahead of the GPU), replayed
+        round robin; at least `steps` steps timed (a multiple of m). Returns (ms per step, steps timed)."""
+        m = max(1, min(copies, -(-600_000_000 // max(set_bytes, 1))))
+        ng = max(1, copies // m)
+        graphs = [self.graph(lambda s, k=k: [step((k * m + i) % copies, s) for i in range(m)]) for k in range(ng)]
+        reps = -(-steps // m)
+        ms = self.replay_ms(graphs, reps, max(1, -(-warmup // m)))
+        del graphs
+        return ms / m, reps * m
+
     def per_launch_ms(self, launch, n, reps=4):
         """average ms of one launch: n launches (launch(i, stream)) in one graph, replayed."""
         g = self.graph(lambda s: [launch(i, s) for i in range(n)])
@@ -146,9 +164,7 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
                 amdc.quant_q8(X, Q, c // 32, stream=s)
             amdc.gemv(kind, M.dev[ci][i], Q, Y, r, c // 32, stream=s)
 
-    graphs = [timer.graph(lambda s, ci=ci: step_unmerged(ci, s)) for ci in range(M.copies)]
-    ms_unmerged = timer.replay_ms(graphs, steps, warmup)
-    del graphs
+    ms_unmerged, _ = timer.step_ms(step_unmerged, M.copies, M.set_bytes, steps, warmup)
     per, tot = {}, 0.0
     for i, (name, r, c) in enumerate(shapes):
         amdc.quant_q8(X, Q, c // 32)
@@ -174,9 +190,7 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
         for gi, (name, r, c, _) in enumerate(groups):
             amdc.gemv_x(kind, G.dev[ci][gi], X, Y, r, c // 32, stream=s)
 
-    graphs = [timer.graph(lambda s, ci=ci: step(ci, s)) for ci in range(G.copies)]
-    ms_launches = timer.replay_ms(graphs, steps, warmup)
-    del graphs
+    ms_launches, steps_timed = timer.step_ms(step, G.copies, G.set_bytes, steps, warmup)
     # the same step as one GEMV chain launch per weight copy, a grid barrier after each operation
     # (the next one waits for it, as the launches wait for each other); as amdc_gemv_q4_x, a GEMV
     # quantizes its f32 input in every workgroup for nb <= 128, else after a quantize operation
@@ -192,30 +206,59 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
         chains.append(amdc.Chain(ops))
     chains[0].launch()
     chains[0].check()
-    graphs = [timer.graph(lambda s, ch=ch: ch.launch(s)) for ch in chains]
-    ms_chain = timer.replay_ms(graphs, steps, warmup)
-    del graphs
+    ms_chain, _ = timer.step_ms(lambda ci, s: chains[ci].launch(s), G.copies, G.set_bytes, steps, warmup)
     chains[0].check()
     del chains
     ms = min(ms_launches, ms_chain)
-    per_m, tot_m = {}, 0.0
+    # each launch of the step alone, the same call as in the step: amdc_gemv_q4_x / _q4k_x (the quantization
+    # inside the GEMV where nb <= 128, else amdc_quant_q8 + the GEMV: two launches)
+    launches = []
     for gi, (name, r, c, _) in enumerate(groups):
-        amdc.quant_q8(X, Q, c // 32)
-        t = timer.per_launch_ms(lambda j, s, gi=gi, r=r, c=c: amdc.gemv(kind, G.dev[j % G.copies][gi], Q, Y, r, c // 32, stream=s),
-                                G.copies, reps=max(2, steps // 4))
-        b = wbytes(r, c)
-        per_m[name] = {"rows": r, "cols": c, "us": round(t * 1e3, 3), "GB/s": round(b / t / 1e6, 1),
-                       "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4)}
-        tot_m += t
+        nb, b = c // 32, wbytes(r, c, kind)
+        if nb <= 128:
+            t = timer.per_launch_ms(lambda j, s, gi=gi, r=r, nb=nb: amdc.gemv_x(kind, G.dev[j % G.copies][gi], X, Y, r, nb, stream=s),
+                                    G.copies, reps=max(2, steps // 4))
+            launches.append(launch_rec(name, decode_kernel(kind, nb, True), r, c, b, t))
+        else:
+            tq = timer.per_launch_ms(lambda j, s, nb=nb: amdc.quant_q8(X, Q, nb, stream=s), 64)
+            launches.append(launch_rec(name + " (input)", "amdc_quant_q8", 1, c, 0, tq))
+            amdc.quant_q8(X, Q, nb)
+            t = timer.per_launch_ms(lambda j, s, gi=gi, r=r, nb=nb: amdc.gemv(kind, G.dev[j % G.copies][gi], Q, Y, r, nb, stream=s),
+                                    G.copies, reps=max(2, steps // 4))
+            launches.append(launch_rec(name, decode_kernel(kind, nb, False), r, c, b, t))
     set_bytes = G.set_bytes
     del G
-    return {"set_bytes": set_bytes, "ms_per_step": ms, "ms_per_step_unmerged": ms_unmerged,
+    kt = {}
+    for l in launches:
+        kt.setdefault(l["kernel"], [0.0, 0, 0])
+        kt[l["kernel"]][0] += l["us"]
+        kt[l["kernel"]][1] += l["bytes"]
+        kt[l["kernel"]][2] += 1
+    dom = max(kt, key=lambda k: kt[k][0])
+    launch_us = sum(l["us"] for l in launches)
+    return {"set_bytes": set_bytes, "ms_per_step": ms, "steps_timed": steps_timed, "ms_per_step_unmerged": ms_unmerged,
             "ms_per_step_launches": ms_launches, "ms_per_step_chain": ms_chain,
             "step_form": "chain" if ms_chain <= ms_launches else "launches",
-            "launches_per_step": sum(1 if (c // 32) <= 128 else 2 for _, _, c, _ in groups),
-            "per_shape": per, "per_merged_shape": per_m,
-            "kernel_GBps": set_bytes / tot_m / 1e6, "kernel_us_total": tot_m * 1e3,
+            "launches_per_step": len(launches), "per_shape": per, "step_launches": launches,
+            "dominant_kernel": dom, "dominant_launches": kt[dom][2],
+            "dominant_bytes_per_launch": kt[dom][1] / kt[dom][2], "dominant_us_per_launch": kt[dom][0] / kt[dom][2],
+            "dominant_GBps": kt[dom][1] / kt[dom][0] / 1e3,
+            "launches_us_total": launch_us, "launches_GBps": set_bytes / launch_us / 1e3,
             "kernel_GBps_unmerged": set_bytes / tot / 1e6, "weight_copies": -(-ROTATE_BYTES // set_bytes)}
+
+
+def decode_kernel(kind, nb, fused):
+    """The decode kernel the host picks for a row of nb blocks (amdc_host.c gemv_launch / gemv_x)."""
+    k = {synth.KIND_Q4_0: "amdc_gemv_q4_0", synth.KIND_Q4_K: "amdc_gemv_q4_k"}[kind]
+    if fused and nb <= 128:
+        return k + "_x1"
+    return k + ("_p2" if (nb + 7) // 8 > 32 else "_p1")
+
+
+def launch_rec(op, kernel, rows, cols, b, t_ms):
+    us = t_ms * 1e3
+    return {"op": op, "kernel": kernel, "rows": rows, "cols": cols, "weight_bytes": b, "bytes": b, "us": round(us, 3),
+            "GB/s": round(b / us / 1e3, 1) if b else None, "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4) if b else None}
 
 
 def verify_set(steps, seed, timer):
@@ -262,7 +305,14 @@ def prefill_set(steps, seed, timer):
         t = timer.per_launch_ms(lambda j, s: amdc.gemm_q4k(M.dev[j % M.copies][0], Q, Y, r, nb, T, xs, r, stream=s), M.copies, reps=2)
         tops = 2.0 * T * r * c / t / 1e9
         out[name] = {"rows": r, "cols": c, "T": T, "us": round(t * 1e3, 3), "TOPS": round(tops, 1),
-                     "int8_mfma_frac": round(tops / INT8_PEAK_TOPS, 4)}
+                     "int8_mfma_frac": round(tops / INT8_PEAK_TOPS, 4), "kernel": "f16 MFMA (default)"}
+        # the int8-MFMA kernel (tuning gemm_kernel 2: 64 rows x 128 tokens, 1: x 64 tokens) beside it
+        for kk, label in ((2, "int8_n128"), (1, "int8_n64")):
+            amdc.set_tuning(gemm_kernel=kk)
+            t8 = timer.per_launch_ms(lambda j, s: amdc.gemm_q4k(M.dev[j % M.copies][0], Q, Y, r, nb, T, xs, r, stream=s), M.copies, reps=2)
+            amdc.set_tuning()
+            out[name][label] = {"us": round(t8 * 1e3, 3), "TOPS": round(2.0 * T * r * c / t8 / 1e9, 1),
+                                "int8_mfma_frac": round(2.0 * T * r * c / t8 / 1e9 / INT8_PEAK_TOPS, 4)}
         del M
     return out
 
@@ -426,15 +476,70 @@ def cpu_baseline_rows(seed, budget_s=6.0):
             "sample": f"{n} c1 steps in {el:.1f} s, {cores} threads, oracle/amdc_oracle.c row-parallel (bit-identical to cpu_gemv_q4)"}
 
 
-def traffic_from_profiles():
-    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC summary, if any."""
-    p = os.path.join(ROOT, "profiles", "gemv_q4_0_c1_traffic.txt")
-    if not os.path.exists(p):
-        return None
-    for line in open(p):
-        if line.startswith("traffic_bytes_per_launch_c1_avg:"):
-            return float(line.split(":")[1])
-    return None
+# ---------------------------------------------------------------- HBM traffic (rocprofv3 counters, live)
+
+CAL_BYTES = 256 << 20
+
+
+def traffic_child(seed):
+    """Run under rocprofv3 --pmc by measure_traffic: the probe copy of CAL_BYTES twice (the counters'
+    yardstick), then each launch of the c1 step 3 times, eager (one copy of the merged matrices)."""
+    amdc.open_device()
+    A, B = amdc.DevBuf(CAL_BYTES), amdc.DevBuf(CAL_BYTES)
+    A.fill(1)
+    for _ in range(2):
+        amdc.probe_copy(B, A, CAL_BYTES, 4096)
+    amdc.sync()
+    del A, B
+    kind = synth.CONFIGS["c1"]["kind"]
+    groups = merged_groups(synth.CONFIGS["c1"]["shapes"])
+    W = [amdc.DevBuf.of(amdc.repack(kind, synth.gguf(kind, r, c, seed + i), r, c)) for i, (_, r, c, _) in enumerate(groups)]
+    cols_max = max(c for _, _, c, _ in groups)
+    X = amdc.DevBuf.of(synth.activations(1, cols_max, seed + 99)[0])
+    Q, Y = amdc.DevBuf(q8_stride(cols_max // 32)), amdc.DevBuf(4 * max(r for _, r, _, _ in groups))
+    for gi, (_, r, c, _) in enumerate(groups):
+        for _ in range(3):
+            amdc.gemv_x(kind, W[gi], X, Y, r, c // 32)
+    amdc.sync()
+
+
+def measure_traffic(seed, kernel):
+    """HBM bytes per launch of `kernel` in the c1 step: two rocprofv3 --pmc passes (FETCH_SIZE, then
+    WRITE_SIZE, KiB per dispatch) over traffic_child, each counter scaled by what it reads for the probe
+    copy (CAL_BYTES read, CAL_BYTES written). Returns (bytes per launch, details) or (None, reason)."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    if shutil.which("rocprofv3") is None:
+        return None, "rocprofv3 not found"
+    per = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="amdc_pmc_", dir="/tmp")
+        cmd = ["rocprofv3", "--pmc", ctr, "-d", d, "-o", "t", "--output-format", "csv", "--",
+               sys.executable, os.path.abspath(__file__), "--traffic-child", "--seed", str(seed)]
+        try:
+            r = subprocess.run(cmd, cwd="/tmp", env={**os.environ, "TMPDIR": "/tmp"}, capture_output=True, text=True, timeout=240)
+        except subprocess.TimeoutExpired:
+            return None, f"rocprofv3 --pmc {ctr} timed out"
+        files = [os.path.join(dp, f) for dp, _, fs in os.walk(d) for f in fs if f.endswith("counter_collection.csv")]
+        if r.returncode != 0 or not files:
+            return None, f"rocprofv3 --pmc {ctr} failed (rc {r.returncode}): {(r.stderr or '')[-300:]}"
+        vals = {}
+        for row in csv.DictReader(open(files[0])):
+            if row["Counter_Name"] == ctr:
+                vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+        shutil.rmtree(d, ignore_errors=True)
+        cal = vals.get("amdc_probe_copy")
+        mine = vals.get(kernel)
+        if not cal or not mine:
+            return None, f"{ctr}: no dispatches of amdc_probe_copy / {kernel} in the counter output"
+        scale = CAL_BYTES / (sum(cal) / len(cal) * 1024.0)
+        per[ctr] = {"KiB_per_dispatch": round(sum(mine) / len(mine), 1), "scale": round(scale, 4),
+                    "bytes_per_launch": sum(mine) / len(mine) * 1024.0 * scale, "dispatches": len(mine)}
+    total = per["FETCH_SIZE"]["bytes_per_launch"] + per["WRITE_SIZE"]["bytes_per_launch"]
+    return total, per
 
 
 def main():
@@ -449,7 +554,12 @@ def main():
                     help="detail sets to run after the headline (comma list of c0, c2, c3, c4, producers, k8, load)")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run the probe copy kernel over 256 MiB 3 times (the FETCH_SIZE / WRITE_SIZE yardstick)")
+    ap.add_argument("--no-traffic", action="store_true", help="no rocprofv3 counter passes (roofline.traffic null)")
+    ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
     a = ap.parse_args()
+    if a.traffic_child:
+        traffic_child(a.seed)
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU; the GEMV path shards by rows across GPUs by design only "
               "(see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
@@ -468,13 +578,15 @@ def main():
     timer = Timer()
     c1 = gemv_set("c1", a.steps, a.warmup, a.seed, timer)
     value = c1["set_bytes"] / (c1["ms_per_step"] * 1e-3) / 1e9
-    print(f"bench: c1 {value:.1f} GB/s per step, kernels {c1['kernel_GBps']:.1f} GB/s", file=sys.stderr, flush=True)
+    print(f"bench: c1 {value:.1f} GB/s per step, {c1['dominant_kernel']} {c1['dominant_GBps']:.1f} GB/s, "
+          f"launches alone {c1['launches_GBps']:.1f} GB/s", file=sys.stderr, flush=True)
     detail = {"c1": c1}
     sets = set() if a.quick else set(a.sets.split(","))
     for name in ("c0", "c2"):
         if name in sets:
             detail[name] = gemv_set(name, a.steps, 2, a.seed + 1000, timer)
-            print(f"bench: {name} kernels {detail[name]['kernel_GBps']:.1f} GB/s", file=sys.stderr, flush=True)
+            print(f"bench: {name} {detail[name]['set_bytes'] / detail[name]['ms_per_step'] / 1e6:.1f} GB/s per step, "
+                  f"launches alone {detail[name]['launches_GBps']:.1f} GB/s", file=sys.stderr, flush=True)
     for key, name, fn in (("c3", "c3", lambda: verify_set(a.steps, a.seed + 2000, timer)),
                           ("c4", "c4", lambda: prefill_set(a.steps, a.seed + 3000, timer)),
                           ("producers", "producers", lambda: producers_set(timer)),
@@ -489,13 +601,16 @@ def main():
         print(f"bench: cpu {json.dumps(cpu)}", file=sys.stderr, flush=True)
         detail["cpu_all_cores"] = cpu_baseline_rows(a.seed)
         print(f"bench: cpu_all_cores {json.dumps(detail['cpu_all_cores'])}", file=sys.stderr, flush=True)
-    ach = c1["kernel_GBps"]
+    traffic, tinfo = (None, "not measured (--no-traffic or --quick)") if (a.no_traffic or a.quick) else \
+        measure_traffic(a.seed, c1["dominant_kernel"])
+    print(f"bench: traffic {traffic} {json.dumps(tinfo)}", file=sys.stderr, flush=True)
+    ach = c1["dominant_GBps"]
     out = {
         "metric": METRIC,
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": a.steps,
+        "steps": c1["steps_timed"],
         "warmup": a.warmup,
         "ms_per_step": round(c1["ms_per_step"], 4),
         "higher_is_better": True,
@@ -509,8 +624,10 @@ def main():
                    "launches_per_step": c1["launches_per_step"], "ms_per_step_unmerged": round(c1["ms_per_step_unmerged"], 4),
                    "weight_bytes_per_step": c1["set_bytes"], "rotation_copies_bytes": ROTATE_BYTES, "batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-                     "kernel": "amdc_gemv_q4_0_p1 (down: amdc_gemv_q4_0_p2)", "bytes_per_launch_avg": c1["set_bytes"] / len(c1["per_merged_shape"])},
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": round(traffic) if traffic else None,
+                     "kernel": c1["dominant_kernel"], "launches_per_step": c1["dominant_launches"],
+                     "algorithmic_bytes_per_launch": round(c1["dominant_bytes_per_launch"]),
+                     "us_per_launch": round(c1["dominant_us_per_launch"], 3), "traffic_counters": tinfo},
         "cpu_baseline": cpu,
         "detail": detail,
     }
