@@ -16,10 +16,9 @@
 //   amdc_gemv_{q4_0,q4_k,q8_0,q6_k}_v8, amdc_gemv_{q4_0,q4_k,q8_0,q6_k}_v16,
 //   amdc_gemm_reduce   the verify GEMV, T <= 8 (_v8) or 16 (_v16) vectors on
 //                      int8 MFMA, weights staged through LDS, K split over
-//                      workgroups and reduced in split order
+//                      workgroups over aligned ranges of tiles and reduced by a
+//                      pairwise tree over the ranges
 //                      (ie_gemv_q4kq8_tr8 / _tr / _ts2, ie_gemv_q6kq8_tr8, ...)
-//   amdc_gemv_{q4_0,q4_k}_t{1,8,16}, _t1u1
-//                      dot4 multi-vector GEMVs (a tuning alternative)
 //   amdc_q8_prep, amdc_gemmh_m64_n{64,128}, amdc_gemmh_{q4_0,q8_0,q6_k}_m64_n{64,128}
 //                      the prefill chunk GEMM on the f16 MFMA with exact
 //                      integer block sums (ie_gemm_q4kr, ie_gemm_q8r, ie_gemm_q6kr)

@@ -174,15 +174,17 @@ int amdc_gemv_q6k_x(const void *w, const float *x, float *y, uint32_t rows, uint
  * graph capture before capturing). Replaces the multi-token branch of
  * OP_GEMV_Q4K (ie_gemv_q4kq8_ts2 / _tr8 / _tr, src/hip.c:1004-1020); the
  * Q4_0 form has no reference kernel (the reference runs OP_GEMV_Q4 per
- * token, src/hip.c:1583-1588); its values agree with T calls of
- * amdc_gemv_q4 within the same bound (the float sums run in another order). */
+ * token, src/hip.c:1583-1588). Every vector's y equals the decode GEMV of that
+ * vector (amdc_gemv_q4 / _q4k / _q8) bit for bit, at every K split, as the
+ * reference's multi-token kernels equal its single-token one
+ * (kernels/ie_kernels.c:481-482); Q6_K's agrees within the 1e-5 bound. */
 int amdc_gemv_q4_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                    uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 int amdc_gemv_q4k_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                     uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
-/* Q8_0 / Q6_K over T vectors: the decode GEMV per vector (the multi-token
- * branches of OP_GEMV_Q8 and OP_GEMV_Q6K, ie_gemv_q8q8_t / _tr and
- * ie_gemv_q6kq8_tr / _tr8 / _ts2, src/hip.c:934-962, 1027-1089). */
+/* Q8_0 / Q6_K over T vectors: the same int8-MFMA verify kernels (the
+ * multi-token branches of OP_GEMV_Q8 and OP_GEMV_Q6K, ie_gemv_q8q8_t / _tr
+ * and ie_gemv_q6kq8_tr / _tr8 / _ts2, src/hip.c:934-962, 1027-1089). */
 int amdc_gemv_q8_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
                    uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 int amdc_gemv_q6k_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
