@@ -201,6 +201,7 @@ static struct {
   hipError_t (*ModuleLoad)(hipModule_t *, const char *);
   hipError_t (*ModuleUnload)(hipModule_t);
   hipError_t (*ModuleGetFunction)(hipFunction_t *, hipModule_t, const char *);
+  hipError_t (*ModuleGetGlobal)(void **, size_t *, hipModule_t, const char *);
   hipError_t (*ModuleLaunchKernel)(hipFunction_t, unsigned, unsigned, unsigned, unsigned, unsigned, unsigned, unsigned, hipStream_t,
                                    void **, void **);
   hipError_t (*Malloc)(void **, size_t);
@@ -296,6 +297,13 @@ static void *g_ws;
 static size_t g_ws_bytes;
 static void *g_ws_old[48];
 static unsigned g_ws_old_n;
+/* The code object's fixed workspace, the device array `scratch` of amdc_kernels.hip: its device
+ * address and size, looked up once at amdc_open (the library drives device 0 only). Inside
+ * amdc_op_gemv_noalloc (g_ws_fixed set) every workspace request is served from it, and a request
+ * larger than it is an error; otherwise it is unused. */
+static void *g_scratch;
+static size_t g_scratch_bytes;
+static int g_ws_fixed;
 
 #define HIPCALL(x)                                                                               \
   do {                                                                                           \
@@ -328,6 +336,7 @@ static int hip_load(void) {
   SYM(ModuleLoad, "hipModuleLoad");
   SYM(ModuleUnload, "hipModuleUnload");
   SYM(ModuleGetFunction, "hipModuleGetFunction");
+  SYM(ModuleGetGlobal, "hipModuleGetGlobal");
   SYM(ModuleLaunchKernel, "hipModuleLaunchKernel");
   SYM(Malloc, "hipMalloc");
   SYM(Free, "hipFree");
@@ -378,6 +387,11 @@ int amdc_open(const char *hsaco) {
   }
   HIPCALL(H.ModuleLoad(&g_mod, hsaco));
   for (int k = 0; k < K_N; k++) HIPCALL(H.ModuleGetFunction(&g_k[k], g_mod, kname[k]));
+  /* the module-API lookup of a device variable (hipGetSymbolAddress of a code object loaded with
+     hipModuleLoad); with device 0 current. Host code uses this address, never the name. */
+  HIPCALL(H.ModuleGetGlobal(&g_scratch, &g_scratch_bytes, g_mod, "scratch"));
+  if (!g_scratch || g_scratch_bytes < AMDC_SCRATCH_BYTES)
+    return fail(AMDC_EHIP, "amdc_kernels.hsaco: scratch array of %zu bytes, expected %zu", g_scratch_bytes, (size_t)AMDC_SCRATCH_BYTES);
   HIPCALL(H.DeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, 0));
   if (t_lanes < 0) t_lanes = envi("AMDC_GEMV_L", 0);
   if (t_unroll < 0) t_unroll = envi("AMDC_GEMV_U", 0);
@@ -400,6 +414,7 @@ void amdc_close(void) {
   if (g_open && g_ws) H.Free(g_ws);
   for (unsigned i = 0; g_open && i < g_ws_old_n; i++) H.Free(g_ws_old[i]);
   g_ws = NULL, g_ws_bytes = 0, g_ws_old_n = 0;
+  g_scratch = NULL, g_scratch_bytes = 0;
   if (g_open && g_mod) H.ModuleUnload(g_mod);
   g_mod = NULL;
   g_open = 0;
@@ -611,7 +626,7 @@ static u32 gemv2_lanes(u32 ng, u32 rows, int k8) {
 /* LDS of the GEMV: 320 bytes per super-group and vector (amdc_kernels.hip). */
 #define GEMV_LDS_T1 (150u * 1024u)
 
-static int ws_reserve(size_t n);
+static int ws_take(size_t n, void **p);
 
 /* The verify GEMV on int8 MFMA (T <= 16): 64 rows per workgroup, K split
  * over aligned ranges of tiles (64 blocks each) until the workgroups fill the
@@ -633,9 +648,8 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
   const u32 ks = (nt + tps - 1u) / tps;
   float *part = NULL;
   if (ks > 1u) {
-    int rc = ws_reserve((size_t)ks * T * rows * 4u);
+    int rc = ws_take((size_t)ks * T * rows * 4u, (void **)&part);
     if (rc) return rc;
-    part = g_ws;
   }
   void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs, &part, &tps};
   const int v16 = T > 8u; /* the 16-vector form */
@@ -774,8 +788,7 @@ static int gemv_x(int kind, const char *op, const void *w, const float *x, float
   const u32 ng = amdc_ngroups(nb), L = gemv_lanes(ng), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
   if (nb > x_fuse_nb || 320u * ng > GEMV_LDS_T1 || kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) {
     if (!q8) {
-      if ((rc = ws_reserve((size_t)40u * nb + 64u))) return rc;
-      q8 = (uint8_t *)g_ws;
+      if ((rc = ws_take((size_t)40u * nb + 64u, (void **)&q8))) return rc;
     }
     if ((rc = amdc_quant_q8(x, q8, nb, 1u, 0u, 0u, stream))) return rc;
     return gemv_t(kind, op, w, q8, y, rows, nb, bias, res, 1u, 0u, 0u, 0u, stream);
@@ -859,6 +872,22 @@ static int ws_reserve(size_t n) {
   return AMDC_OK;
 }
 
+/* The workspace of an operator: n bytes at *p, from the grown allocation, or from the fixed
+ * scratch array inside amdc_op_gemv_noalloc. Every caller asks before its first launch, so a
+ * rejected request launches nothing. No operator needs its workspace to start at zero. */
+static int ws_take(size_t n, void **p) {
+  if (g_ws_fixed) {
+    if (n > g_scratch_bytes)
+      return fail(AMDC_EINVAL, "op_gemv_noalloc: needs %zu bytes of workspace, the scratch array holds %zu (%u MiB)", n, g_scratch_bytes,
+                  (unsigned)(AMDC_SCRATCH_BYTES >> 20));
+    *p = g_scratch;
+    return AMDC_OK;
+  }
+  int rc = ws_reserve(n);
+  if (!rc) *p = g_ws;
+  return rc;
+}
+
 /* The f16-MFMA GEMM kernels: rows x tokens per workgroup. */
 static const struct {
   int k;
@@ -898,9 +927,9 @@ static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *x
   if (ks > 16u) ks = 16u; /* amdc_gemm_reduce adds at most 16 splits */
   const u32 Tp = (T + 127u) / 128u * 128u, K = 32u * nb;
   const size_t xh_b = (size_t)Tp * K * 2u, sc_b = (size_t)nb * Tp * 4u, part_b = ks > 1u ? (size_t)ks * T * rows * 4u : 0u;
-  rc = ws_reserve(xh_b + 2u * sc_b + part_b);
+  uint8_t *ws = NULL;
+  rc = ws_take(xh_b + 2u * sc_b + part_b, (void **)&ws);
   if (rc) return rc;
-  uint8_t *ws = g_ws;
   void *xh = ws, *da = ws + xh_b, *xa = ws + xh_b + sc_b, *part = ks > 1u ? (void *)(ws + xh_b + 2u * sc_b) : NULL;
   const u64 np = (u64)nb * Tp;
   void *pa[] = {&xq, &nb, &T, &xs, &xh, &da, &xa, (void *)&Tp};
@@ -964,6 +993,15 @@ int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t 
   }
   if (use_gemm(T, rows, nb)) return gemm_launch(kind, "op_gemv", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
   return gemv_t(kind, "op_gemv", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+}
+
+int amdc_op_gemv_noalloc(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
+                         const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
+  NEED_OPEN();
+  g_ws_fixed = 1;
+  const int rc = amdc_op_gemv(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+  g_ws_fixed = 0;
+  return rc;
 }
 
 int amdc_block_dots(int kind, const void *w, const uint8_t *xq, int32_t *out, uint32_t rows, uint32_t nb, void *stream) {

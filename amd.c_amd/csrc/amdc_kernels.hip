@@ -38,6 +38,14 @@
 
 #include "amdc_layout.h"
 
+// The fixed workspace of amdc_op_gemv_noalloc (AMDC_SCRATCH_BYTES): split-K partial sums and
+// the GEMM's prepared activations, for callers that cannot allocate device memory. Every
+// device that loads this code object holds one copy until the module is unloaded. No kernel
+// names it: the host looks its address up once (hipModuleGetGlobal, with the device current)
+// and passes that address as the workspace argument, as it passes an allocated workspace.
+// Not static, so that the code object exports the symbol for that lookup.
+__device__ __align__(256) unsigned char scratch[AMDC_SCRATCH_BYTES];
+
 typedef uint32_t u32;
 typedef uint64_t u64;
 typedef int v4i __attribute__((ext_vector_type(4)));

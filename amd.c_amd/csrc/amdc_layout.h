@@ -62,6 +62,10 @@
 
 enum { AMDC_Q4_0 = 0, AMDC_Q8_0 = 2, AMDC_Q4_K = 3, AMDC_Q6_K = 4 }; /* the reference's MAT_* (src/model.h:15) */
 
+/* The size of the kernels' fixed workspace (the device array `scratch`); the same definition as
+ * in include/amdc_q4.h, where the host reads it. */
+#define AMDC_SCRATCH_BYTES ((size_t)64 << 20)
+
 AMDC_INLINE uint32_t amdc_ngroups(uint32_t nb) { return (nb + 7u) >> 3; }
 AMDC_INLINE uint64_t amdc_row_bytes(uint32_t nb) { return 144ull * amdc_ngroups(nb); }
 AMDC_INLINE uint64_t amdc_header_off(uint32_t g) { return 16ull * g; }

@@ -22,7 +22,8 @@
  * that use the library's device workspace (the GEMMs, the split-K multi-vector
  * GEMV, amdc_gemv_*_x with q8 NULL above the fused size) share it: work of
  * theirs queued on different streams, or in graphs replayed on them, must be
- * ordered (one stream, or an event between), or their results race. */
+ * ordered (one stream, or an event between), or their results race. The same
+ * holds for amdc_op_gemv_noalloc and its fixed workspace. */
 #ifndef AMDC_Q4_H
 #define AMDC_Q4_H
 
@@ -228,6 +229,20 @@ int amdc_gemm_q6k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uin
  * for T >= 20 on matrices of at most 2^24 weights. kind: any AMDC_KIND_*. */
 int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                  const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
+
+/* amdc_op_gemv without any device allocation, for callers that cannot allocate (code under
+ * HIP graph capture on a workspace size not seen before, tight serving loops, hosts that
+ * forbid hipMalloc). No reference counterpart. The same kernels and launch choices as
+ * amdc_op_gemv, so the same bits; the workspace (split-K partial sums, the GEMM's prepared
+ * activations) is a fixed device array of AMDC_SCRATCH_BYTES in the code object, held by the
+ * device from amdc_open until amdc_close. A call whose workspace would exceed it fails with
+ * AMDC_EINVAL before any launch (e.g. T = 256 prefill chunks fit up to about 17408 x 5120
+ * and 5120 x 17408 matrices). All calls share the one array: calls that overlap on the
+ * device (other streams, graphs replayed concurrently) race; order them. Its contents are
+ * whatever the last call left; no kernel needs it cleared. */
+#define AMDC_SCRATCH_BYTES ((size_t)64 << 20)
+int amdc_op_gemv_noalloc(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
+                         const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream);
 
 /* Parity probe: out[r * nb + b] = the int32 dot product of block b of row r
  * with Q8 block b, as the GEMV kernels compute it: sum (q - 8) a for Q4_0
