@@ -1052,6 +1052,30 @@ typedef struct {
 #define CHAIN_SPIN_NS 200000000u
 #define CHAIN_SYNC_BYTES (35u * 128u) /* the kernel's NGRP + 3 lines */
 
+/* A byte range [lo, hi) of device memory. */
+typedef struct {
+  uintptr_t lo, hi;
+} span;
+static span span_of(const void *p, u64 n) {
+  span r = {(uintptr_t)p, (uintptr_t)p + (p ? (uintptr_t)n : 0u)};
+  return r;
+}
+static int spans_meet(span a, span b) { return a.lo < a.hi && b.lo < b.hi && a.lo < b.hi && b.lo < a.hi; }
+/* The bytes a (validated) chain operation writes (*w) and reads (r, returns how many ranges). */
+static unsigned chain_spans(const chain_dev_op *e, const amdc_chain_op *o, span *w, span r[4]) {
+  if (e->type == 0u) { /* quantize: 32 nb floats -> 40 nb Q8 bytes */
+    *w = span_of(o->q, 40ull * o->nb);
+    r[0] = span_of(o->x, 128ull * o->nb);
+    return 1;
+  }
+  *w = span_of(o->y, 4ull * o->rows);
+  r[0] = o->type == AMDC_CHAIN_GEMV_X ? span_of(o->x, 128ull * o->nb) : span_of(o->xq, 40ull * o->nb);
+  r[1] = span_of(o->w, (u64)o->rows * amdc_row_bytes_k(o->kind, o->nb));
+  r[2] = span_of(o->bias, 4ull * o->rows);
+  r[3] = span_of(o->res, 4ull * o->rows);
+  return 4;
+}
+
 int amdc_chain_create(const amdc_chain_op *ops, uint32_t n, void **chain) {
   NEED_OPEN();
   if (!ops || !n || !chain) return fail(AMDC_EINVAL, "chain_create: null pointer or empty list");
@@ -1087,12 +1111,15 @@ int amdc_chain_create(const amdc_chain_op *ops, uint32_t n, void **chain) {
     } else {
       rc = fail(AMDC_EINVAL, "chain op %u: type %d", k, o->type);
     }
-    /* a read of a buffer written earlier in the same segment (no sync between) */
+    /* two operations of one segment (no sync between) run concurrently: neither may write bytes
+       the other reads or writes */
     for (u32 j = seg0; j < k && !rc; j++) {
-      const void *wj = d[j].type == 0u ? d[j].b : (const void *)d[j].y;
-      const void *r1 = e->type == 0u ? e->a : e->b;
-      if (wj == r1 || (e->type && (wj == (const void *)e->bias || wj == (const void *)e->res)))
-        rc = fail(AMDC_EINVAL, "chain op %u reads what op %u writes without a sync between them", k, j);
+      span wk, wj, rk[4], rj[4];
+      const unsigned nk = chain_spans(&d[k], &ops[k], &wk, rk), nj = chain_spans(&d[j], &ops[j], &wj, rj);
+      int clash = spans_meet(wk, wj);
+      for (unsigned i = 0; i < nk; i++) clash |= spans_meet(rk[i], wj);
+      for (unsigned i = 0; i < nj; i++) clash |= spans_meet(rj[i], wk);
+      if (clash) rc = fail(AMDC_EINVAL, "chain op %u and op %u share bytes one of them writes, without a sync between them", k, j);
     }
     if (o->sync) seg0 = k + 1u;
   }

@@ -280,8 +280,9 @@ int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kern
  *   AMDC_CHAIN_GEMV_X: Q4_0 / Q4_K on x (32 nb floats): every workgroup
  *                     quantizes x into its LDS (as amdc_gemv_q4_x, no Q8
  *                     buffer, no barrier between quantization and GEMV)
- * An operation that reads what an earlier one writes must come after a sync
- * (the check compares buffer pointers). All workgroups must be resident at
+ * Operations between two syncs run concurrently: when one writes bytes that
+ * another reads or writes, the later one must come after a sync (the check
+ * compares the byte ranges of every operand). All workgroups must be resident at
  * once: the grid is what the device holds (at most 2 per CU); nothing else
  * should run on the device meanwhile. A barrier that waits longer than 200 ms
  * aborts the launch (every workgroup leaves); amdc_chain_check reports it. */

@@ -92,6 +92,16 @@ def test_chain_rejects_read_before_sync(dev, orc):
     x0, q0, y = dev.DevBuf.of(A.x[0]), dev.DevBuf(q8_stride(8)), dev.DevBuf(4 * 64)
     with pytest.raises(dev.AmdcError, match="without a sync"):
         dev.Chain([dev.chain_quant(x0, q0, 8, sync=False), dev.chain_gemv(0, A.W, q0, y, 64, 8)])
+    # overlapping byte ranges, not only equal pointers: the GEMV's input starts inside the Q8 bytes being written
+    Qb = dev.DevBuf(2 * q8_stride(8))
+    with pytest.raises(dev.AmdcError, match="without a sync"):
+        dev.Chain([dev.chain_quant(x0, Qb, 8, sync=False), dev.chain_gemv(0, A.W, Qb.ptr + 256, y, 64, 8)])
+    # a write after a read in one segment (the GEMV may still read q0 while the quantization overwrites it)
+    with pytest.raises(dev.AmdcError, match="without a sync"):
+        dev.Chain([dev.chain_gemv(0, A.W, q0, y, 64, 8, sync=False), dev.chain_quant(x0, q0, 8)])
+    # disjoint ranges of one buffer in one segment are accepted
+    ch = dev.Chain([dev.chain_quant(x0, Qb, 8, sync=False), dev.chain_gemv(0, A.W, Qb.ptr + q8_stride(8), y, 64, 8)])
+    del ch
     with pytest.raises(dev.AmdcError, match="type"):
         op = dev.chain_quant(x0, q0, 8)
         op.type = 7
