@@ -111,6 +111,7 @@ ABI = {
     "amdc_gemv_q4k_t": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_gemm_q4k": (C.c_int, [_P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_op_gemv": (C.c_int, [C.c_int, _P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
+    "amdc_last_kernel": (C.c_char_p, []),
     "amdc_op_gemv_noalloc": (C.c_int, [C.c_int, _P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_block_dots": (C.c_int, [C.c_int, _P, _P, _P, _U32, _U32, _P]),
     "amdc_set_tuning": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
@@ -404,7 +405,12 @@ def op_gemv_noalloc(kind, w, xq, y, rows, nb, T, xs, ys, rs=0, bias=None, res=No
     _check(lib().amdc_op_gemv_noalloc(kind, _p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), T, xs, ys, rs, stream))
 
 
-SCRATCH_BYTES = 64 << 20  # AMDC_SCRATCH_BYTES of include/amdc_q4.h
+SCRATCH_BYTES = 64 << 20
+
+
+def last_kernel():
+    """The kernel the library launched last."""
+    return lib().amdc_last_kernel().decode()  # AMDC_SCRATCH_BYTES of include/amdc_q4.h
 
 
 def block_dots(kind, w, xq, out, rows, nb, stream=None):

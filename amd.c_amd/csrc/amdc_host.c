@@ -271,7 +271,9 @@ enum {
   K_GEMV_Q4K_V16,
   K_GEMV_Q8_V16,
   K_GEMV_Q6K_V16,
-  K_N
+  K_GEMVS_Q4, /* amdc_gemv_q4_0_s1 .. _s4, then amdc_gemv_q4_k_s1 .. _s4 */
+  K_GEMVXS_Q4 = K_GEMVS_Q4 + 8, /* amdc_gemv_q4_0_xs1 .. _xs4, then amdc_gemv_q4_k_xs1 .. _xs4 */
+  K_N = K_GEMVXS_Q4 + 8
 };
 static const char *const kname[K_N] = {
     "amdc_quant_q8",           "amdc_dots_q4_0",          "amdc_dots_q4_k",          "amdc_gemm_q4_k_n128",
@@ -283,7 +285,11 @@ static const char *const kname[K_N] = {
     "amdc_dots_q8_0",          "amdc_dots_q6_k",          "amdc_gemmh_q8_0_m64_n128", "amdc_gemmh_q8_0_m64_n64",
     "amdc_gemmh_q6_k_m64_n128", "amdc_gemmh_q6_k_m64_n64", "amdc_gemv_q8_0_v8",       "amdc_gemv_q6_k_v8",
     "amdc_gemmh_q4_0_m64_n128", "amdc_gemmh_q4_0_m64_n64", "amdc_gemv_q4_0_v16",      "amdc_gemv_q4_k_v16",
-    "amdc_gemv_q8_0_v16",      "amdc_gemv_q6_k_v16"};
+    "amdc_gemv_q8_0_v16",      "amdc_gemv_q6_k_v16",
+    "amdc_gemv_q4_0_s1",       "amdc_gemv_q4_0_s2",       "amdc_gemv_q4_0_s3",       "amdc_gemv_q4_0_s4",
+    "amdc_gemv_q4_k_s1",       "amdc_gemv_q4_k_s2",       "amdc_gemv_q4_k_s3",       "amdc_gemv_q4_k_s4",
+    "amdc_gemv_q4_0_xs1",      "amdc_gemv_q4_0_xs2",      "amdc_gemv_q4_0_xs3",      "amdc_gemv_q4_0_xs4",
+    "amdc_gemv_q4_k_xs1",      "amdc_gemv_q4_k_xs2",      "amdc_gemv_q4_k_xs3",      "amdc_gemv_q4_k_xs4"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -429,7 +435,7 @@ int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kern
   if (gemm_kernel < 0 || gemm_kernel > 4) return fail(AMDC_EINVAL, "gemm kernel %d: 0..4", gemm_kernel);
   if (gemm_ksplit < 0 || gemm_ksplit > 16) return fail(AMDC_EINVAL, "gemm ksplit %d: 0..16", gemm_ksplit);
   if (gemv_wgs < 0) return fail(AMDC_EINVAL, "gemv workgroups %d", gemv_wgs);
-  if (gemv_form < 0 || gemv_form > 2) return fail(AMDC_EINVAL, "gemv form %d: 0, 1 or 2", gemv_form);
+  if (gemv_form < 0 || gemv_form > 3) return fail(AMDC_EINVAL, "gemv form %d: 0..3", gemv_form);
   t_lanes = gemv_lanes, t_unroll = gemv_unroll, t_wgs = gemv_wgs, t_gemm = gemm_kernel, t_ksplit = gemm_ksplit, t_form = gemv_form;
   return AMDC_OK;
 }
@@ -542,10 +548,14 @@ int amdc_graph_destroy(void *exec) {
 
 /* ---------------------------------------------------------------- launches */
 
+static int g_last_k = -1; /* the kernel of the last launch (amdc_last_kernel) */
 static int launch(int k, unsigned gx, unsigned gy, unsigned lds, void *stream, void **args) {
+  g_last_k = k;
   HIPCALL(H.ModuleLaunchKernel(g_k[k], gx, gy, 1, 256, 1, 1, lds, stream, args, NULL));
   return AMDC_OK;
 }
+
+const char *amdc_last_kernel(void) { return g_last_k >= 0 ? kname[g_last_k] : ""; }
 
 static int aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -657,6 +667,7 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
                 : kind == AMDC_KIND_Q4_K ? (v16 ? K_GEMV_Q4K_V16 : K_GEMV_Q4K_V8)
                 : kind == AMDC_KIND_Q8_0 ? (v16 ? K_GEMV_Q8_V16 : K_GEMV_Q8_V8)
                                          : (v16 ? K_GEMV_Q4_V16 : K_GEMV_Q4_V8);
+  g_last_k = k;
   HIPCALL(H.ModuleLaunchKernel(g_k[k], wgs, ks, 1, 256, 1, 1, 0, stream, args, NULL));
   if (ks > 1u) {
     const u64 n = (u64)rows * T;
@@ -693,6 +704,38 @@ static int gemv_k8_launch(int kind, const void *w, const uint8_t *xq, float *y, 
   return AMDC_OK;
 }
 
+/* Lanes per row of the single-shot decode kernels: the tuning value, else the smallest power of
+ * two (4..64) >= the super-groups of a row (one per lane, up to 4 for rows of more than 64).
+ * With the quantization in every workgroup (fq), while the grid is over 3 workgroups per CU,
+ * half the lanes (two super-groups per lane, half the workgroups: half the quantizations).
+ * Measured on MI355X (us, Q8 vector / f32 vector): 22016 x 4096 Q4_0 10.3 / 11.8 (12.5 at 16
+ * lanes), 32000 x 4096 13.3 / 15.4; 4096 x 11008 8.1 (64 lanes); 152064 x 5120 Q4_K 72-75. */
+static u32 gemvs_lanes(u32 ng, u32 rows, int fq) {
+  if (t_lanes > 0) return lanes_fit((u32)t_lanes, ng);
+  u32 L = 4u;
+  while (L < 64u && L < ng) L <<= 1;
+  const u32 cus = g_cus > 0 ? (u32)g_cus : 256u;
+  if (fq && L > 4u && (rows + 4u * (64u / L) - 1u) / (4u * (64u / L)) > 3u * cus && (ng + L / 2u - 1u) / (L / 2u) <= 4u) L >>= 1;
+  return L;
+}
+
+/* The single-shot decode GEMV (amdc_gemv_*_s<NI>; with x: _xs<NI>, the quantization in every
+ * workgroup): one row group per workgroup, NI = ceil(ng / L) super-groups per lane, all loaded at
+ * once. */
+static int gemvs_launch(int kind, const void *w, const void *in, int fq, float *y, uint32_t rows, uint32_t nb, const float *bias,
+                        const float *res, uint8_t *q8, void *stream) {
+  const u32 ng = amdc_ngroups(nb), L = gemvs_lanes(ng, rows, fq), ni = (ng + L - 1u) / L;
+  const u32 rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
+  if (ni > 4u) return fail(AMDC_EINVAL, "gemv: %u super-groups on %u lanes (at most 4 per lane)", ng, L);
+  const int k = (fq ? K_GEMVXS_Q4 : K_GEMVS_Q4) + (kind == AMDC_KIND_Q4_K ? 4 : 0) + (int)ni - 1;
+  if (fq) {
+    void *a[] = {&w, &in, &y, &rows, &nb, &bias, &res, (void *)&L, &q8};
+    return launch(k, nrg, 1, 320u * ng, stream, a);
+  }
+  void *a[] = {&w, &in, &y, &rows, &nb, &bias, &res, (void *)&L};
+  return launch(k, nrg, 1, 320u * ng, stream, a);
+}
+
 static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                        const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
   if (kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) {
@@ -717,7 +760,9 @@ static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uin
     return AMDC_OK;
   }
   const u32 ng = amdc_ngroups(nb), L = gemv_lanes(ng), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
-  const int form = t_form > 0 ? t_form : ng > 32u ? 2 : 1;
+  /* the single-shot kernels (form 3) by default: up to 256 super-groups per row */
+  const int form = t_form > 0 ? t_form : ng <= 256u ? 3 : 2;
+  if (form == 3) return gemvs_launch(kind, w, xq, 0, y, rows, nb, bias, res, NULL, stream);
   if (form == 2 && (u64)rows * 144u * ng + 144u * ng < (1ull << 32)) {
     /* the decode kernel with buffer loads (32-bit offsets: matrices under 4 GiB), for long rows: up
        to 3 super-groups per lane (it keeps the next one in flight), at most 2 workgroups per CU; LDS
@@ -776,9 +821,9 @@ static int gemv_t(int kind, const char *op, const void *w, const uint8_t *xq, fl
  * one launch whose workgroups quantize the vector in their prologue (the
  * quantization then hides under the weight loads); for larger nb, where that
  * prologue costs more than a launch, amdc_quant_q8 into q8 (or the library's
- * workspace when q8 is NULL) and the GEMV. Measured on MI355X: 4096 x 4096
- * Q4_0 4.9 us fused against 6.3 us for the two launches, 4096 x 11008 14.4
- * against 11.7. */
+ * workspace when q8 is NULL) and the GEMV. Measured on MI355X (single-shot
+ * kernels): 4096 x 4096 Q4_0 4.5 us fused against 6.0 us for the two
+ * launches, 12288 x 4096 7.9 against 8.8, 22016 x 4096 11.8 against 12.2. */
 static int gemv_x(int kind, const char *op, const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias,
                   const float *res, uint8_t *q8, void *stream) {
   NEED_OPEN();
@@ -793,6 +838,7 @@ static int gemv_x(int kind, const char *op, const void *w, const float *x, float
     if ((rc = amdc_quant_q8(x, q8, nb, 1u, 0u, 0u, stream))) return rc;
     return gemv_t(kind, op, w, q8, y, rows, nb, bias, res, 1u, 0u, 0u, 0u, stream);
   }
+  if (t_form == 0 || t_form == 3) return gemvs_launch(kind, w, x, 1, y, rows, nb, bias, res, q8, stream);
   /* every workgroup quantizes the whole vector first: a persistent grid of at most 3 workgroups
      per CU (each loops over row groups) pays that once per slot */
   const u32 cap = 3u * (g_cus > 0 ? (u32)g_cus : 256u);
@@ -942,6 +988,7 @@ static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *x
                  : kind == AMDC_KIND_Q6_K ? (v ? K_GEMMH_Q6K_N64 : K_GEMMH_Q6K_N128)
                  : kind == AMDC_KIND_Q4_0 ? (v ? K_GEMMH_Q4_N64 : K_GEMMH_Q4_N128)
                                           : gh[v].k;
+  g_last_k = kk;
   HIPCALL(H.ModuleLaunchKernel(g_k[kk], (unsigned)grid, ks, 1, gh[v].threads, 1, 1, 0, stream, ga, NULL));
   if (ks > 1u) {
     const u64 n = (u64)rows * T;

@@ -376,13 +376,14 @@ __device__ __forceinline__ float item_dot(const typename ItemOf<KIND>::type &it,
 // unconditional (a block past nb reads the last block again and takes zeros),
 // so that no branch joins them. The max and the sum of a block's 8 lanes go
 // by DPP (xor 1, xor 2, then the half-row mirror).
-template <u32 NC> struct FusedQ8T {
+template <u32 NC, u32 NTH = NT> struct FusedQ8T {
+  static constexpr u32 BP = NTH / 8u; // blocks per pass
   v4f xv[NC];
   __device__ __forceinline__ void load(const float *__restrict__ xf, u32 nb, u32 b0) {
     const u32 tid = threadIdx.x, e = tid & 7u;
 #pragma unroll
     for (u32 c = 0; c < NC; c++) {
-      const u32 b = b0 + 32u * c + (tid >> 3);
+      const u32 b = b0 + BP * c + (tid >> 3);
       const v4f v = *(const v4f *)(xf + 32u * (b < nb ? b : nb - 1u) + 4u * e);
       xv[c] = b < nb ? v : (v4f){0.0f, 0.0f, 0.0f, 0.0f};
     }
@@ -391,8 +392,8 @@ template <u32 NC> struct FusedQ8T {
     const u32 tid = threadIdx.x, e = tid & 7u, nblk = 8u * ng;
 #pragma unroll
     for (u32 c = 0; c < NC; c++) {
-      if (b0 + 32u * c >= nblk) break;
-      const u32 b = b0 + 32u * c + (tid >> 3);
+      if (b0 + BP * c >= nblk) break;
+      const u32 b = b0 + BP * c + (tid >> 3);
       float a = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(xv[c].x), __builtin_fabsf(xv[c].y)),
                                 __builtin_fmaxf(__builtin_fabsf(xv[c].z), __builtin_fabsf(xv[c].w)));
       a = __builtin_fmaxf(a, dpp<0xB1>(a));
@@ -512,6 +513,97 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_x1(const uint8_
                                                                    const float *bias, const float *res, u32 L, uint8_t *q8) {
   gemv1_body<AMDC_Q4_K, true>(W, nullptr, y, rows, nb, bias, res, L, x, q8);
 }
+
+// The decode GEMV, single-shot form (amdc_gemv_*_s{1,2,3,4}, _xs{1,2,3,4}):
+// one row group per workgroup (grid = the row groups), and each lane issues
+// the loads of all NI = ceil(ng / L) of its super-groups at once, before the
+// activations are staged (or quantized: _xs), so that no load waits for
+// another's arithmetic and no register carries an item across a loop. Without
+// the second item buffer and the loop the kernel needs far fewer registers
+// (64 to 80 VGPRs at NI = 1: 6 to 8 waves per SIMD), so that the workgroups
+// of a whole matrix are resident at once and the arithmetic of one overlaps
+// the loads of the others. Lane split, LDS layout, block arithmetic and
+// summation order are those of gemv1_body (bit-equal results).
+template <int KIND, u32 NI, bool FQ, u32 NTH>
+__device__ __forceinline__ void gemvs_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
+                                           u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 L,
+                                           const float *__restrict__ xf = nullptr, uint8_t *__restrict__ q8out = nullptr) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const u32 ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = (NTH / 64u) * rpw;
+  const u64 RB = amdc_row_bytes(nb);
+  const u32 nblk = 8u * ng;
+  u32x4 *s_lo = (u32x4 *)smem;
+  u32x4 *s_hi = s_lo + nblk;
+  float *s_d = (float *)(s_hi + nblk);
+  u32 *s_as = (u32 *)(s_d + nblk);
+  const u32 r = blockIdx.x * rpg + wv * rpw + q;
+  const uint8_t *wr = W + (u64)(r < rows ? r : rows - 1u) * RB;
+  constexpr u32 QC = (QCH * NT) / NTH; // passes in flight: 128 blocks
+  FusedQ8T<QC, NTH> fq;
+  if (FQ) {
+    fq.load(xf, nb, 0);
+    __asm__ volatile("" ::: "memory"); // the activation loads ahead of the weight loads
+  }
+  Item it[NI];
+#pragma unroll
+  for (u32 i = 0; i < NI; i++) load_item<KIND>(it[i], wr, ng, l + L * i, l + L * i < ng);
+  if (FQ) {
+    fq.quant(0, nb, ng, s_lo, s_hi, s_d, s_as, q8out);
+    for (u32 b0 = fq.BP * QC; b0 < nblk; b0 += fq.BP * QC) {
+      fq.load(xf, nb, b0);
+      fq.quant(b0, nb, ng, s_lo, s_hi, s_d, s_as, q8out);
+    }
+  } else {
+    for (u32 j = tid; j < nblk; j += NTH) { // stage the whole Q8 vector (permuted)
+      const u32 p = (j & 7u) * ng + (j >> 3);
+      u32x4 lo = (u32x4)(0u), hi = (u32x4)(0u);
+      float d = 0.0f;
+      u32 as = 0;
+      if (j < nb) {
+        lo = *(const u32x4 *)(xq + 32u * j);
+        hi = *(const u32x4 *)(xq + 32u * j + 16u);
+        d = ((const float *)(xq + 32u * nb))[j];
+        as = ((const u32 *)(xq + 36u * nb))[j];
+      }
+      s_lo[p] = lo, s_hi[p] = hi, s_d[p] = d, s_as[p] = as;
+    }
+  }
+  __syncthreads();
+  ItemTree tr;
+#pragma unroll
+  for (u32 i = 0; i < NI; i++) {
+    const u32 g = l + L * i;
+    const float leaf = item_dot<KIND>(it[i], g < ng ? g : 0u, ng, s_lo, s_hi, s_d, s_as, 0.0f);
+    tr.add(seg_sum(g < ng ? leaf : 0.0f, L), i);
+  }
+  const float v = tr.sum(NI);
+  if (l == 0u && r < rows) {
+    float o = v;
+    if (bias) o = o + bias[r];
+    if (res) o = res[r] + o;
+    y[r] = o;
+  }
+}
+
+#define GEMVS_KERNELS(KN, KIND, NI, TAG, NTH)                                                                                            \
+  extern "C" __global__ __launch_bounds__(NTH) void amdc_gemv_##KN##_##TAG##NI(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, \
+                                                                               u32 nb, const float *bias, const float *res, u32 L) {  \
+    gemvs_body<KIND, NI, false, NTH>(W, xq, y, rows, nb, bias, res, L);                                                                 \
+  }                                                                                                                                      \
+  extern "C" __global__ __launch_bounds__(NTH) void amdc_gemv_##KN##_x##TAG##NI(const uint8_t *W, const float *x, float *y, u32 rows,  \
+                                                                                u32 nb, const float *bias, const float *res, u32 L,   \
+                                                                                uint8_t *q8) {                                        \
+    gemvs_body<KIND, NI, true, NTH>(W, nullptr, y, rows, nb, bias, res, L, x, q8);                                                      \
+  }
+GEMVS_KERNELS(q4_0, AMDC_Q4_0, 1, s, 256)
+GEMVS_KERNELS(q4_0, AMDC_Q4_0, 2, s, 256)
+GEMVS_KERNELS(q4_0, AMDC_Q4_0, 3, s, 256)
+GEMVS_KERNELS(q4_0, AMDC_Q4_0, 4, s, 256)
+GEMVS_KERNELS(q4_k, AMDC_Q4_K, 1, s, 256)
+GEMVS_KERNELS(q4_k, AMDC_Q4_K, 2, s, 256)
+GEMVS_KERNELS(q4_k, AMDC_Q4_K, 3, s, 256)
+GEMVS_KERNELS(q4_k, AMDC_Q4_K, 4, s, 256)
 
 // The decode GEMV, second form: the same lane split, LDS layout and
 // per-block arithmetic as gemv1_body, with the weights read through a buffer

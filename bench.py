@@ -19,7 +19,8 @@ their stream. roofline describes the step's own launches: each launch of the
 step (the same call, the same kernel) timed alone by HIP events on the
 stream it runs on, in a graph of that launch repeated over the weight
 copies; "achieved" is the algorithmic bytes over the summed durations of the
-step's dominant kernel (amdc_gemv_q4_0_x1, 4 of its 6 launches), and
+step's dominant kernel (the one with the largest share of the step's time,
+named by the library, amdc_last_kernel), and
 "traffic" the HBM bytes per launch of that kernel read live from rocprofv3
 FETCH_SIZE / WRITE_SIZE counter passes over the same launches (a child
 process under rocprofv3, one pass per counter), scaled by what the counters
@@ -216,16 +217,20 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
     for gi, (name, r, c, _) in enumerate(groups):
         nb, b = c // 32, wbytes(r, c, kind)
         if nb <= 128:
+            amdc.gemv_x(kind, G.dev[0][gi], X, Y, r, nb)
+            kname = amdc.last_kernel()  # the kernel the library picked for this shape
             t = timer.per_launch_ms(lambda j, s, gi=gi, r=r, nb=nb: amdc.gemv_x(kind, G.dev[j % G.copies][gi], X, Y, r, nb, stream=s),
                                     G.copies, reps=max(2, steps // 4))
-            launches.append(launch_rec(name, decode_kernel(kind, nb, True), r, c, b, t))
+            launches.append(launch_rec(name, kname, r, c, b, t))
         else:
             tq = timer.per_launch_ms(lambda j, s, nb=nb: amdc.quant_q8(X, Q, nb, stream=s), 64)
             launches.append(launch_rec(name + " (input)", "amdc_quant_q8", 1, c, 0, tq))
             amdc.quant_q8(X, Q, nb)
+            amdc.gemv(kind, G.dev[0][gi], Q, Y, r, nb)
+            kname = amdc.last_kernel()
             t = timer.per_launch_ms(lambda j, s, gi=gi, r=r, nb=nb: amdc.gemv(kind, G.dev[j % G.copies][gi], Q, Y, r, nb, stream=s),
                                     G.copies, reps=max(2, steps // 4))
-            launches.append(launch_rec(name, decode_kernel(kind, nb, False), r, c, b, t))
+            launches.append(launch_rec(name, kname, r, c, b, t))
     set_bytes = G.set_bytes
     del G
     kt = {}
@@ -245,14 +250,6 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
             "dominant_GBps": kt[dom][1] / kt[dom][0] / 1e3,
             "launches_us_total": launch_us, "launches_GBps": set_bytes / launch_us / 1e3,
             "kernel_GBps_unmerged": set_bytes / tot / 1e6, "weight_copies": -(-ROTATE_BYTES // set_bytes)}
-
-
-def decode_kernel(kind, nb, fused):
-    """The decode kernel the host picks for a row of nb blocks (amdc_host.c gemv_launch / gemv_x)."""
-    k = {synth.KIND_Q4_0: "amdc_gemv_q4_0", synth.KIND_Q4_K: "amdc_gemv_q4_k"}[kind]
-    if fused and nb <= 128:
-        return k + "_x1"
-    return k + ("_p2" if (nb + 7) // 8 > 32 else "_p1")
 
 
 def launch_rec(op, kernel, rows, cols, b, t_ms):

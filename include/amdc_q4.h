@@ -41,6 +41,10 @@ enum { AMDC_OK = 0, AMDC_EINVAL = 1, AMDC_ENOHIP = 2, AMDC_EHIP = 3, AMDC_ENOTOP
 enum { AMDC_KIND_Q4_0 = 0, AMDC_KIND_Q8_0 = 2, AMDC_KIND_Q4_K = 3, AMDC_KIND_Q6_K = 4 };
 
 const char *amdc_last_error(void);
+/* The name of the kernel the library launched last ("" before any launch):
+ * for profilers and benchmarks that label their timings (no reference
+ * counterpart). */
+const char *amdc_last_kernel(void);
 
 /* ---------------------------------------------------------------- load time (host only) */
 
@@ -257,9 +261,10 @@ int amdc_block_dots(int kind, const void *w, const uint8_t *xq, int32_t *out, ui
  * launch; the GEMM kernel (1, 2: int8 MFMA with 64 or 128 tokens per
  * workgroup; 3, 4: f16 MFMA, rows x tokens 64x128, 64x64);
  * the GEMM's K split (1..16); the decode kernel's form when gemv_unroll is 0
- * (1: the split across whole rows, 2: the buffer-load form that keeps the
- * next super-group in flight; 0: form 2 for rows of more than 32
- * super-groups). Also read once from the environment: AMDC_GEMV_L,
+ * (1: the persistent pipelined form, 2: the buffer-load form that keeps the
+ * next super-group in flight, 3: the single-shot form, one row group per
+ * workgroup with all its loads issued at once; 0: form 3 up to 256
+ * super-groups per row, else form 2). Also read once from the environment: AMDC_GEMV_L,
  * AMDC_GEMV_U, AMDC_GEMV_WG, AMDC_GEMM_KERNEL, AMDC_GEMM_KSPLIT,
  * AMDC_GEMV_FORM. */
 int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kernel, int gemm_ksplit, int gemv_form);

@@ -72,7 +72,7 @@ def test_exact_decode(dev, orc, kind, rows, nb):
     e = Exact(orc, kind, rows, nb, 1, seed=kind * 10 + nb, dev=dev)
     try:
         tried = []
-        for form in (0, 1, 2):
+        for form in (0, 1, 2, 3):
             for lanes in (0, 4, 8, 16, 32, 64):
                 if kind in (2, 4) and form == 1:
                     continue  # Q8_0 / Q6_K have the second form only

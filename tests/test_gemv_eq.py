@@ -3,8 +3,8 @@
 The reference's multi-token kernels give each token exactly the bits of the
 single-token kernel (kernels/ie_kernels.c:481-482, checked by its
 tools/gemv_eq.c), which its MTP speculative decode relies on to emit exactly
-the greedy tokens (README.md:515-522). Here every decode form (first form at
-any lane count, second form, the fused-quantization form) and the int8-MFMA
+the greedy tokens (README.md:515-522). Here every decode form (persistent first
+form, second form, single-shot form, at any lane count, and the fused-quantization forms) and the int8-MFMA
 verify kernels (T = 1..16, any K split) follow the super-group tree order, so
 on ordinary (rounding) data they all return the same bits; the oracle check
 of these values is in test_gpu_parity.py. Q6_K's verify kernel joins a
@@ -47,7 +47,7 @@ def test_decode_forms_equal(dev, kind, rows, nb):
     Y = dev.DevBuf(4 * rows)
     ref = None
     try:
-        for form in (0, 1, 2):
+        for form in (0, 1, 2, 3):
             for lanes in (0, 4, 8, 16, 32, 64):
                 for wgs in (0, 5):
                     dev.set_tuning(lanes=lanes, form=form, wgs=wgs)
@@ -57,10 +57,12 @@ def test_decode_forms_equal(dev, kind, rows, nb):
                     if ref is None:
                         ref = got
                     assert np.array_equal(got, ref), (form, lanes, wgs, int((got != ref).sum()))
-        dev.set_tuning()
-        Y.fill(0xFF)
-        dev.gemv_x(kind, W, X, Y, rows, nb)
-        assert np.array_equal(Y.download(np.uint32), ref), "gemv_x"
+        for form in (0, 1, 3):  # the fused-quantization forms: persistent (x1) and single-shot (xs)
+            for lanes in (0, 8, 16):
+                dev.set_tuning(form=form, lanes=lanes)
+                Y.fill(0xFF)
+                dev.gemv_x(kind, W, X, Y, rows, nb)
+                assert np.array_equal(Y.download(np.uint32), ref), ("gemv_x", form, lanes)
     finally:
         dev.set_tuning()
 
