@@ -273,7 +273,8 @@ enum {
   K_GEMV_Q6K_V16,
   K_GEMVS_Q4, /* amdc_gemv_q4_0_s1 .. _s4, then amdc_gemv_q4_k_s1 .. _s4 */
   K_GEMVXS_Q4 = K_GEMVS_Q4 + 8, /* amdc_gemv_q4_0_xs1 .. _xs4, then amdc_gemv_q4_k_xs1 .. _xs4 */
-  K_N = K_GEMVXS_Q4 + 8
+  K_GEMVM_Q4 = K_GEMVXS_Q4 + 8, /* amdc_gemv_q4_0_m1, amdc_gemv_q4_k_m1 */
+  K_N = K_GEMVM_Q4 + 2
 };
 static const char *const kname[K_N] = {
     "amdc_quant_q8",           "amdc_dots_q4_0",          "amdc_dots_q4_k",          "amdc_gemm_q4_k_n128",
@@ -289,7 +290,8 @@ static const char *const kname[K_N] = {
     "amdc_gemv_q4_0_s1",       "amdc_gemv_q4_0_s2",       "amdc_gemv_q4_0_s3",       "amdc_gemv_q4_0_s4",
     "amdc_gemv_q4_k_s1",       "amdc_gemv_q4_k_s2",       "amdc_gemv_q4_k_s3",       "amdc_gemv_q4_k_s4",
     "amdc_gemv_q4_0_xs1",      "amdc_gemv_q4_0_xs2",      "amdc_gemv_q4_0_xs3",      "amdc_gemv_q4_0_xs4",
-    "amdc_gemv_q4_k_xs1",      "amdc_gemv_q4_k_xs2",      "amdc_gemv_q4_k_xs3",      "amdc_gemv_q4_k_xs4"};
+    "amdc_gemv_q4_k_xs1",      "amdc_gemv_q4_k_xs2",      "amdc_gemv_q4_k_xs3",      "amdc_gemv_q4_k_xs4",
+    "amdc_gemv_q4_0_m1",       "amdc_gemv_q4_k_m1"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -746,6 +748,20 @@ static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uin
       if (rc) return rc;
     }
     return AMDC_OK;
+  }
+  if (T > 1u && T <= 8u && (kind == AMDC_KIND_Q4_0 || kind == AMDC_KIND_Q4_K) && t_ksplit == 0) {
+    /* a few vectors on a small matrix: the decode kernel's dots for every vector (amdc_gemv_*_m1), one
+       launch, no K split; the int8-MFMA kernels below cost about 11 us at any size (the K split and the
+       reduction launch). Measured on MI355X (us, this kernel / the MFMA kernels): T = 2 17408 x 5120
+       Q4_K 20.7 / 21.3, 11008 x 4096 Q4_0 9.8 / 13.2; T = 4 6144 x 5120 Q4_K 11.7 / 12.2, 11008 x 4096
+       12.6 / 13.0, 17408 x 5120 26.0 / 21.5; T = 8 4096 x 4096 Q4_0 10.1 / 11.4, 6144 x 5120 Q4_K
+       17.4 / 12.3. One super-group per lane (up to 64 per row), LDS for every vector. */
+    const u32 ng = amdc_ngroups(nb), L = gemvs_lanes(ng, rows, 0), rpg = 4u * (64u / L), lds = 320u * ng * T;
+    if (ng <= L && (u64)T * rows * ng <= 786432u && lds <= 64u * 1024u) {
+      const u32 nrg = (rows + rpg - 1u) / rpg;
+      void *a[] = {&w, &xq, &y, &rows, &nb, &bias, &res, (void *)&L, &T, &xs, &ys, &rs};
+      return launch(K_GEMVM_Q4 + (kind == AMDC_KIND_Q4_K ? 1 : 0), nrg, 1, lds, stream, a);
+    }
   }
   if (T > 1u) {
     /* the int8-MFMA verify kernels, up to 16 vectors per launch; measured on MI355X, T = 16:

@@ -605,6 +605,101 @@ GEMVS_KERNELS(q4_k, AMDC_Q4_K, 2, s, 256)
 GEMVS_KERNELS(q4_k, AMDC_Q4_K, 3, s, 256)
 GEMVS_KERNELS(q4_k, AMDC_Q4_K, 4, s, 256)
 
+// The multi-vector GEMV of a few vectors (T <= 8: the MTP verify step) on
+// the decode kernel's integer dots (amdc_gemv_*_m<NI>): the single-shot split
+// (one row group per workgroup, each lane's NI super-groups loaded at once),
+// with the Q8 vectors of all T tokens staged in LDS (320 ng bytes per token,
+// permuted as the weights), and each lane's super-groups dotted with every
+// token: the weights are read once for all T vectors and the arithmetic of
+// each token is the decode GEMV's (the same block steps, leaves and tree, so
+// each y_t equals the decode GEMV of vector t bit for bit). No K split and no
+// reduction launch. Vector t at xq + t xs bytes, y_t at y + t ys floats,
+// res_t at res + t rs floats. The VALU work grows with T (8 dot4 per block and
+// vector), so the host takes it for few vectors on small matrices, where the
+// int8-MFMA kernels' fixed costs (K split, reduction launch) dominate.
+template <int KIND, u32 NI>
+__device__ __forceinline__ void gemvm_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
+                                           u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 L, u32 T, u32 xs,
+                                           u32 ys, u32 rs) {
+  constexpr u32 TM = 8u; // the most vectors per launch
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const u32 ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw;
+  const u64 RB = amdc_row_bytes(nb);
+  const u32 nblk = 8u * ng, tb = 320u * ng; // LDS bytes per token
+  const u32 r = blockIdx.x * rpg + wv * rpw + q;
+  const uint8_t *wr = W + (u64)(r < rows ? r : rows - 1u) * RB;
+  Item it[NI];
+#pragma unroll
+  for (u32 i = 0; i < NI; i++) load_item<KIND>(it[i], wr, ng, l + L * i, l + L * i < ng);
+  // stage (token, block) pairs, 4 per thread in flight at a time
+  for (u32 j0 = tid; j0 < T * nblk; j0 += 4u * NT) {
+    u32x4 lo[4], hi[4];
+    float d[4];
+    u32 as[4];
+#pragma unroll
+    for (u32 c = 0; c < 4u; c++) {
+      const u32 j = j0 + c * NT, t = j / nblk, jb = j - t * nblk;
+      const bool in = j < T * nblk && jb < nb;
+      const uint8_t *xt = xq + (u64)(in ? t : 0u) * xs;
+      const u32 jj = in ? jb : 0u;
+      lo[c] = *(const u32x4 *)(xt + 32u * jj);
+      hi[c] = *(const u32x4 *)(xt + 32u * jj + 16u);
+      d[c] = ((const float *)(xt + 32u * nb))[jj];
+      as[c] = ((const u32 *)(xt + 36u * nb))[jj];
+      if (!in) lo[c] = (u32x4)(0u), hi[c] = (u32x4)(0u), d[c] = 0.0f, as[c] = 0u;
+    }
+#pragma unroll
+    for (u32 c = 0; c < 4u; c++) {
+      const u32 j = j0 + c * NT;
+      if (j < T * nblk) {
+        const u32 t = j / nblk, jb = j - t * nblk, p = (jb & 7u) * ng + (jb >> 3);
+        uint8_t *base = smem + t * tb;
+        ((u32x4 *)base)[p] = lo[c];
+        ((u32x4 *)base + nblk)[p] = hi[c];
+        ((float *)(base + 32u * nblk))[p] = d[c];
+        ((u32 *)(base + 36u * nblk))[p] = as[c];
+      }
+    }
+  }
+  __syncthreads();
+  ItemTree tr[TM];
+#pragma unroll
+  for (u32 i = 0; i < NI; i++) {
+    const u32 g = l + L * i;
+#pragma unroll
+    for (u32 t = 0; t < TM; t++) {
+      if (t < T) {
+        const uint8_t *base = smem + t * tb;
+        const float leaf = item_dot<KIND>(it[i], g < ng ? g : 0u, ng, (const u32x4 *)base, (const u32x4 *)base + nblk,
+                                          (const float *)(base + 32u * nblk), (const u32 *)(base + 36u * nblk), 0.0f);
+        tr[t].add(seg_sum(g < ng ? leaf : 0.0f, L), i);
+      }
+    }
+  }
+  if (l == 0u && r < rows) {
+    const float b = bias ? bias[r] : 0.0f;
+#pragma unroll
+    for (u32 t = 0; t < TM; t++) {
+      if (t < T) {
+        float o = tr[t].sum(NI);
+        if (bias) o = o + b;
+        if (res) o = res[(u64)t * rs + r] + o;
+        y[(u64)t * ys + r] = o;
+      }
+    }
+  }
+}
+
+#define GEMVM_KERNEL(KN, KIND, NI)                                                                                                         \
+  extern "C" __global__ __launch_bounds__(256) void amdc_gemv_##KN##_m##NI(const uint8_t *W, const uint8_t *xq, float *y, u32 rows,    \
+                                                                           u32 nb, const float *bias, const float *res, u32 L, u32 T,  \
+                                                                           u32 xs, u32 ys, u32 rs) {                                   \
+    gemvm_body<KIND, NI>(W, xq, y, rows, nb, bias, res, L, T, xs, ys, rs);                                                               \
+  }
+GEMVM_KERNEL(q4_0, AMDC_Q4_0, 1)
+GEMVM_KERNEL(q4_k, AMDC_Q4_K, 1)
+
 // The decode GEMV, second form: the same lane split, LDS layout and
 // per-block arithmetic as gemv1_body, with the weights read through a buffer
 // resource (32-bit offsets; the host checks rows * row bytes + row bytes <
