@@ -120,6 +120,9 @@ ABI = {
     "amdc_rmsnorm_q8": (C.c_int, [_P, _P, _P, _U32, C.c_float, _P, _U32, _U32, _U32, _U32, _P]),
     "amdc_swiglu_q8": (C.c_int, [_P, _P, _U32, _P, _U32, _U32, _U32, _P]),
     "amdc_chain_create": (C.c_int, [_P, _U32, C.POINTER(_P)]),
+    "amdc_chain_create_form": (C.c_int, [_P, _U32, C.c_int, C.POINTER(_P)]),
+    "amdc_chain_trace": (C.c_int, [_P, _P]),
+    "amdc_chain_trace_words": (_U32, [_P]),
     "amdc_chain_launch": (C.c_int, [_P, _P]),
     "amdc_chain_check": (C.c_int, [_P]),
     "amdc_chain_destroy": (C.c_int, [_P]),
@@ -450,13 +453,17 @@ def chain_gemv_x(kind, w, x, y, rows, nb, bias=None, res=None, sync=True):
     return ChainOp(CHAIN_GEMV_X, kind, int(sync), rows, nb, _p(w), _p(x), None, None, _p(y), _p(bias), _p(res))
 
 
-class Chain:
-    """amdc_chain_create / _launch / _check / _destroy: a list of ChainOp run by one launch."""
+CHAIN_AUTO, CHAIN_PERSISTENT, CHAIN_STREAMING = 0, 1, 2
 
-    def __init__(self, ops):
+
+class Chain:
+    """amdc_chain_create_form / _launch / _check / _destroy: a list of ChainOp run by one launch (form:
+    CHAIN_AUTO, CHAIN_PERSISTENT or CHAIN_STREAMING)."""
+
+    def __init__(self, ops, form=CHAIN_AUTO):
         arr = (ChainOp * len(ops))(*ops)
         h = _P()
-        _check(lib().amdc_chain_create(C.cast(arr, _P), len(ops), C.byref(h)))
+        _check(lib().amdc_chain_create_form(C.cast(arr, _P), len(ops), form, C.byref(h)))
         self.h = h
 
     def launch(self, stream=None):
@@ -464,6 +471,14 @@ class Chain:
 
     def check(self):
         _check(lib().amdc_chain_check(self.h))
+
+    def trace(self, buf):
+        """amdc_chain_trace: record the timeline of later launches into buf (a DevBuf of trace_words()
+        u64 words), or stop (None)."""
+        _check(lib().amdc_chain_trace(self.h, buf.ptr if buf is not None else None))
+
+    def trace_words(self):
+        return lib().amdc_chain_trace_words(self.h)
 
     def __del__(self):
         if getattr(self, "h", None) and _lib is not None:

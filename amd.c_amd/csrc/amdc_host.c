@@ -274,7 +274,8 @@ enum {
   K_GEMVS_Q4, /* amdc_gemv_q4_0_s1 .. _s4, then amdc_gemv_q4_k_s1 .. _s4 */
   K_GEMVXS_Q4 = K_GEMVS_Q4 + 8, /* amdc_gemv_q4_0_xs1 .. _xs4, then amdc_gemv_q4_k_xs1 .. _xs4 */
   K_GEMVM_Q4 = K_GEMVXS_Q4 + 8, /* amdc_gemv_q4_0_m1, amdc_gemv_q4_k_m1 */
-  K_N = K_GEMVM_Q4 + 2
+  K_CHAIN_S = K_GEMVM_Q4 + 2, /* amdc_chain_s_q4_0, amdc_chain_s_q4_k */
+  K_N = K_CHAIN_S + 2
 };
 static const char *const kname[K_N] = {
     "amdc_quant_q8",           "amdc_dots_q4_0",          "amdc_dots_q4_k",          "amdc_gemm_q4_k_n128",
@@ -291,7 +292,7 @@ static const char *const kname[K_N] = {
     "amdc_gemv_q4_k_s1",       "amdc_gemv_q4_k_s2",       "amdc_gemv_q4_k_s3",       "amdc_gemv_q4_k_s4",
     "amdc_gemv_q4_0_xs1",      "amdc_gemv_q4_0_xs2",      "amdc_gemv_q4_0_xs3",      "amdc_gemv_q4_0_xs4",
     "amdc_gemv_q4_k_xs1",      "amdc_gemv_q4_k_xs2",      "amdc_gemv_q4_k_xs3",      "amdc_gemv_q4_k_xs4",
-    "amdc_gemv_q4_0_m1",       "amdc_gemv_q4_k_m1"};
+    "amdc_gemv_q4_0_m1",       "amdc_gemv_q4_k_m1",       "amdc_chain_s_q4_0",       "amdc_chain_s_q4_k"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -551,11 +552,12 @@ int amdc_graph_destroy(void *exec) {
 /* ---------------------------------------------------------------- launches */
 
 static int g_last_k = -1; /* the kernel of the last launch (amdc_last_kernel) */
-static int launch(int k, unsigned gx, unsigned gy, unsigned lds, void *stream, void **args) {
+static int launch_nt(int k, unsigned gx, unsigned gy, unsigned nt, unsigned lds, void *stream, void **args) {
   g_last_k = k;
-  HIPCALL(H.ModuleLaunchKernel(g_k[k], gx, gy, 1, 256, 1, 1, lds, stream, args, NULL));
+  HIPCALL(H.ModuleLaunchKernel(g_k[k], gx, gy, 1, nt, 1, 1, lds, stream, args, NULL));
   return AMDC_OK;
 }
+static int launch(int k, unsigned gx, unsigned gy, unsigned lds, void *stream, void **args) { return launch_nt(k, gx, gy, 256u, lds, stream, args); }
 
 const char *amdc_last_kernel(void) { return g_last_k >= 0 ? kname[g_last_k] : ""; }
 
@@ -1109,8 +1111,15 @@ typedef char chain_dev_op_is_64_bytes[sizeof(chain_dev_op) == 64 ? 1 : -1];
 typedef struct {
   chain_dev_op *ops; /* device: the list, then the barrier state (CHAIN_SYNC_BYTES) */
   uint32_t *sync;
-  uint32_t n, grid, lds;
+  uint32_t n, grid, lds, nt, outb, vecb;
+  uint64_t *trace; /* amdc_chain_trace's buffer (streaming form), or NULL */
+  int k; /* the kernel: K_CHAIN, or K_CHAIN_S (+ 1 for Q4_K) for the streaming form */
 } chain_t;
+
+/* Threads per workgroup of the streaming chain (amdc_chain_s_*: one workgroup per CU): 4 staging
+   and 8 compute waves. */
+#define CHAIN_S_NT 768u
+#define CHAIN_S_NC 8u
 
 #define CHAIN_SPIN_NS 200000000u
 #define CHAIN_SYNC_BYTES (35u * 128u) /* the kernel's NGRP + 3 lines */
@@ -1139,8 +1148,11 @@ static unsigned chain_spans(const chain_dev_op *e, const amdc_chain_op *o, span 
   return 4;
 }
 
-int amdc_chain_create(const amdc_chain_op *ops, uint32_t n, void **chain) {
+int amdc_chain_create(const amdc_chain_op *ops, uint32_t n, void **chain) { return amdc_chain_create_form(ops, n, AMDC_CHAIN_AUTO, chain); }
+
+int amdc_chain_create_form(const amdc_chain_op *ops, uint32_t n, int form, void **chain) {
   NEED_OPEN();
+  if (form < AMDC_CHAIN_AUTO || form > AMDC_CHAIN_STREAMING) return fail(AMDC_EINVAL, "chain_create: form %d", form);
   if (!ops || !n || !chain) return fail(AMDC_EINVAL, "chain_create: null pointer or empty list");
   chain_dev_op *d = (chain_dev_op *)calloc(n, sizeof(chain_dev_op));
   if (!d) return fail(AMDC_EINVAL, "chain_create: out of host memory");
@@ -1190,8 +1202,43 @@ int amdc_chain_create(const amdc_chain_op *ops, uint32_t n, void **chain) {
     free(d);
     return rc;
   }
+  /* The streaming form (amdc_chain_s_*) runs lists whose GEMVs are all Q4_0 or all Q4_K, with at
+     least one GEMV (the form AMDC_CHAIN_AUTO picks it for them). */
+  u32 kinds = 0, ngemv = 0;
+  for (u32 k = 0; k < n; k++) {
+    if (d[k].type == 0u) continue;
+    ngemv++;
+    kinds |= d[k].type == 1u || d[k].type == 3u ? 1u : d[k].type == 2u || d[k].type == 4u ? 2u : 4u;
+  }
+  const int can_stream = ngemv && (kinds == 1u || kinds == 2u);
+  if (form == AMDC_CHAIN_STREAMING && !can_stream) {
+    free(d);
+    return fail(AMDC_EINVAL, "chain_create: the streaming form needs at least one GEMV and every GEMV Q4_0, or every one Q4_K");
+  }
+  const int streaming = form == AMDC_CHAIN_STREAMING || (form == AMDC_CHAIN_AUTO && can_stream);
+  const int kk = streaming ? K_CHAIN_S + (kinds == 2u ? 1 : 0) : K_CHAIN;
+  const u32 nt = streaming ? CHAIN_S_NT : 256u, cus = (u32)(g_cus > 0 ? g_cus : 256);
+  u32 outb = 0, vecb = 0;
+  if (streaming) {
+    /* LDS of the streaming kernel: the workgroup's results of one operation (its 8 compute waves x
+       their most row groups x rows per group, floats), then the vector */
+    const u32 GW = CHAIN_S_NC * cus;
+    u32 xrb = 0; /* the raw f32 vector of an f32-input operation */
+    for (u32 k = 0; k < n; k++) {
+      if (d[k].type == 0u) continue;
+      const u32 rpw = 64u / d[k].L, nwr = (d[k].rows + rpw - 1u) / rpw, mj = (nwr + GW - 1u) / GW;
+      if (4u * CHAIN_S_NC * mj * rpw > outb) outb = 4u * CHAIN_S_NC * mj * rpw;
+      if (d[k].type >= 3u && 128u * d[k].nb > xrb) xrb = 128u * d[k].nb;
+    }
+    vecb = lds;
+    lds += outb + xrb;
+    if (lds > GEMV_LDS_T1) {
+      free(d);
+      return fail(AMDC_EINVAL, "chain_create: %u operations and their results need %u bytes of LDS in the streaming form", n, lds);
+    }
+  }
   int occ = 0;
-  if (H.OccupancyMaxActiveBlocks(&occ, g_k[K_CHAIN], 256, lds) != 0 || occ < 1) {
+  if (H.OccupancyMaxActiveBlocks(&occ, g_k[kk], (int)nt, lds) != 0 || occ < 1) {
     free(d);
     return fail(AMDC_EHIP, "chain_create: the chain kernel does not fit on a CU (LDS %u)", lds);
   }
@@ -1200,7 +1247,8 @@ int amdc_chain_create(const amdc_chain_op *ops, uint32_t n, void **chain) {
     free(d);
     return fail(AMDC_EINVAL, "chain_create: out of host memory");
   }
-  c->n = n, c->lds = lds, c->grid = (u32)(g_cus > 0 ? g_cus : 256) * (u32)(occ < 2 ? occ : 2);
+  c->n = n, c->lds = lds, c->k = kk, c->nt = nt, c->outb = outb, c->vecb = vecb;
+  c->grid = cus * (u32)(streaming ? 1 : occ < 2 ? occ : 2);
   const size_t bytes = (size_t)n * sizeof(chain_dev_op) + CHAIN_SYNC_BYTES;
   if (H.Malloc((void **)&c->ops, bytes) != 0) rc = fail(AMDC_EHIP, "chain_create: device allocation of %zu bytes", bytes);
   if (!rc) {
@@ -1224,8 +1272,23 @@ int amdc_chain_launch(void *chain, void *stream) {
   chain_t *c = (chain_t *)chain;
   if (!c) return fail(AMDC_EINVAL, "chain_launch: null chain");
   u32 spin = CHAIN_SPIN_NS;
-  void *args[] = {&c->ops, &c->n, &c->sync, &spin};
-  return launch(K_CHAIN, c->grid, 1, c->lds, stream, args);
+  void *args[] = {&c->ops, &c->n, &c->sync, &spin, &c->outb, &c->vecb, &c->trace}; /* the streaming kernel's last three */
+  if (c->k == K_CHAIN) args[4] = NULL;
+  return launch_nt(c->k, c->grid, 1, c->nt, c->lds, stream, args);
+}
+
+int amdc_chain_trace(void *chain, uint64_t *buf) {
+  NEED_OPEN();
+  chain_t *c = (chain_t *)chain;
+  if (!c) return fail(AMDC_EINVAL, "chain_trace: null chain");
+  if (buf && c->k == K_CHAIN) return fail(AMDC_EINVAL, "chain_trace: the persistent form records no timeline");
+  c->trace = buf;
+  return AMDC_OK;
+}
+
+uint32_t amdc_chain_trace_words(void *chain) {
+  const chain_t *c = (const chain_t *)chain;
+  return c && c->k != K_CHAIN ? c->grid * (2u + 4u * c->n + 64u) : 0u;
 }
 
 int amdc_chain_check(void *chain) {

@@ -326,7 +326,9 @@ __device__ __forceinline__ void load_item(Item &it, const uint8_t *wr, u32 ng, u
 // One super-group's contribution to a row: for each of its 8 blocks k (LDS
 // slot p = k GC + gl of the staged vector), the integer block dot and the
 // reference's per-block float step (src/cpu.c:81, 112, 142, 168).
-template <int KIND>
+// LEAN: a scheduling barrier after every block, so that the LDS words of at
+// most two blocks are live at once (for kernels that hold two items).
+template <int KIND, bool LEAN = false>
 __device__ __forceinline__ float item_dot(const typename ItemOf<KIND>::type &it, u32 gl, u32 GC, const u32x4 *s_lo, const u32x4 *s_hi,
                                           const float *s_d, const u32 *s_as, float acc) {
   float dsc = 0.0f, dmn = 0.0f;
@@ -361,6 +363,7 @@ __device__ __forceinline__ float item_dot(const typename ItemOf<KIND>::type &it,
         acc = __builtin_fmaf(-mm, da * (float)(int)as, __builtin_fmaf(sw * (float)dq, da, acc));
       }
     }
+    if (LEAN && (k & 1u)) __builtin_amdgcn_sched_barrier(0);
   }
   return acc;
 }
@@ -1171,6 +1174,386 @@ extern "C" __global__ __launch_bounds__(256, 2) void amdc_chain(const ChainOp *_
   if (threadIdx.x == 0u && chain_arrive(sync, nbar + 1u)) {
     for (u32 g = 0; g < NGRP + 2u; g++) __hip_atomic_store(sync + SYNC_LINE * g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+}
+
+// ------------------------------------------------------------------ the streaming chain
+
+// The GEMV chain, streaming form (amdc_chain_s_q4_0 / _q4_k: every GEMV of
+// the list of one kind): one workgroup of 768 threads per CU, in two roles.
+// - 8 compute waves issue nothing but weight loads. Wave gw = 8 blockIdx.x +
+//   (wave - 4) of the GW = 8 gridDim.x compute waves takes the wave row
+//   groups (64 / L rows each) gw, gw + GW, ... of every GEMV, each as
+//   ceil(ng / L) items of one super-group per lane (the decode kernels' lane
+//   split, block arithmetic and summation order: bit-equal results). A wave
+//   keeps NBUF item buffers (2 for Q4_0, 3 for Q4_K, as the registers allow):
+//   right after it computes an item it loads the next one of its sequence
+//   into the freed buffer, whichever operation that item belongs to, so while
+//   the workgroup passes an operation boundary the weights of the next NBUF
+//   items of every compute wave are in flight. Row results go to the LDS.
+// - 4 staging waves do the rest: they write the workgroup's results of an
+//   operation to memory (with bias and residual), take part in the grid
+//   barrier, quantize or load the next operation's vector into the LDS, and
+//   run the quantize operations.
+// A wave's vector memory operations complete in issue order; with the roles
+// apart, no barrier poll, vector load or output store waits behind weight
+// loads. The operation list is copied to the LDS once (the compute waves'
+// cursors read it there). Outputs and the vectors between operations are
+// coherent (sc1) accesses, as in amdc_chain.
+#define CS_NS 4u // staging waves per workgroup
+#define CS_NC 8u // compute waves per workgroup
+
+__device__ __forceinline__ bool chain_wait(u32 *sync, u32 nbar, u32 spin_ns) {
+  const u64 t0 = __builtin_amdgcn_s_memrealtime(), lim = spin_ns / 10u;
+  for (u32 it = 0;; it++) {
+    if ((int)(__hip_atomic_load(sync + SYNC_LINE * (NGRP + 1u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - nbar) >= 0) return true;
+    if ((it & 15u) == 15u) {
+      if (__hip_atomic_load(sync + SYNC_LINE * (NGRP + 2u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+      if (__builtin_amdgcn_s_memrealtime() - t0 > lim) {
+        __hip_atomic_store(sync + SYNC_LINE * (NGRP + 2u), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+      }
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// The per-operation values of a GEMV of the streaming chain for one compute wave.
+struct CsOp {
+  const uint8_t *W;
+  u64 RB;
+  u32 rows, nb, ng, L, ni, rpw, nwr, nit;
+};
+__device__ __forceinline__ CsOp cs_op(const ChainOp &op, u32 gw, u32 GW) {
+  CsOp c;
+  c.W = (const uint8_t *)op.a, c.rows = op.rows, c.nb = op.nb, c.ng = amdc_ngroups(op.nb), c.L = op.L ? op.L : 64u; // L = 0: a quantization
+  c.RB = amdc_row_bytes(op.nb), c.ni = (c.ng + c.L - 1u) / c.L, c.rpw = 64u / c.L;
+  c.nwr = (c.rows + c.rpw - 1u) / c.rpw; // wave row groups
+  c.nit = op.type >= 1u && op.type <= 4u && gw < c.nwr ? (c.nwr - gw + GW - 1u) / GW * c.ni : 0u;
+  return c;
+}
+
+// An operation of the list, read through the constant address space: scalar
+// loads (counted apart from the vector memory operations, so that reading the
+// list never waits for weight loads), every word uniform.
+typedef const __attribute__((address_space(4))) ChainOp *cops_t;
+__device__ __forceinline__ ChainOp ld_op(cops_t p) { return *p; }
+
+// The load cursor of a compute wave: operation kl, its item fl (of cl.nit
+// items), ahead of the computation. Once the wave's sequence is done it loads
+// its last item again (unused), so that every call issues the same 9 loads
+// and no load is under a branch.
+struct CsCursor {
+  cops_t ops;
+  u32 n, gw, GW, kl, fl;
+  CsOp cl;
+  // the first item at or after operation k (false: none)
+  __device__ __forceinline__ bool seek(u32 k) {
+    for (; k < n; k++) {
+      const CsOp c = cs_op(ld_op(ops + k), gw, GW);
+      if (c.nit) {
+        cl = c, kl = k, fl = 0;
+        return true;
+      }
+    }
+    return false;
+  }
+  // the host puts a GEMV operation in every streaming chain: a wave without
+  // items loads (clamped) addresses of the first one
+  __device__ __forceinline__ void init(cops_t o, u32 n_, u32 gw_, u32 GW_) {
+    ops = o, n = n_, gw = gw_, GW = GW_, kl = n, fl = 0;
+    if (!seek(0)) {
+      u32 k = 0;
+      while (k + 1u < n && (ld_op(ops + k).type < 1u || ld_op(ops + k).type > 4u)) k++;
+      cl = cs_op(ld_op(ops + k), gw, GW);
+    }
+  }
+  // the next item of the sequence into it
+  __device__ __forceinline__ void issue(Item &it) {
+    typedef const __attribute__((address_space(1))) u32x4 *gp;
+    const u32 lane = threadIdx.x & 63u, j = fl / cl.ni, i = fl - j * cl.ni, l = lane & (cl.L - 1u), q = lane / cl.L, g = l + cl.L * i;
+    const u32 r = (gw + GW * j) * cl.rpw + q, gg = g < cl.ng ? g : 0u;
+    const uint8_t *wr = cl.W + (u64)(r < cl.rows ? r : cl.rows - 1u) * cl.RB;
+    it.h = __builtin_nontemporal_load((gp)(wr + amdc_header_off(gg))); // the loads of load_item, as global (not flat) accesses
+#pragma unroll
+    for (u32 kk = 0; kk < 8u; kk++) it.n[kk] = __builtin_nontemporal_load((gp)(wr + amdc_nib_off(cl.ng, gg, kk)));
+    if (kl < n && ++fl == cl.nit) {
+      const CsOp keep = cl;
+      fl--;
+      if (!seek(kl + 1u)) kl = n, cl = keep; // done: the last item again
+    }
+  }
+};
+
+// The quantization of nb blocks of the f32 vector op.a into the Q8 buffer
+// op.b, blocks b0 + 32 p .. by the staging threads of workgroup p (the
+// arithmetic of amdc_quant_q8).
+__device__ __forceinline__ void cs_quant_op(const ChainOp &op, u32 t) {
+  const u32 nb = op.nb, e = t & 7u;
+  const __amdgpu_buffer_rsrc_t rx = rsrc(op.a, 128u * nb), rq = rsrc(op.b, 40u * nb);
+  for (u32 b0 = 32u * blockIdx.x; b0 < nb; b0 += 32u * gridDim.x) {
+    const u32 b = b0 + (t >> 3);
+    const v4f v = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rx, b < nb ? 128u * b + 16u * e : 0xFFFFFFF0u, 0, CPOL_SC1));
+    float a = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)), __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
+    a = __builtin_fmaxf(a, dpp<0xB1>(a));
+    a = __builtin_fmaxf(a, dpp<0x4E>(a));
+    a = __builtin_fmaxf(a, dpp<0x141>(a));
+    const float d = a / 127.0f;
+    int qi[4];
+#pragma unroll
+    for (int m = 0; m < 4; m++) qi[m] = d != 0.0f ? (int)__builtin_roundf(v[m] / d) : 0;
+    const u32 word = (u32)(qi[0] & 255) | (u32)(qi[1] & 255) << 8 | (u32)(qi[2] & 255) << 16 | (u32)qi[3] << 24;
+    u32 sum = (u32)qi[0] + (u32)qi[1] + (u32)qi[2] + (u32)qi[3];
+    sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0xB1, 0xF, 0xF, false);
+    sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0x4E, 0xF, 0xF, false);
+    sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0x141, 0xF, 0xF, false);
+    if (b < nb) {
+      __builtin_amdgcn_raw_buffer_store_b32(word, rq, 32u * b + 4u * e, 0, CPOL_SC1);
+      if (e == 0u) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(u32, d), rq, 32u * nb + 4u * b, 0, CPOL_SC1);
+        __builtin_amdgcn_raw_buffer_store_b32(sum, rq, 36u * nb + 4u * b, 0, CPOL_SC1);
+      }
+    }
+  }
+}
+
+// The vector of GEMV operation op, by the staging threads (t < 256): a Q8
+// vector into the LDS (vec), permuted as the weights; an f32 vector raw into
+// the LDS (xr, 128 nb bytes), up to 16 loads of 16 bytes per thread in
+// flight at once, for cs_quant_lds.
+__device__ __forceinline__ void cs_stage(const ChainOp &op, u32 t, uint8_t *vec, float *xr) {
+  const u32 nb = op.nb, ng = amdc_ngroups(nb), nblk = 8u * ng;
+  if (op.type >= 3u) {
+    constexpr u32 NL = 16u;
+    const __amdgpu_buffer_rsrc_t rx = rsrc(op.b, 128u * nb);
+    const u32 nw = 8u * nb; // 16-byte words
+    for (u32 w0 = 0; w0 < nw; w0 += 256u * NL) {
+      u32x4 v[NL];
+#pragma unroll
+      for (u32 i = 0; i < NL; i++) {
+        const u32 wi = w0 + 256u * i + t;
+        v[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, wi < nw ? 16u * wi : 0xFFFFFFF0u, 0, CPOL_SC1);
+      }
+#pragma unroll
+      for (u32 i = 0; i < NL; i++) {
+        const u32 wi = w0 + 256u * i + t;
+        if (wi < nw) ((u32x4 *)xr)[wi] = v[i];
+      }
+    }
+    return;
+  }
+  u32x4 *s_lo = (u32x4 *)vec, *s_hi = s_lo + nblk;
+  float *s_d = (float *)(s_hi + nblk);
+  u32 *s_as = (u32 *)(s_d + nblk);
+  const __amdgpu_buffer_rsrc_t rq = rsrc(op.b, 40u * nb);
+  for (u32 j = t; j < nblk; j += 256u) {
+    const u32 p = (j & 7u) * ng + (j >> 3);
+    const bool in = j < nb;
+    s_lo[p] = __builtin_amdgcn_raw_buffer_load_b128(rq, in ? 32u * j : 0xFFFFFFF0u, 0, CPOL_SC1);
+    s_hi[p] = __builtin_amdgcn_raw_buffer_load_b128(rq, in ? 32u * j + 16u : 0xFFFFFFF0u, 0, CPOL_SC1);
+    s_d[p] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, in ? 32u * nb + 4u * j : 0xFFFFFFF0u, 0, CPOL_SC1));
+    s_as[p] = __builtin_amdgcn_raw_buffer_load_b32(rq, in ? 36u * nb + 4u * j : 0xFFFFFFF0u, 0, CPOL_SC1);
+  }
+}
+
+// The quantization of the raw f32 vector xr (nb blocks) into vec, by all NT_
+// threads of the workgroup (the arithmetic of amdc_quant_q8 and FusedQ8T: 8
+// lanes per block, blocks past nb up to the super-group end are zeros).
+template <u32 NT_>
+__device__ __forceinline__ void cs_quant_lds(const float *xr, u32 nb, uint8_t *vec) {
+  const u32 ng = amdc_ngroups(nb), nblk = 8u * ng, tid = threadIdx.x, e = tid & 7u;
+  u32x4 *s_lo = (u32x4 *)vec, *s_hi = s_lo + nblk;
+  float *s_d = (float *)(s_hi + nblk);
+  u32 *s_as = (u32 *)(s_d + nblk);
+  for (u32 b0 = 0; b0 < nblk; b0 += NT_ / 8u) {
+    const u32 b = b0 + (tid >> 3);
+    const v4f x = b < nb ? ((const v4f *)xr)[8u * b + e] : (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    float a = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(x.x), __builtin_fabsf(x.y)), __builtin_fmaxf(__builtin_fabsf(x.z), __builtin_fabsf(x.w)));
+    a = __builtin_fmaxf(a, dpp<0xB1>(a));
+    a = __builtin_fmaxf(a, dpp<0x4E>(a));
+    a = __builtin_fmaxf(a, dpp<0x141>(a));
+    const float d = a / 127.0f;
+    int qi[4];
+#pragma unroll
+    for (int m = 0; m < 4; m++) qi[m] = d != 0.0f ? (int)__builtin_roundf(x[m] / d) : 0;
+    const u32 word = (u32)(qi[0] & 255) | (u32)(qi[1] & 255) << 8 | (u32)(qi[2] & 255) << 16 | (u32)qi[3] << 24;
+    u32 sum = (u32)qi[0] + (u32)qi[1] + (u32)qi[2] + (u32)qi[3];
+    sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0xB1, 0xF, 0xF, false);
+    sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0x4E, 0xF, 0xF, false);
+    sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0x141, 0xF, 0xF, false);
+    if (b < nblk) {
+      const u32 p = (b & 7u) * ng + (b >> 3);
+      ((u32 *)(e < 4u ? &s_lo[p] : &s_hi[p]))[e & 3u] = word;
+      if (e == 0u) s_d[p] = d, s_as[p] = sum;
+    }
+  }
+}
+
+// LDS: the results of the workgroup's rows of one operation (outb bytes:
+// compute wave w, its row group j, row q at float (w mj + j) rpw + q, mj =
+// the most row groups of a compute wave), the vector (vecb bytes: the
+// staged Q8 vector), then the raw f32 vector of an f32-input operation. Every operation boundary is four workgroup barriers, met by every
+// wave in the same order (a compute wave may meet them after either of its
+// buffers): B1 the compute waves' results of operation k are in the LDS; Bw
+// the staging waves' stores of them are complete; Br the grid barrier has
+// passed (thread 0); Bx the next operation's vector (raw f32 or Q8) is in the
+// LDS; B2 it is quantized (all waves quantize an f32 vector between Bx and
+// B2). After the last operation only B1.
+// Each workgroup arrives once more after its last grid barrier (the last
+// arrival sets the counters back to zero, while the last operation runs).
+// trace (or NULL): per workgroup 2 + 4 n + 64 words of the 100 MHz clock:
+// the start, B2 of the start, B1 Bw Br B2 of each operation (thread 0), then
+// the time each of the first 64 items of the first compute wave is computed.
+template <int KIND, u32 NBUF>
+__device__ __forceinline__ void chain_s_body(const ChainOp *__restrict__ gops, u32 n, u32 *sync, u32 spin_ns, u32 outb, u32 vecb,
+                                             u64 *trace) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ u32 s_ok;
+  const cops_t ops = (cops_t)gops;
+  float *outs = (float *)smem;
+  uint8_t *vec = smem + outb;
+  float *xr = (float *)(smem + outb + vecb);
+  constexpr u32 NT_ = (CS_NS + CS_NC) * 64u;
+  const u32 tid = threadIdx.x, lane = tid & 63u, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const u32 GW = CS_NC * gridDim.x;
+  u64 *tr0 = trace ? trace + (u64)blockIdx.x * (2u + 4u * n + 64u) : nullptr;
+  if (tr0 && tid == 0u) tr0[0] = __builtin_amdgcn_s_memrealtime();
+  if (tid == 0u) s_ok = 1u;
+  u32 nsync = 0; // grid barriers in the list
+  for (u32 k = 0; k + 1u < n; k++) nsync += ld_op(ops + k).sync ? 1u : 0u;
+  u32 nbar = 0;
+  if (wv >= CS_NS) { // ---------------- a compute wave
+    const u32 w = wv - CS_NS, gw = CS_NC * blockIdx.x + w;
+    CsCursor cur;
+    cur.init(ops, n, gw, GW);
+    Item A, B, C; // C: the third buffer (NBUF 3)
+    cur.issue(A);
+    cur.issue(B);
+    if (NBUF == 3) cur.issue(C);
+    __syncthreads(); // Bx of the start
+    if (ld_op(ops).type >= 3u) cs_quant_lds<NT_>(xr, ld_op(ops).nb, vec);
+    __syncthreads(); // B2 of the start: operation 0's vector
+    u32 nt_ = 0;      // items computed (trace)
+    u32 k = 0, f = 0;
+    CsOp c = cs_op(ld_op(ops), gw, GW);
+    bool live = s_ok != 0u;
+    // past the operation boundaries this wave has reached; false when the list is done or aborted
+    auto next = [&]() {
+      while (live && f == c.nit) {
+        __syncthreads(); // B1
+        if (k + 1u == n) { // the last operation: the staging waves write the results and end
+          live = false;
+          break;
+        }
+        __syncthreads(); // Bw
+        __syncthreads(); // Br
+        __syncthreads(); // Bx
+        live = s_ok != 0u && ++k < n;
+        if (live) {
+          const ChainOp nx = ld_op(ops + k);
+          if (nx.type >= 3u) cs_quant_lds<NT_>(xr, nx.nb, vec);
+        }
+        __syncthreads(); // B2
+        if (live) c = cs_op(ld_op(ops + k), gw, GW), f = 0;
+      }
+      return live;
+    };
+    ItemTree tr;
+    auto step = [&](Item &it) {
+      const u32 ng = c.ng, nblk = 8u * ng, L = c.L, l = lane & (L - 1u), q = lane / L, ni = c.ni;
+      const u32x4 *s_lo = (const u32x4 *)vec, *s_hi = s_lo + nblk;
+      const float *s_d = (const float *)(s_hi + nblk);
+      const u32 *s_as = (const u32 *)(s_d + nblk);
+      const u32 j = f / ni, i = f - j * ni, g = l + L * i, mj = (c.nwr + GW - 1u) / GW;
+      const float leaf = item_dot<KIND>(it, g < ng ? g : 0u, ng, s_lo, s_hi, s_d, s_as, 0.0f);
+      tr.add(seg_sum(g < ng ? leaf : 0.0f, L), i);
+      if (i == ni - 1u && l == 0u) outs[(w * mj + j) * c.rpw + q] = tr.sum(ni);
+      if (tr0 && w == 0u && lane == 0u && nt_ < 64u) tr0[2u + 4u * n + nt_] = __builtin_amdgcn_s_memrealtime();
+      nt_++;
+      cur.issue(it);
+      f++;
+    };
+    for (;;) {
+      if (!next()) break;
+      step(A);
+      if (!next()) break;
+      step(B);
+      if (NBUF == 3) {
+        if (!next()) break;
+        step(C);
+      }
+    }
+    return;
+  }
+  // ---------------- a staging wave (threads tid < 256)
+  {
+    const ChainOp op = ld_op(ops);
+    if (op.type == 0u) cs_quant_op(op, tid);
+    else cs_stage(op, tid, vec, xr);
+  }
+  __syncthreads(); // Bx of the start
+  if (ld_op(ops).type >= 3u) cs_quant_lds<NT_>(xr, ld_op(ops).nb, vec);
+  __syncthreads(); // B2 of the start
+  auto stamp = [&](u32 i) {
+    if (tr0 && tid == 0u) tr0[i] = __builtin_amdgcn_s_memrealtime();
+  };
+  stamp(1u);
+  if (nsync == 0u && tid == 0u && chain_arrive(sync, 1u)) // no grid barrier: the end's arrival now
+    for (u32 g = 0; g < NGRP + 2u; g++) __hip_atomic_store(sync + SYNC_LINE * g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (u32 k = 0; k < n; k++) {
+    const ChainOp op = ld_op(ops + k);
+    const CsOp c = cs_op(op, 0u, GW);
+    __syncthreads(); // B1
+    stamp(2u + 4u * k);
+    if (op.type != 0u) { // the workgroup's results of operation k
+      const __amdgpu_buffer_rsrc_t ry = rsrc(op.y, 4u * c.rows), rb = rsrc(op.bias, 4u * c.rows), rr = rsrc(op.res, 4u * c.rows);
+      const u32 mj = (c.nwr + GW - 1u) / GW, per = mj * c.rpw;
+      for (u32 s = tid; s < CS_NC * per; s += CS_NS * 64u) {
+        const u32 ww = s / per, j = (s - ww * per) / c.rpw, q = s - ww * per - j * c.rpw;
+        const u32 r = ((CS_NC * blockIdx.x + ww) + GW * j) * c.rpw + q;
+        if (r < c.rows) {
+          float o = outs[s];
+          if (op.bias) o = o + __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, 4u * r, 0, CPOL_SC1));
+          if (op.res) o = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, 4u * r, 0, CPOL_SC1)) + o;
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(u32, o), ry, 4u * r, 0, CPOL_SC1);
+        }
+      }
+    }
+    if (k + 1u == n) break; // the end: the stores complete with the launch
+    __builtin_amdgcn_s_waitcnt(0); // this wave's stores (results, quantizations) are complete
+    __syncthreads();               // Bw: ... and those of the other staging waves
+    stamp(3u + 4u * k);
+    if (tid == 0u && op.sync) {
+      nbar++;
+      if (chain_arrive(sync, nbar)) __hip_atomic_store(sync + SYNC_LINE * (NGRP + 1u), nbar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_ok = chain_wait(sync, nbar, spin_ns) ? 1u : 0u;
+      // after the last grid barrier, the end's arrival (the last one sets the counters back to zero)
+      if (s_ok && nbar == nsync && chain_arrive(sync, nbar + 1u))
+        for (u32 g = 0; g < NGRP + 2u; g++) __hip_atomic_store(sync + SYNC_LINE * g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads(); // Br
+    stamp(4u + 4u * k);
+    const bool live = s_ok != 0u;
+    const ChainOp nx = ld_op(ops + k + 1u);
+    if (live) {
+      if (nx.type == 0u) cs_quant_op(nx, tid);
+      else cs_stage(nx, tid, vec, xr);
+    }
+    __syncthreads(); // Bx
+    if (live && nx.type >= 3u) cs_quant_lds<NT_>(xr, nx.nb, vec);
+    __syncthreads(); // B2
+    stamp(5u + 4u * k);
+    if (!live) break;
+  }
+  // an aborted launch leaves the counters as they are: the host reads them
+}
+
+extern "C" __global__ __launch_bounds__(768, 1) void amdc_chain_s_q4_0(const ChainOp *__restrict__ ops, u32 n, u32 *sync, u32 spin_ns, u32 outb,
+                                                                       u32 vecb, u64 *trace) {
+  chain_s_body<AMDC_Q4_0, 2u>(ops, n, sync, spin_ns, outb, vecb, trace);
+}
+extern "C" __global__ __launch_bounds__(768, 1) void amdc_chain_s_q4_k(const ChainOp *__restrict__ ops, u32 n, u32 *sync, u32 spin_ns, u32 outb,
+                                                                       u32 vecb, u64 *trace) {
+  chain_s_body<AMDC_Q4_K, 3u>(ops, n, sync, spin_ns, outb, vecb, trace);
 }
 
 // ------------------------------------------------------------------ bandwidth probes

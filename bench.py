@@ -193,24 +193,20 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
 
     ms_launches, steps_timed = timer.step_ms(step, G.copies, G.set_bytes, steps, warmup)
     # the same step as one GEMV chain launch per weight copy, a grid barrier after each operation
-    # (the next one waits for it, as the launches wait for each other); as amdc_gemv_q4_x, a GEMV
-    # quantizes its f32 input in every workgroup for nb <= 128, else after a quantize operation
-    Qc = amdc.DevBuf(q8_stride(cols_max // 32))
-    chains = []
-    for ci in range(G.copies):
-        ops = []
-        for gi, (name, r, c, _) in enumerate(groups):
-            if c // 32 <= 128:
-                ops.append(amdc.chain_gemv_x(kind, G.dev[ci][gi], X, Y, r, c // 32))
-            else:
-                ops += [amdc.chain_quant(X, Qc, c // 32), amdc.chain_gemv(kind, G.dev[ci][gi], Qc, Y, r, c // 32)]
-        chains.append(amdc.Chain(ops))
-    chains[0].launch()
-    chains[0].check()
-    ms_chain, _ = timer.step_ms(lambda ci, s: chains[ci].launch(s), G.copies, G.set_bytes, steps, warmup)
-    chains[0].check()
-    del chains
-    ms = min(ms_launches, ms_chain)
+    # (the next one waits for it, as the launches wait for each other); each GEMV quantizes its f32
+    # input inside the chain (AMDC_CHAIN_GEMV_X). Both chain kernels: the streaming form (one
+    # workgroup per CU, the next operations' weights in flight across the barriers) and the
+    # persistent form (2 workgroups per CU).
+    ms_chain = {}
+    for form, fm in (("streaming", amdc.CHAIN_STREAMING), ("persistent", amdc.CHAIN_PERSISTENT)):
+        chains = [amdc.Chain([amdc.chain_gemv_x(kind, G.dev[ci][gi], X, Y, r, c // 32) for gi, (name, r, c, _) in enumerate(groups)],
+                             form=fm) for ci in range(G.copies)]
+        chains[0].launch()
+        chains[0].check()
+        ms_chain[form], _ = timer.step_ms(lambda ci, s: chains[ci].launch(s), G.copies, G.set_bytes, steps, warmup)
+        chains[0].check()
+        del chains
+    ms = min(ms_launches, ms_chain["streaming"])
     # each launch of the step alone, the same call as in the step: amdc_gemv_q4_x / _q4k_x (the quantization
     # inside the GEMV where nb <= 128, else amdc_quant_q8 + the GEMV: two launches)
     launches = []
@@ -242,8 +238,9 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
     dom = max(kt, key=lambda k: kt[k][0])
     launch_us = sum(l["us"] for l in launches)
     return {"set_bytes": set_bytes, "ms_per_step": ms, "steps_timed": steps_timed, "ms_per_step_unmerged": ms_unmerged,
-            "ms_per_step_launches": ms_launches, "ms_per_step_chain": ms_chain,
-            "step_form": "chain" if ms_chain <= ms_launches else "launches",
+            "ms_per_step_launches": ms_launches, "ms_per_step_chain": ms_chain["streaming"],
+            "ms_per_step_chain_persistent": ms_chain["persistent"],
+            "step_form": "chain" if ms_chain["streaming"] <= ms_launches else "launches",
             "launches_per_step": len(launches), "per_shape": per, "step_launches": launches,
             "dominant_kernel": dom, "dominant_launches": kt[dom][2],
             "dominant_bytes_per_launch": kt[dom][1] / kt[dom][2], "dominant_us_per_launch": kt[dom][0] / kt[dom][2],

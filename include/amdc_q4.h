@@ -288,7 +288,8 @@ int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kern
  * Operations between two syncs run concurrently: when one writes bytes that
  * another reads or writes, the later one must come after a sync (the check
  * compares the byte ranges of every operand). All workgroups must be resident at
- * once: the grid is what the device holds (at most 2 per CU); nothing else
+ * once: the grid is what the device holds (at most 2 per CU, 1 per CU for the
+ * streaming form); nothing else
  * should run on the device meanwhile. A barrier that waits longer than 200 ms
  * aborts the launch (every workgroup leaves); amdc_chain_check reports it. */
 enum { AMDC_CHAIN_QUANT = 0, AMDC_CHAIN_GEMV = 1, AMDC_CHAIN_GEMV_X = 2 };
@@ -305,6 +306,30 @@ typedef struct {
 /* Validate the list, upload it and the barrier counters (allocates: call
  * before any graph capture); *chain receives the handle. */
 int amdc_chain_create(const amdc_chain_op *ops, uint32_t n, void **chain);
+/* The same with the kernel chosen (no reference counterpart: the reference's
+ * megakernel has one form):
+ *   AMDC_CHAIN_PERSISTENT: 2 workgroups of 256 threads per CU, any kinds;
+ *   AMDC_CHAIN_STREAMING: one workgroup of 768 threads per CU, every GEMV of
+ *     the list Q4_0 or every one Q4_K (else AMDC_EINVAL); work is dealt per
+ *     wave, each wave loads the weights of its next two items while it
+ *     computes, across operations and barriers (a wave waiting at a barrier
+ *     has the next operation's weights in flight), the barriers are split
+ *     (arrive when done, wait before staging the next vector), and an f32
+ *     input is quantized once per CU;
+ *   AMDC_CHAIN_AUTO (amdc_chain_create): the streaming form where it applies.
+ * Both give the same bits as the separate launches. */
+enum { AMDC_CHAIN_AUTO = 0, AMDC_CHAIN_PERSISTENT = 1, AMDC_CHAIN_STREAMING = 2 };
+int amdc_chain_create_form(const amdc_chain_op *ops, uint32_t n, int form, void **chain);
+/* The timeline of the streaming form (the reference's megakernel profiler,
+ * IE_MK_TRACE and IE_MK_PROF, kernels/ie_mk.c:16-19): with buf (device
+ * memory, amdc_chain_trace_words(chain) words; NULL: off) every later launch
+ * records, per workgroup p, at buf + p (2 + 4 n + 64), the 100 MHz clock at:
+ * its start; the first operation's vector staged; for each operation k
+ * (words 2 + 4 k ..) its results in the LDS, their stores complete, the grid
+ * barrier passed, the next vector staged; then (words 2 + 4 n ..) each of
+ * the first 64 items of its first compute wave computed. */
+int amdc_chain_trace(void *chain, uint64_t *buf);
+uint32_t amdc_chain_trace_words(void *chain);
 /* One launch of the whole list on stream (no allocation: can be captured). */
 int amdc_chain_launch(void *chain, void *stream);
 /* Synchronizes the device; AMDC_EHIP if a launch of this chain aborted at a

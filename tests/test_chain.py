@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 from amdc import synth
-from test_gpu_parity import Case, rel_err, TOL, q8_stride
+from test_gpu_parity import Case, rel_err, TOL, q8_stride, ttype as synth_ttype
 
 pytestmark = pytest.mark.gpu
 
@@ -64,12 +64,14 @@ def test_chain_equals_separate_launches(dev, orc):
     assert rel_err(yA, A.y_oracle(0), A.mag(0)) < TOL
 
 
-def test_chain_graph_replay(dev, orc):
+@pytest.mark.parametrize("form", ["persistent", "streaming"])
+def test_chain_graph_replay(dev, orc, form):
     """A chain captured in a HIP graph and replayed, with eager work between replays, equals the eager chain."""
     A = Case(dev, orc, 3, 3000, 160, seed=5)
     x0 = dev.DevBuf.of(A.x[0])
     q0, y = dev.DevBuf(q8_stride(160)), dev.DevBuf(4 * 3000)
-    ch = dev.Chain([dev.chain_quant(x0, q0, 160), dev.chain_gemv(3, A.W, q0, y, 3000, 160)])
+    fm = dev.CHAIN_PERSISTENT if form == "persistent" else dev.CHAIN_STREAMING
+    ch = dev.Chain([dev.chain_quant(x0, q0, 160), dev.chain_gemv(3, A.W, q0, y, 3000, 160)], form=fm)
     ch.launch()
     ch.check()
     want = y.download(np.uint32)
@@ -212,3 +214,155 @@ def test_chain_rejects_f32_input_for_q8_0(dev, orc):
     y = dev.DevBuf(4 * 64)
     with pytest.raises(dev.AmdcError):
         dev.Chain([dev.chain_gemv_x(synth.KIND_Q8_0, A.W, x0, y, 64, 8)])
+
+
+@pytest.mark.parametrize("kind", [0, 3])
+def test_chain_streaming_equals_separate_launches(dev, orc, kind):
+    """The streaming form (one workgroup of 768 threads per CU, each wave's next two items in flight across
+    operations and barriers, split barriers, the f32 input quantized once per CU) on a list of one kind:
+    x0 -> Q8 -> A (Q8 input) -> y1 -> B (f32 input, bias and residual) -> y2 -> C and D (one input, no
+    barrier between them), then E (nb 600: the quantization in several passes) on its own vector. Each
+    output equals amdc_quant_q8 + amdc_gemv bit for bit, across repeated launches; the auto form picks the
+    streaming kernel for such a list, and the streaming form refuses a list of two kinds."""
+    g = np.random.default_rng(17 + kind)
+    nbA = 13 if kind == 0 else 16
+    A = Case(dev, orc, kind, 256, nbA, seed=31)
+    B = Case(dev, orc, kind, 1024, 8, seed=32)
+    C_ = Case(dev, orc, kind, 77, 32, seed=33)
+    D = Case(dev, orc, kind, 300, 32, seed=34)
+    E = Case(dev, orc, kind, 90, 600, seed=35)
+    x0, xe = dev.DevBuf.of(A.x[0]), dev.DevBuf.of(E.x[0])
+    q0 = dev.DevBuf(q8_stride(nbA))
+    y1, y2, y3, y4, y5 = (dev.DevBuf(4 * r) for r in (256, 1024, 77, 300, 90))
+    bias = dev.DevBuf.of(g.standard_normal(1024).astype(np.float32))
+    res = dev.DevBuf.of(g.standard_normal(1024).astype(np.float32))
+    ops = [dev.chain_quant(x0, q0, nbA),
+           dev.chain_gemv(kind, A.W, q0, y1, 256, nbA),
+           dev.chain_gemv_x(kind, B.W, y1, y2, 1024, 8, bias=bias, res=res),
+           dev.chain_gemv_x(kind, C_.W, y2, y3, 77, 32, sync=False),
+           dev.chain_gemv_x(kind, D.W, y2, y4, 300, 32),
+           dev.chain_gemv_x(kind, E.W, xe, y5, 90, 600)]
+    q = dev.DevBuf(q8_stride(600))
+    z0 = dev.DevBuf(q8_stride(nbA))
+    z1, z2, z3, z4, z5 = (dev.DevBuf(4 * r) for r in (256, 1024, 77, 300, 90))
+    dev.quant_q8(x0, z0, nbA)
+    dev.gemv(kind, A.W, z0, z1, 256, nbA)
+    dev.quant_q8(z1, q, 8)
+    dev.gemv(kind, B.W, q, z2, 1024, 8, bias=bias, res=res)
+    dev.quant_q8(z2, q, 32)
+    dev.gemv(kind, C_.W, q, z3, 77, 32)
+    dev.gemv(kind, D.W, q, z4, 300, 32)
+    dev.quant_q8(xe, q, 600)
+    dev.gemv(kind, E.W, q, z5, 90, 600)
+    want = [b.download(np.uint32) for b in (z0, z1, z2, z3, z4, z5)]
+    for fm in (dev.CHAIN_STREAMING, dev.CHAIN_AUTO):
+        ch = dev.Chain(ops, form=fm)
+        for rep in range(3):
+            for b in (q0, y1, y2, y3, y4, y5):
+                b.fill(0)
+            ch.launch()
+            ch.check()
+            got = [b.download(np.uint32) for b in (q0, y1, y2, y3, y4, y5)]
+            assert np.array_equal(got[0][:10 * nbA], want[0][:10 * nbA]), (fm, rep)
+            for i in range(1, 6):
+                assert np.array_equal(got[i], want[i]), (fm, rep, i)
+        del ch
+    assert rel_err(y5.download(np.float32), E.y_oracle(0), E.mag(0)) < TOL
+    other = Case(dev, orc, 3 - kind, 64, 8, seed=36)
+    with pytest.raises(dev.AmdcError, match="streaming form"):
+        dev.Chain(ops + [dev.chain_gemv_x(3 - kind, other.W, x0, y3, 64, 8)], form=dev.CHAIN_STREAMING)
+
+
+MODEL_CHAINS = {
+    # (kind, [(name, rows, cols)]): each GEMV reads the previous one's output (its first cols values)
+    "c1": (0, [("qkv", 12288, 4096), ("o", 4096, 4096), ("gate_up", 22016, 4096), ("down", 4096, 11008), ("lm_head", 32000, 4096)]),
+    "c2": (3, [("gate_up", 34816, 5120), ("down", 5120, 17408), ("attn_in", 6144, 5120), ("attn_out", 5120, 6144),
+               ("lm_head", 152064, 5120)]),
+}
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c2"])
+@pytest.mark.parametrize("form", ["persistent", "streaming"])
+def test_chain_model_shapes(dev, orc, cfg, form):
+    """A decode step's GEMVs at the c1 (Q4_0, Llama-7B) and c2 (Q4_K, 27B) shapes as one chain of dependent
+    operations: each GEMV quantizes the previous GEMV's output (its first cols values) in the chain
+    (AMDC_CHAIN_GEMV_X) and waits for it at a barrier, so a missing or early barrier changes the result.
+    The waves hold up to about 25 items each (the 152064-row lm_head), so the streaming form's weight
+    loads run ahead across every operation boundary. Every output equals amdc_quant_q8 + amdc_gemv bit for
+    bit over three launches; the first and last GEMVs also match the oracle."""
+    kind, shapes = MODEL_CHAINS[cfg]
+    fm = dev.CHAIN_PERSISTENT if form == "persistent" else dev.CHAIN_STREAMING
+    cases = [Case(dev, orc, kind, r, c // 32, seed=40 + i) for i, (_, r, c) in enumerate(shapes)]
+    x0 = dev.DevBuf.of(cases[0].x[0])
+    ys = [dev.DevBuf(4 * r) for _, r, _ in shapes]
+    ops, src = [], x0
+    for i, (_, r, c) in enumerate(shapes):
+        ops.append(dev.chain_gemv_x(kind, cases[i].W, src, ys[i], r, c // 32))
+        src = ys[i]
+    q = dev.DevBuf(q8_stride(max(c for _, _, c in shapes) // 32))
+    zs = [dev.DevBuf(4 * r) for _, r, _ in shapes]
+    src = x0
+    for i, (_, r, c) in enumerate(shapes):
+        dev.quant_q8(src, q, c // 32)
+        dev.gemv(kind, cases[i].W, q, zs[i], r, c // 32)
+        src = zs[i]
+    want = [z.download(np.uint32) for z in zs]
+    ch = dev.Chain(ops, form=fm)
+    for rep in range(3):
+        for y in ys:
+            y.fill(0)
+        ch.launch()
+        ch.check()
+        for i, y in enumerate(ys):
+            assert np.array_equal(y.download(np.uint32), want[i]), (rep, shapes[i][0])
+    del ch
+    # the first GEMV against the oracle; the last one on the oracle's quantization of its real input
+    assert rel_err(ys[0].download(np.float32), cases[0].y_oracle(0), cases[0].mag(0)) < TOL
+    last = cases[-1]
+    xin = ys[-2].download(np.float32)[:32 * last.nb][None, :]
+    xq = orc.quant_q8(xin)[0]
+    yref = orc.gemv(synth_ttype(kind), last.qw, last.qs, last.rows, last.nb, xq, threads=16)
+    mag = orc.gemv_f64(synth_ttype(kind), last.src, last.rows, last.nb, xq)[1]
+    assert rel_err(ys[-1].download(np.float32), yref, mag) < TOL
+
+
+def test_chain_trace(dev, orc):
+    """amdc_chain_trace (the streaming form's timeline, as the reference megakernel's IE_MK_TRACE): every
+    workgroup records its start, the first vector staged and the four boundary points of every operation
+    in order, and the first compute wave's item times; the results do not change; the persistent form
+    refuses a timeline."""
+    A = Case(dev, orc, 0, 4096, 128, seed=51)
+    B = Case(dev, orc, 0, 1000, 128, seed=52)
+    x0 = dev.DevBuf.of(A.x[0])
+    y1, y2 = dev.DevBuf(4 * 4096), dev.DevBuf(4 * 1000)
+    ops = [dev.chain_gemv_x(0, A.W, x0, y1, 4096, 128), dev.chain_gemv_x(0, B.W, y1, y2, 1000, 128)]
+    ch = dev.Chain(ops, form=dev.CHAIN_STREAMING)
+    ch.launch()
+    ch.check()
+    want = y2.download(np.uint32)
+    nw = ch.trace_words()
+    grid = dev.cu_count()
+    n, per = 2, 2 + 4 * 2 + 64
+    assert nw == grid * per
+    TB = dev.DevBuf(8 * nw)
+    TB.fill(0)
+    ch.trace(TB)
+    ch.launch()
+    ch.check()
+    ch.trace(None)
+    assert np.array_equal(y2.download(np.uint32), want)
+    t = TB.download(np.uint64).reshape(grid, per).astype(np.int64)
+    # start, B2 of the start, op 0: B1 Bw Br B2, op 1: B1 (the last operation records only B1)
+    marks = t[:, [0, 1, 2, 3, 4, 5, 6]]
+    assert (marks > 0).all()
+    assert (np.diff(marks, axis=1) >= 0).all()
+    # every workgroup passed the grid barrier after every workgroup's stores of op 0 completed
+    assert marks[:, 4].min() >= marks[:, 3].max()
+    items = t[:, 2 + 4 * n:]
+    # the first compute wave of workgroup b is wave 8 b of the grid's compute waves: it has items of op 0
+    # (4096 rows of 4 per wave: 1024 wave row groups) for 8 b < 1024
+    nb_ = min(grid, 128)
+    assert (items[:nb_, 0] > 0).all() and (items[grid:, 0] if grid > 128 else items[:0, 0]).size == 0
+    ch2 = dev.Chain(ops, form=dev.CHAIN_PERSISTENT)
+    with pytest.raises(dev.AmdcError, match="timeline"):
+        ch2.trace(TB)
