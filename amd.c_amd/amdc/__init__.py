@@ -370,8 +370,8 @@ def gemv(kind, w, xq, y, rows, nb, bias=None, res=None, stream=None):
 
 
 def gemv_x(kind, w, x, y, rows, nb, bias=None, res=None, q8=None, stream=None):
-    """Decode GEMV on the f32 vector x (quantized in the kernel for nb <= 128, else quantize + GEMV;
-    q8: optional Q8 output)."""
+    """Decode GEMV on the f32 vector x (quantized in the kernel where a workgroup per CU holds the rows or
+    nb <= 128, else quantize + GEMV; q8: optional Q8 output)."""
     f = getattr(lib(), f"amdc_gemv_{_SUF[kind]}_x")
     _check(f(_p(w), _p(x), _p(y), rows, nb, _p(bias), _p(res), _p(q8), stream))
 

@@ -275,7 +275,8 @@ enum {
   K_GEMVXS_Q4 = K_GEMVS_Q4 + 8, /* amdc_gemv_q4_0_xs1 .. _xs4, then amdc_gemv_q4_k_xs1 .. _xs4 */
   K_GEMVM_Q4 = K_GEMVXS_Q4 + 8, /* amdc_gemv_q4_0_m1, amdc_gemv_q4_k_m1 */
   K_CHAIN_S = K_GEMVM_Q4 + 2, /* amdc_chain_s_q4_0, amdc_chain_s_q4_k */
-  K_N = K_CHAIN_S + 2
+  K_GEMVXW_Q4 = K_CHAIN_S + 2, /* amdc_gemv_q4_0_xw1, amdc_gemv_q4_k_xw1, _xw2 */
+  K_N = K_GEMVXW_Q4 + 3
 };
 static const char *const kname[K_N] = {
     "amdc_quant_q8",           "amdc_dots_q4_0",          "amdc_dots_q4_k",          "amdc_gemm_q4_k_n128",
@@ -292,7 +293,8 @@ static const char *const kname[K_N] = {
     "amdc_gemv_q4_k_s1",       "amdc_gemv_q4_k_s2",       "amdc_gemv_q4_k_s3",       "amdc_gemv_q4_k_s4",
     "amdc_gemv_q4_0_xs1",      "amdc_gemv_q4_0_xs2",      "amdc_gemv_q4_0_xs3",      "amdc_gemv_q4_0_xs4",
     "amdc_gemv_q4_k_xs1",      "amdc_gemv_q4_k_xs2",      "amdc_gemv_q4_k_xs3",      "amdc_gemv_q4_k_xs4",
-    "amdc_gemv_q4_0_m1",       "amdc_gemv_q4_k_m1",       "amdc_chain_s_q4_0",       "amdc_chain_s_q4_k"};
+    "amdc_gemv_q4_0_m1",       "amdc_gemv_q4_k_m1",       "amdc_chain_s_q4_0",       "amdc_chain_s_q4_k",
+    "amdc_gemv_q4_0_xw1",      "amdc_gemv_q4_k_xw1",      "amdc_gemv_q4_k_xw2"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -835,13 +837,38 @@ static int gemv_t(int kind, const char *op, const void *w, const uint8_t *xq, fl
   return rc;
 }
 
-/* The decode GEMV of an f32 input: for nb <= x_fuse_nb (128 by default)
- * one launch whose workgroups quantize the vector in their prologue (the
- * quantization then hides under the weight loads); for larger nb, where that
- * prologue costs more than a launch, amdc_quant_q8 into q8 (or the library's
- * workspace when q8 is NULL) and the GEMV. Measured on MI355X (single-shot
- * kernels): 4096 x 4096 Q4_0 4.5 us fused against 6.0 us for the two
- * launches, 12288 x 4096 7.9 against 8.8, 22016 x 4096 11.8 against 12.2. */
+/* The decode GEMV of an f32 input: where one workgroup can hold a CU's share
+ * of the rows (gemvxw_pick), one launch of about one workgroup per CU that
+ * quantizes the vector once per CU in its prologue; else, for nb <= x_fuse_nb
+ * (128 by default), one launch whose 256-thread workgroups quantize the
+ * vector in their prologue (the quantization then hides under the weight
+ * loads); for larger nb, where that prologue costs more than a launch,
+ * amdc_quant_q8 into q8 (or the library's workspace when q8 is NULL) and the
+ * GEMV. Measured on MI355X (single-shot kernels): 4096 x 4096 Q4_0 4.5 us
+ * fused against 6.0 us for the two launches, 12288 x 4096 7.9 against 8.8,
+ * 22016 x 4096 11.8 against 12.2. */
+/* The workgroup-per-CU form of the fused quantization (amdc_gemv_q4_0_xw1, amdc_gemv_q4_k_xw1 /
+ * _xw2): the lanes per row L, super-groups per lane ni and threads nth such that one workgroup
+ * holds the rows of one CU's share, for more than 4 and at most 16 waves (Q4_0: one super-group
+ * per lane only); 0 when no such size exists (the 256-thread kernels then). Measured on MI355X, f32
+ * input, Q4_0 (us, this form / the 256-thread kernels): 12288 x 4096 7.6 / 8.4, 4096 x 11008 9.3 /
+ * 10.7 (there against a separate quantization launch); 22016 x 4096 on two super-groups per lane
+ * 12.7 / 12.3 (not taken). */
+static int gemvxw_pick(int kind, u32 ng, u32 rows, u32 *L, u32 *ni, u32 *nth) {
+  const u32 cus = g_cus > 0 ? (u32)g_cus : 256u, rpc = (rows + cus - 1u) / cus;
+  for (u32 n = 1u; n <= (kind == AMDC_KIND_Q4_0 ? 1u : 2u); n++) {
+    u32 l = 4u;
+    while (l < 64u && l * n < ng) l <<= 1;
+    if ((ng + l - 1u) / l != n) continue;
+    const u32 rpw = 64u / l, waves = (rpc + rpw - 1u) / rpw;
+    if (waves > 4u && waves <= 16u) {
+      *L = l, *ni = n, *nth = 64u * waves;
+      return 1;
+    }
+  }
+  return 0;
+}
+
 static int gemv_x(int kind, const char *op, const void *w, const float *x, float *y, uint32_t rows, uint32_t nb, const float *bias,
                   const float *res, uint8_t *q8, void *stream) {
   NEED_OPEN();
@@ -849,6 +876,13 @@ static int gemv_x(int kind, const char *op, const void *w, const float *x, float
   if (rc) return rc;
   if (q8 && !aligned16(q8)) return fail(AMDC_EINVAL, "%s: q8 must be 16-byte aligned", op);
   const u32 ng = amdc_ngroups(nb), L = gemv_lanes(ng), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
+  u32 Lw, niw, nthw;
+  if ((kind == AMDC_KIND_Q4_0 || kind == AMDC_KIND_Q4_K) && (t_form == 0 || t_form == 3) && t_lanes <= 0 && t_wgs <= 0 &&
+      320u * ng <= GEMV_LDS_T1 && gemvxw_pick(kind, ng, rows, &Lw, &niw, &nthw)) {
+    const u32 rpgw = (nthw / 64u) * (64u / Lw), gw = (rows + rpgw - 1u) / rpgw;
+    void *a[] = {&w, &x, &y, &rows, &nb, &bias, &res, (void *)&Lw, &q8};
+    return launch_nt(kind == AMDC_KIND_Q4_K ? K_GEMVXW_Q4 + (int)niw : K_GEMVXW_Q4, gw, 1, nthw, 320u * ng, stream, a);
+  }
   if (nb > x_fuse_nb || 320u * ng > GEMV_LDS_T1 || kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) {
     if (!q8) {
       if ((rc = ws_take((size_t)40u * nb + 64u, (void **)&q8))) return rc;

@@ -166,6 +166,15 @@ __device__ __forceinline__ u32 q4k_sc(u32x4 h, u32 k) { return (u32)((((u64)h.z 
 __device__ __forceinline__ u32 q4k_mn(u32x4 h, u32 k) { return (u32)((((u64)h.w << 32) | h.z) >> (16u + 6u * k)) & 63u; }
 __device__ __forceinline__ u32 hword(u32x4 h, u32 i) { return i == 0 ? h.x : i == 1 ? h.y : i == 2 ? h.z : h.w; }
 
+// q = roundf(x / d) for the 4 values of a lane (IEEE division, rounded half
+// away from zero; 0 for d = 0). A division-free form (the reciprocal, and the
+// division only for quotients within 2^-15 of a half-integer) measured slower
+// on MI355X (the c1 step 49.8 against 48.6 us).
+__device__ __forceinline__ void q8_round4(const v4f &x, float d, int (&qi)[4]) {
+#pragma unroll
+  for (int m = 0; m < 4; m++) qi[m] = d != 0.0f ? (int)__builtin_roundf(x[m] / d) : 0;
+}
+
 // ------------------------------------------------------------------ Q8 quantization
 
 // One 32-lane half of a wave per block of 32: amax by xor shuffles inside
@@ -381,12 +390,13 @@ __device__ __forceinline__ float item_dot(const typename ItemOf<KIND>::type &it,
 // by DPP (xor 1, xor 2, then the half-row mirror).
 template <u32 NC, u32 NTH = NT> struct FusedQ8T {
   static constexpr u32 BP = NTH / 8u; // blocks per pass
+  u32 bp = BP;                         // ... at run time (a workgroup of blockDim.x < NTH threads: blockDim.x / 8)
   v4f xv[NC];
   __device__ __forceinline__ void load(const float *__restrict__ xf, u32 nb, u32 b0) {
     const u32 tid = threadIdx.x, e = tid & 7u;
 #pragma unroll
     for (u32 c = 0; c < NC; c++) {
-      const u32 b = b0 + BP * c + (tid >> 3);
+      const u32 b = b0 + bp * c + (tid >> 3);
       const v4f v = *(const v4f *)(xf + 32u * (b < nb ? b : nb - 1u) + 4u * e);
       xv[c] = b < nb ? v : (v4f){0.0f, 0.0f, 0.0f, 0.0f};
     }
@@ -395,8 +405,8 @@ template <u32 NC, u32 NTH = NT> struct FusedQ8T {
     const u32 tid = threadIdx.x, e = tid & 7u, nblk = 8u * ng;
 #pragma unroll
     for (u32 c = 0; c < NC; c++) {
-      if (b0 + BP * c >= nblk) break;
-      const u32 b = b0 + BP * c + (tid >> 3);
+      if (b0 + bp * c >= nblk) break;
+      const u32 b = b0 + bp * c + (tid >> 3);
       float a = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(xv[c].x), __builtin_fabsf(xv[c].y)),
                                 __builtin_fmaxf(__builtin_fabsf(xv[c].z), __builtin_fabsf(xv[c].w)));
       a = __builtin_fmaxf(a, dpp<0xB1>(a));
@@ -404,8 +414,7 @@ template <u32 NC, u32 NTH = NT> struct FusedQ8T {
       a = __builtin_fmaxf(a, dpp<0x141>(a));
       const float d = a / 127.0f;
       int qi[4];
-#pragma unroll
-      for (int m = 0; m < 4; m++) qi[m] = d != 0.0f ? (int)__builtin_roundf(xv[c][m] / d) : 0;
+      q8_round4(xv[c], d, qi);
       const u32 word = (u32)(qi[0] & 255) | (u32)(qi[1] & 255) << 8 | (u32)(qi[2] & 255) << 16 | (u32)qi[3] << 24;
       u32 sum = (u32)qi[0] + (u32)qi[1] + (u32)qi[2] + (u32)qi[3];
       sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0xB1, 0xF, 0xF, false);
@@ -527,13 +536,16 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_x1(const uint8_
 // of a whole matrix are resident at once and the arithmetic of one overlaps
 // the loads of the others. Lane split, LDS layout, block arithmetic and
 // summation order are those of gemv1_body (bit-equal results).
-template <int KIND, u32 NI, bool FQ, u32 NTH>
+// QCN > 0 (the xw kernels): QCN passes of quantization loads in flight, and
+// the workgroup's size taken at run time (blockDim.x <= NTH threads).
+template <int KIND, u32 NI, bool FQ, u32 NTH, u32 QCN = 0u>
 __device__ __forceinline__ void gemvs_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
                                            u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 L,
                                            const float *__restrict__ xf = nullptr, uint8_t *__restrict__ q8out = nullptr) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const u32 nth = QCN ? blockDim.x : NTH;
   const u32 ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
-  const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = (NTH / 64u) * rpw;
+  const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = (nth / 64u) * rpw;
   const u64 RB = amdc_row_bytes(nb);
   const u32 nblk = 8u * ng;
   u32x4 *s_lo = (u32x4 *)smem;
@@ -542,8 +554,9 @@ __device__ __forceinline__ void gemvs_body(const uint8_t *__restrict__ W, const 
   u32 *s_as = (u32 *)(s_d + nblk);
   const u32 r = blockIdx.x * rpg + wv * rpw + q;
   const uint8_t *wr = W + (u64)(r < rows ? r : rows - 1u) * RB;
-  constexpr u32 QC = (QCH * NT) / NTH; // passes in flight: 128 blocks
+  constexpr u32 QC = QCN ? QCN : (QCH * NT) / NTH; // passes in flight: 128 blocks (QCN: QCN passes of nth / 8 blocks)
   FusedQ8T<QC, NTH> fq;
+  fq.bp = nth / 8u;
   if (FQ) {
     fq.load(xf, nb, 0);
     __asm__ volatile("" ::: "memory"); // the activation loads ahead of the weight loads
@@ -553,7 +566,7 @@ __device__ __forceinline__ void gemvs_body(const uint8_t *__restrict__ W, const 
   for (u32 i = 0; i < NI; i++) load_item<KIND>(it[i], wr, ng, l + L * i, l + L * i < ng);
   if (FQ) {
     fq.quant(0, nb, ng, s_lo, s_hi, s_d, s_as, q8out);
-    for (u32 b0 = fq.BP * QC; b0 < nblk; b0 += fq.BP * QC) {
+    for (u32 b0 = fq.bp * QC; b0 < nblk; b0 += fq.bp * QC) {
       fq.load(xf, nb, b0);
       fq.quant(b0, nb, ng, s_lo, s_hi, s_d, s_as, q8out);
     }
@@ -607,6 +620,24 @@ GEMVS_KERNELS(q4_k, AMDC_Q4_K, 1, s, 256)
 GEMVS_KERNELS(q4_k, AMDC_Q4_K, 2, s, 256)
 GEMVS_KERNELS(q4_k, AMDC_Q4_K, 3, s, 256)
 GEMVS_KERNELS(q4_k, AMDC_Q4_K, 4, s, 256)
+
+// The single-shot form with the quantization fused, sized to one workgroup per
+// CU (amdc_gemv_q4_0_xw1, amdc_gemv_q4_k_xw1 / _xw2: blockDim.x threads, up
+// to 1024; the host picks the size so that the grid is about one workgroup
+// per CU; a Q4_0 two-item form measured slower than 256-thread workgroups on
+// 22016 x 4096 and is not built): the vector
+// is quantized once per CU instead of once per 16 or 32 rows, by every
+// thread, with up to 4 passes of blockDim.x / 8 blocks loaded at once (ahead
+// of the weight loads). Same lane split and arithmetic: bit-equal results.
+#define GEMVXW_KERNEL(KN, KIND, NI, NTH)                                                                                             \
+  extern "C" __global__ __launch_bounds__(NTH) void amdc_gemv_##KN##_xw##NI(const uint8_t *W, const float *x, float *y, u32 rows,  \
+                                                                            u32 nb, const float *bias, const float *res, u32 L,   \
+                                                                            uint8_t *q8) {                                        \
+    gemvs_body<KIND, NI, true, NTH, 4u>(W, nullptr, y, rows, nb, bias, res, L, x, q8);                                             \
+  }
+GEMVXW_KERNEL(q4_0, AMDC_Q4_0, 1, 1024)
+GEMVXW_KERNEL(q4_k, AMDC_Q4_K, 1, 1024)
+GEMVXW_KERNEL(q4_k, AMDC_Q4_K, 2, 1024)
 
 // The multi-vector GEMV of a few vectors (T <= 8: the MTP verify step) on
 // the decode kernel's integer dots (amdc_gemv_*_m<NI>): the single-shot split
@@ -1117,8 +1148,7 @@ __device__ __forceinline__ void chain_quant(const ChainOp &op) {
     a = __builtin_fmaxf(a, dpp<0x141>(a));
     const float d = a / 127.0f;
     int qi[4];
-#pragma unroll
-    for (int m = 0; m < 4; m++) qi[m] = d != 0.0f ? (int)__builtin_roundf(v[m] / d) : 0;
+    q8_round4(v, d, qi);
     const u32 word = (u32)(qi[0] & 255) | (u32)(qi[1] & 255) << 8 | (u32)(qi[2] & 255) << 16 | (u32)qi[3] << 24;
     u32 sum = (u32)qi[0] + (u32)qi[1] + (u32)qi[2] + (u32)qi[3];
     sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0xB1, 0xF, 0xF, false);
@@ -1299,8 +1329,7 @@ __device__ __forceinline__ void cs_quant_op(const ChainOp &op, u32 t) {
     a = __builtin_fmaxf(a, dpp<0x141>(a));
     const float d = a / 127.0f;
     int qi[4];
-#pragma unroll
-    for (int m = 0; m < 4; m++) qi[m] = d != 0.0f ? (int)__builtin_roundf(v[m] / d) : 0;
+    q8_round4(v, d, qi);
     const u32 word = (u32)(qi[0] & 255) | (u32)(qi[1] & 255) << 8 | (u32)(qi[2] & 255) << 16 | (u32)qi[3] << 24;
     u32 sum = (u32)qi[0] + (u32)qi[1] + (u32)qi[2] + (u32)qi[3];
     sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0xB1, 0xF, 0xF, false);
@@ -1373,8 +1402,7 @@ __device__ __forceinline__ void cs_quant_lds(const float *xr, u32 nb, uint8_t *v
     a = __builtin_fmaxf(a, dpp<0x141>(a));
     const float d = a / 127.0f;
     int qi[4];
-#pragma unroll
-    for (int m = 0; m < 4; m++) qi[m] = d != 0.0f ? (int)__builtin_roundf(x[m] / d) : 0;
+    q8_round4(x, d, qi);
     const u32 word = (u32)(qi[0] & 255) | (u32)(qi[1] & 255) << 8 | (u32)(qi[2] & 255) << 16 | (u32)qi[3] << 24;
     u32 sum = (u32)qi[0] + (u32)qi[1] + (u32)qi[2] + (u32)qi[3];
     sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0xB1, 0xF, 0xF, false);

@@ -207,26 +207,18 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
         chains[0].check()
         del chains
     ms = min(ms_launches, ms_chain["streaming"])
-    # each launch of the step alone, the same call as in the step: amdc_gemv_q4_x / _q4k_x (the quantization
-    # inside the GEMV where nb <= 128, else amdc_quant_q8 + the GEMV: two launches)
+    # each launch of the step alone, the same call as in the step: amdc_gemv_q4_x / _q4k_x (the library
+    # quantizes inside the GEMV where it can, else amdc_quant_q8 + the GEMV: two launches in one record)
     launches = []
     for gi, (name, r, c, _) in enumerate(groups):
         nb, b = c // 32, wbytes(r, c, kind)
-        if nb <= 128:
-            amdc.gemv_x(kind, G.dev[0][gi], X, Y, r, nb)
-            kname = amdc.last_kernel()  # the kernel the library picked for this shape
-            t = timer.per_launch_ms(lambda j, s, gi=gi, r=r, nb=nb: amdc.gemv_x(kind, G.dev[j % G.copies][gi], X, Y, r, nb, stream=s),
-                                    G.copies, reps=max(2, steps // 4))
-            launches.append(launch_rec(name, kname, r, c, b, t))
-        else:
-            tq = timer.per_launch_ms(lambda j, s, nb=nb: amdc.quant_q8(X, Q, nb, stream=s), 64)
-            launches.append(launch_rec(name + " (input)", "amdc_quant_q8", 1, c, 0, tq))
-            amdc.quant_q8(X, Q, nb)
-            amdc.gemv(kind, G.dev[0][gi], Q, Y, r, nb)
-            kname = amdc.last_kernel()
-            t = timer.per_launch_ms(lambda j, s, gi=gi, r=r, nb=nb: amdc.gemv(kind, G.dev[j % G.copies][gi], Q, Y, r, nb, stream=s),
-                                    G.copies, reps=max(2, steps // 4))
-            launches.append(launch_rec(name, kname, r, c, b, t))
+        amdc.gemv_x(kind, G.dev[0][gi], X, Y, r, nb)
+        kname = amdc.last_kernel()  # the kernel the library picked for this shape
+        if "_x" not in kname:  # the fused forms are amdc_gemv_*_x1 / _xs<n> / _xw<n>
+            kname = "amdc_quant_q8 + " + kname
+        t = timer.per_launch_ms(lambda j, s, gi=gi, r=r, nb=nb: amdc.gemv_x(kind, G.dev[j % G.copies][gi], X, Y, r, nb, stream=s),
+                                G.copies, reps=max(2, steps // 4))
+        launches.append(launch_rec(name, kname, r, c, b, t))
     set_bytes = G.set_bytes
     del G
     kt = {}
@@ -526,7 +518,7 @@ def measure_traffic(seed, kernel):
                 vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
         shutil.rmtree(d, ignore_errors=True)
         cal = vals.get("amdc_probe_copy")
-        mine = vals.get(kernel)
+        mine = vals.get(kernel.split(" + ")[-1])  # a quantize + GEMV record: the GEMV's counters
         if not cal or not mine:
             return None, f"{ctr}: no dispatches of amdc_probe_copy / {kernel} in the counter output"
         scale = CAL_BYTES / (sum(cal) / len(cal) * 1024.0)

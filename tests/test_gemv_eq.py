@@ -67,6 +67,31 @@ def test_decode_forms_equal(dev, kind, rows, nb):
         dev.set_tuning()
 
 
+# shapes whose f32-input GEMV takes the workgroup-per-CU kernels (amdc_gemv_*_xw1 / _xw2: 5 to 16 waves
+# of rows per CU on 256 CUs): ragged row counts, a partial super-group, long rows (344 and 544 blocks:
+# the quantization in one and in two load batches), with bias and residual
+XW_SHAPES = [(0, 5003, 128), (0, 12288, 128), (0, 4096, 344), (0, 3001, 344), (0, 30000, 13), (3, 6144, 160), (3, 5121, 192),
+             (3, 3000, 544)]
+
+
+@pytest.mark.parametrize("kind,rows,nb", XW_SHAPES)
+def test_gemv_x_workgroup_per_cu(dev, kind, rows, nb):
+    """gemv_x on the workgroup-per-CU fused-quantization kernels equals quant_q8 + gemv bit for bit (the
+    Q8 copy too), with and without bias and residual."""
+    W, X, Q, xs = setup(dev, kind, rows, nb, 1, seed=5 * rows + nb)
+    g = np.random.default_rng(rows)
+    B = dev.DevBuf.of(g.standard_normal(rows).astype(np.float32))
+    R = dev.DevBuf.of(g.standard_normal(rows).astype(np.float32))
+    Y, Y2, Q2 = dev.DevBuf(4 * rows), dev.DevBuf(4 * rows), dev.DevBuf(xs)
+    for bias, res in ((None, None), (B, R)):
+        dev.gemv(kind, W, Q, Y, rows, nb, bias=bias, res=res)
+        Y2.fill(0xFF)
+        Q2.fill(0)
+        dev.gemv_x(kind, W, X, Y2, rows, nb, bias=bias, res=res, q8=Q2)
+        assert np.array_equal(Y2.download(np.uint32), Y.download(np.uint32)), (bias is None,)
+        assert np.array_equal(Q2.download(np.uint8)[:40 * nb], Q.download(np.uint8)[:40 * nb])
+
+
 @pytest.mark.parametrize("kind,rows,nb", SHAPES)
 def test_verify_equals_decode(dev, kind, rows, nb):
     """gemv_t (T = 1..16, every K split the host can take, bias and residual) gives each token the bits of
@@ -95,3 +120,53 @@ def test_verify_equals_decode(dev, kind, rows, nb):
                 assert same.all(), (ks, Tn, int((~same).sum()))
     finally:
         dev.set_tuning()
+
+
+def halfway_vector(nb, seed):
+    """Activations whose quotients x / d fall on and next to the half-integers, where a quantization that
+    does not divide could round the other way: per block, amax 127 d for a random or a unit d, and the
+    other values (k + 0.5) d, moved by 0..3 ulp either way; some blocks with a tiny d (1e-39 .. 1e-30:
+    a denormal amax and the reciprocal's range)."""
+    g = np.random.default_rng(seed)
+    x = np.zeros((nb, 32), np.float32)
+    for b in range(nb):
+        d = np.float32(1.0) if b % 3 == 0 else np.float32(g.uniform(0.01, 50.0))
+        if b % 7 == 6:
+            d = np.float32(10.0 ** g.uniform(-41, -32))
+        x[b, 0] = np.float32(127.0) * d
+        k = g.integers(-127, 127, 31).astype(np.float32) + np.float32(0.5)
+        v = (k * d).astype(np.float32)
+        steps = g.integers(-3, 4, 31)
+        v = np.array([np.float32(np.nextafter(vi, np.float32(np.inf) if s > 0 else np.float32(-np.inf))) if s else vi
+                      for vi, s in zip(v, steps)], np.float32)
+        for _ in range(2):  # up to 3 ulp
+            v = np.where(np.abs(steps) > 1, np.nextafter(v, np.where(steps > 0, np.inf, -np.inf).astype(np.float32)), v)
+            steps = np.sign(steps) * np.maximum(np.abs(steps) - 1, 0)
+        x[b, 1:] = np.clip(v, -np.float32(127.0) * d, np.float32(127.0) * d)
+        g.shuffle(x[b])
+    return x.reshape(-1)
+
+
+@pytest.mark.parametrize("kind,rows,nb", [(0, 200, 128), (0, 12288, 128), (0, 4096, 344), (3, 6144, 160)])
+def test_fused_quant_halfway(dev, orc, kind, rows, nb):
+    """The fused quantizations (the GEMV prologue of the 256-thread and workgroup-per-CU kernels, and the
+    streaming chain's) give the bits of the oracle's quantization (the reference's IEEE division and
+    roundf) on values at and next to the rounding boundaries, and tiny scales."""
+    x = halfway_vector(nb, seed=rows + nb)
+    want = orc.quant_q8(x[None, :])[0]
+    src = synth.gguf(kind, rows, 32 * nb, seed=rows)
+    W = dev.DevBuf.of(dev.repack(kind, src, rows, 32 * nb))
+    X = dev.DevBuf.of(x)
+    Q, Qs = dev.DevBuf(q8_stride(nb)), dev.DevBuf(q8_stride(nb))
+    Y, Y2, Y3 = dev.DevBuf(4 * rows), dev.DevBuf(4 * rows), dev.DevBuf(4 * rows)
+    Q.fill(0)
+    dev.gemv_x(kind, W, X, Y, rows, nb, q8=Q)
+    assert np.array_equal(Q.download(np.uint8)[:40 * nb], want)
+    dev.quant_q8(X, Qs, nb)
+    assert np.array_equal(Qs.download(np.uint8)[:40 * nb], want)
+    dev.gemv(kind, W, Qs, Y2, rows, nb)
+    assert np.array_equal(Y.download(np.uint32), Y2.download(np.uint32))
+    ch = dev.Chain([dev.chain_gemv_x(kind, W, X, Y3, rows, nb)], form=dev.CHAIN_STREAMING)
+    ch.launch()
+    ch.check()
+    assert np.array_equal(Y3.download(np.uint32), Y2.download(np.uint32))
