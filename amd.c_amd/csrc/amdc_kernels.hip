@@ -2282,6 +2282,14 @@ __device__ __forceinline__ void v8_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// The column swizzle of the verify kernels' B operands in the LDS (sB[..][pair
+// p + 4 k][quarter q][column]): column n of (k, q) sits at n ^ v8_bswz(k, q).
+// The staging writes of 16 consecutive threads (the 8 blocks k of a
+// super-group, both 16-byte halves) then land in 16 distinct 16-byte columns
+// instead of one (a 16-way bank conflict), and a quarter-wave's reads of one
+// (k, q) stay a permutation of 16 consecutive columns.
+__device__ __forceinline__ u32 v8_bswz(u32 k, u32 q) { return ((k << 1) | (q & 1u)) & 15u; }
+
 template <int KIND, int NS, int NH>
 __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
                                            u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 xs, u32 ys,
@@ -2392,7 +2400,8 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
 #pragma unroll
     for (u32 c = 0; c < 4u * NH; c++) { // block (gl, k) of token tok: quarter 2 (gl & 1) + half of column tok % 8 + 8 (gl & 1)
       const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, gl = bl >> 3, k = bl & 7u;
-      sB[tok >> 3][(gl >> 1) + 4u * k][2u * (gl & 1u) + half][(tok & 7u) + 8u * (gl & 1u)] = ra4[c];
+      const u32 q_ = 2u * (gl & 1u) + half;
+      sB[tok >> 3][(gl >> 1) + 4u * k][q_][((tok & 7u) + 8u * (gl & 1u)) ^ v8_bswz(k, q_)] = ra4[c];
     }
 #pragma unroll
     for (u32 c = 0; c < 2u * NH; c++) {
@@ -2419,7 +2428,7 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
       const u32x4 a = KIND == AMDC_Q8_0 ? wq : (wq >> (4u * (h & 1u))) & 0x0F0F0F0Fu;
 #pragma unroll
       for (u32 th = 0; th < (u32)NH; th++) {
-        const u32x4 bq = sB[th][p + 4u * k][h][n];
+        const u32x4 bq = sB[th][p + 4u * k][h][n ^ v8_bswz(k, h)];
         c[th][p & 1u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, bq), (v4i){0, 0, 0, 0}, 0, 0, 0);
       }
     };
@@ -2466,7 +2475,8 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
 #pragma unroll
   for (u32 c = 0; c < 4u * NH; c++) {
     const u32 i = tid + c * NT, n_ = i & 15u, qz = (i >> 4) & 1u, pk = (i >> 5) & 31u, th = i >> 10;
-    sB[th][pk][2u * (1u - (n_ >> 3)) + qz][n_] = (u32x4)(0u);
+    const u32 q_ = 2u * (1u - (n_ >> 3)) + qz;
+    sB[th][pk][q_][n_ ^ v8_bswz(pk >> 2, q_)] = (u32x4)(0u);
   }
   if (t0 < t1) {
     fetch_tile(t0);
