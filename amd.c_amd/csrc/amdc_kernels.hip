@@ -1960,13 +1960,15 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
 
   u32x4 rb[NCH];
   float rd = 0.0f, rxv = 0.0f; // d_a, d_a asum: threads < 2 NTT, one (block, token) each
+  // every load of a stage is issued by every thread (threads past 2 NTT read past the resource: zeros,
+  // unused), and the loop issues them unconditionally: the compiler then counts the loads in flight
+  // statically, and a wait for one stage's data does not become a wait for the next stage's loads
+  const u32 daoa = tid < 2u * NTT ? dao : 0xFFFFFFF0u;
   auto fetch = [&](u32 s) { // stage s = blocks 2s, 2s+1
 #pragma unroll
     for (u32 c = 0; c < NCH; c++) rb[c] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo[c], 128u * s, 0);
-    if (tid < 2u * NTT) {
-      rd = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rda, dao, 8u * s * Tp, 0));
-      rxv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxa, dao, 8u * s * Tp, 0));
-    }
+    rd = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rda, daoa, 8u * s * Tp, 0));
+    rxv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxa, daoa, 8u * s * Tp, 0));
   };
   auto store = [&](u32 bf, u32 s) {
 #pragma unroll
@@ -1998,13 +2000,13 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
       }
     }
   };
-  u32x4 hd[2]; // the super-group header of the lane's A rows (scales; Q8_0: the 8 d)
-  u32 hdd[2];  // Q6_K: f16 d
-  auto load_h = [&](u32 g) {
+  u32x4 hd[2], hn[2]; // the super-group header of the lane's A rows (scales; Q8_0: the 8 d), and the next one's
+  u32 hdd[2], hnd[2];  // Q6_K: f16 d
+  auto load_h = [&](u32 g, u32x4(&hx)[2], u32(&hxd)[2]) {
 #pragma unroll
     for (u32 i = 0; i < 2u; i++) {
-      hd[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo[i], 16u * g, 0);
-      if constexpr (KIND == AMDC_Q6_K) hdd[i] = __builtin_amdgcn_raw_buffer_load_b16(rw, wo[i], 16u * ng + 2u * g, 0);
+      hx[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo[i], 16u * g, 0);
+      if constexpr (KIND == AMDC_Q6_K) hxd[i] = __builtin_amdgcn_raw_buffer_load_b16(rw, wo[i], 16u * ng + 2u * g, 0);
     }
   };
 
@@ -2115,25 +2117,24 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
     fetch(s0);
     store(0, s0);
     load_w(s0, wa);
-    load_h(g0);
+    load_h(g0, hn, hnd);
   }
   __syncthreads();
   for (u32 s = s0; s < s1; s += 2u) {
+#pragma unroll
+    for (u32 i = 0; i < 2u; i++) hd[i] = hn[i], hdd[i] = hnd[i]; // the header of stages s, s + 1 (loaded a stage ago)
     fetch(s + 1u);
     load_w(s + 1u, wb);
     compute(2u * (s & 3u), 0, wa);
     store(1, s + 1u);
     __syncthreads();
     const bool more = s + 2u < s1;
-    if (more) {
-      fetch(s + 2u);
-      load_w(s + 2u, wa);
-    }
+    load_h((s + 2u) >> 2, hn, hnd); // the super-group header of stage s + 2 (the current one's again inside a super-group)
+    __asm__ volatile("" ::: "memory"); // issued before the stage's other loads: waiting for it does not wait for them
+    fetch(s + 2u);                     // past the range: unused bytes (or zeros past the resource)
+    load_w(s + 2u, wa);
     compute(2u * ((s + 1u) & 3u), 1, wb);
-    if (((s + 1u) & 3u) == 3u) {
-      close_group((s >> 2) & 1u);
-      if (more) load_h((s + 2u) >> 2);
-    }
+    if (((s + 1u) & 3u) == 3u) close_group((s >> 2) & 1u);
     if (more) store(0, s + 2u);
     __syncthreads();
   }
