@@ -645,8 +645,8 @@ static u32 gemv2_lanes(u32 ng, u32 rows, int k8) {
 static int ws_take(size_t n, void **p);
 
 /* The verify GEMV on int8 MFMA (T <= 16): 64 rows per workgroup, K split
- * over aligned ranges of tiles (64 blocks each) until the workgroups fill the
- * CUs four times. A range holds S tiles, S a power of two <= 4, so that its
+ * over aligned ranges of tiles (64 blocks each): for T <= 8 until the
+ * workgroups fill the CUs four times, for T > 8 by an estimate of the time. A range holds S tiles, S a power of two <= 4, so that its
  * sum is a subtree of the super-group tree (the kernels' order, equal to the
  * decode GEMV's) and amdc_gemm_reduce's tree over the ranges completes it. */
 static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
@@ -661,6 +661,19 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
   if (want > 16u) want = 16u; /* amdc_gemm_reduce adds at most 16 ranges */
   u32 tps = 1;
   while (tps < 4u && tps * want < nt) tps <<= 1; /* the smallest S with ceil(nt / S) <= want (nt <= 32: S <= 2 for 16) */
+  if (T > 8u && t_ksplit <= 0 && wgs < 2u * cus) {
+    /* the 16-vector kernels hold one workgroup per CU: the range size S (1, 2, 4 tiles) with the fewest
+       tile times, (rounds of workgroups) x S, plus one for the reduction launch of a split; ties to the
+       larger S (grids of two workgroups per CU and more are not split). Measured on MI355X (T = 16, us): 11008 x 4096 Q4_0 16.7 unsplit against 20.8 in 2 splits,
+       4096 x 11008 Q4_0 19.3 in 3 against 21.4 in 6, 17408 x 5120 Q4_K 33.1 in 3 against 37.8 unsplit */
+    u64 best = ~0ull;
+    for (u32 S = 4u; S >= 1u; S >>= 1) {
+      const u32 n = (nt + S - 1u) / S;
+      if (n > 16u) break;
+      const u64 est = ((u64)wgs * n + cus - 1u) / cus * (S < nt ? S : nt) + (n > 1u ? 1u : 0u);
+      if (est < best) best = est, tps = S;
+    }
+  }
   const u32 ks = (nt + tps - 1u) / tps;
   float *part = NULL;
   if (ks > 1u) {
@@ -674,7 +687,9 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
                 : kind == AMDC_KIND_Q8_0 ? (v16 ? K_GEMV_Q8_V16 : K_GEMV_Q8_V8)
                                          : (v16 ? K_GEMV_Q4_V16 : K_GEMV_Q4_V8);
   g_last_k = k;
-  HIPCALL(H.ModuleLaunchKernel(g_k[k], wgs, ks, 1, 256, 1, 1, 0, stream, args, NULL));
+  /* Q4_0 / Q4_K: 8 waves, two per 16 rows, each with half of a tile's super-group pairs */
+  const unsigned nth = kind == AMDC_KIND_Q4_0 || kind == AMDC_KIND_Q4_K ? 512u : 256u;
+  HIPCALL(H.ModuleLaunchKernel(g_k[k], wgs, ks, 1, nth, 1, 1, 0, stream, args, NULL));
   if (ks > 1u) {
     const u64 n = (u64)rows * T;
     void *ra[] = {&part, (void *)&ks, &y, &rows, &T, &bias, &res, &ys, &rs};

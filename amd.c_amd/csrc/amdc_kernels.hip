@@ -2253,20 +2253,27 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *
 // into a pairwise tree kept as a stack (ItemTree's tree, over tiles); the
 // ranges' sums are added by amdc_gemm_reduce in the same tree.
 //
-// Workgroup: 4 waves, wave w: rows 16 w .. 16 w + 15 of a 64-row tile; K in
-// tiles of 8 super-groups (64 blocks): the tile's activations are staged in
-// LDS, B-ready (the zero halves written once), with d_a, d_a asum (or asum)
-// per (block, token); each wave builds its rows' scale tables from the headers.
+// Workgroup: 4 row groups of 16 rows (a 64-row tile), each with WS waves: one
+// (Q8_0) or two (Q4_0, Q4_K: each wave takes 2 of a tile's 4 pairs of super-
+// groups, so that the dependent chain of LDS reads, MFMAs and scale arithmetic
+// per plane is half as long; the second wave's tile sum goes to the first
+// through the LDS, which adds it in the order above). K in tiles of 8
+// super-groups (64 blocks): the tile's activations are staged in LDS,
+// B-ready (the zero halves written once), with d_a, d_a asum (or asum) per
+// (block, token); each wave builds its scale tables from the headers.
 // The weights go from memory straight into LDS (buffer_load ... lds) in whole
-// 128-byte lines: plane k of a tile is 128 contiguous bytes of a row, and each
-// load instruction moves 8 rows x 128 bytes (register loads in the MFMA's lane
-// order touch 16 rows x 32 bytes per instruction, which held the vector memory
-// pipeline to about 2.5 TB/s); the A operand is then read from LDS in lane
-// order. Per wave a ring of NS plane steps (Q4: one plane of its 16 rows, 2 KB;
-// Q8_0: the two half planes of a block, 4 KB), one LDS array per slot so that
-// the waits for each step's loads are counted separately; within a wave's
-// plane, row i's 16-byte column c holds super-group c ^ v8_swz(i), so that the
-// A reads (16 rows, one column pair) fall on distinct banks.
+// lines: plane k of a tile is 128 contiguous bytes of a row, and each load
+// instruction moves 8 rows x 128 bytes (one wave per row group) or 16 rows x
+// 64 bytes (two) (register loads in the MFMA's lane order touch 16 rows x 32
+// bytes per instruction, which held the vector memory pipeline to about 2.5
+// TB/s); the A operand is then read from LDS in lane order. Per wave a ring of
+// NS plane steps (Q4: one plane of its rows and columns, 2 or 1 KB; Q8_0: the
+// two half planes of a block, 4 KB). The compiler's own waits for loads into
+// the LDS are not relied on (it missed one after the loop's back edge): before
+// each plane the wave waits explicitly for the loads issued before the plane's
+// step (vm_wait, counted from the fixed issue order). Within a wave's plane,
+// row i's 16-byte column c holds super-group c ^ swz(i), so that the A reads
+// (16 rows, one column pair) fall on distinct banks.
 // NH token halves of 8 (T <= 8 NH): the _v16 kernels take two, each A operand
 // then feeds two MFMAs.
 // Split K over gridDim.y: split ks takes tiles [ks S, ks S + S) (S = tps, at
@@ -2283,6 +2290,23 @@ __device__ __forceinline__ void v8_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// Wait until at most n vector memory loads of the wave are in flight (gfx9 s_waitcnt: vmcnt in bits
+// 3:0 and 15:14, expcnt and lgkmcnt at their maxima). The loads complete in order, so this is how a
+// wave knows that its loads into the LDS issued before the last n have landed. n is a constant once
+// the caller's loop is unrolled.
+__device__ __forceinline__ void vm_wait(u32 n) {
+  __asm__ volatile("" ::: "memory");
+  switch (n) {
+#define VMW(N)                                                                                                                     \
+  case N: __builtin_amdgcn_s_waitcnt(0x0F70 | ((N) & 15) | (((N) >> 4) << 14)); break;
+    VMW(0) VMW(1) VMW(2) VMW(3) VMW(4) VMW(5) VMW(6) VMW(7) VMW(8) VMW(9) VMW(10) VMW(11) VMW(12) VMW(13) VMW(14) VMW(15)
+    VMW(16) VMW(17) VMW(18) VMW(19) VMW(20) VMW(21) VMW(22) VMW(23) VMW(24) VMW(25) VMW(26) VMW(27) VMW(28) VMW(29) VMW(30)
+#undef VMW
+  default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  }
+  __asm__ volatile("" ::: "memory");
+}
+
 // The column swizzle of the verify kernels' B operands in the LDS (sB[..][pair
 // p + 4 k][quarter q][column]): column n of (k, q) sits at n ^ v8_bswz(k, q).
 // The staging writes of 16 consecutive threads (the 8 blocks k of a
@@ -2291,36 +2315,50 @@ __device__ __forceinline__ void v8_barrier() {
 // (k, q) stay a permutation of 16 consecutive columns.
 __device__ __forceinline__ u32 v8_bswz(u32 k, u32 q) { return ((k << 1) | (q & 1u)) & 15u; }
 
-template <int KIND, int NS, int NH>
+template <int KIND, int NS, int NH, int WS>
 __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
                                            u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 xs, u32 ys,
                                            u32 rs, float *__restrict__ part, u32 tps) {
   constexpr u32 SC = KIND == AMDC_Q8_0 ? 2u : 1u; // 2 KB chunks (planes of 16 rows) per step
+  static_assert(WS == 1 || SC == 1, "the pair split is built for the nibble kinds");
   constexpr bool K4 = KIND == AMDC_Q4_K;
+  constexpr u32 NW = 4u * WS, NTH = 64u * NW; // waves, threads
+  constexpr u32 CW = 8u / WS;                 // 16-byte columns (super-groups of the tile) of a plane line per wave
+  constexpr u32 SL = SC * 16u * CW;           // u32x4 per ring slot: 16 rows x CW columns (x SC)
+  constexpr u32 NPW = 4u / WS;                // pairs of super-groups per wave
   typedef __attribute__((address_space(3))) void lds_t;
-  __shared__ __attribute__((aligned(16))) u32x4 sw0[4][SC * 128u];
-  __shared__ __attribute__((aligned(16))) u32x4 sw1[4][SC * 128u];
-  __shared__ __attribute__((aligned(16))) u32x4 sw2[NS > 2 ? 4 : 1][NS > 2 ? SC * 128u : 1u];
-  __shared__ __attribute__((aligned(16))) u32x4 sw3[NS > 2 ? 4 : 1][NS > 2 ? SC * 128u : 1u];
+  __shared__ __attribute__((aligned(16))) u32x4 sw0[NW][SL];
+  __shared__ __attribute__((aligned(16))) u32x4 sw1[NW][SL];
+  __shared__ __attribute__((aligned(16))) u32x4 sw2[NS > 2 ? NW : 1][NS > 2 ? SL : 1u];
+  __shared__ __attribute__((aligned(16))) u32x4 sw3[NS > 2 ? NW : 1][NS > 2 ? SL : 1u];
   constexpr u32 NTK = 8u * NH;                                      // tokens per launch: NH halves of 8
   // [token half][pair p + 4 k][K quarter][column]: the B operands, read by every lane as they are (the
   // quarters outside a column's half of K hold zeros, written once)
   __shared__ __attribute__((aligned(16))) u32x4 sB[NH][32][4][16];
   __shared__ __attribute__((aligned(16))) float sda[64][NTK];      // d_a [block of tile][token]
   __shared__ __attribute__((aligned(16))) float sxa[64][NTK];      // Q4_K: d_a asum; Q4_0: asum (as int bits)
-  // per wave and plane (double-buffered): s (Q4_K d sc, Q4_0 / Q8_0 d) and Q4_K -(dmin mn) [super-group of tile][row]
-  __shared__ __attribute__((aligned(16))) float ssc[4][2][8][16];
-  __shared__ __attribute__((aligned(16))) float smn[K4 ? 4 : 1][2][8][16];
+  // per wave and plane (double-buffered): s (Q4_K d sc, Q4_0 / Q8_0 d) and Q4_K -(dmin mn) [the wave's
+  // super-group of the tile][row]
+  __shared__ __attribute__((aligned(16))) float ssc[NW][2][CW][16];
+  __shared__ __attribute__((aligned(16))) float smn[K4 ? NW : 1][2][CW][16];
+  __shared__ __attribute__((aligned(16))) float sx[WS > 1 ? 4 : 1][NH][4][64]; // split pairs: the second wave's tile sums
   const u32 ng = amdc_ngroups(nb), nt = (ng + 7u) >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
+  const u32 wr = w & 3u, wp = w >> 2; // the wave's 16 rows, its half of the pairs (WS = 2)
   const u32 i16 = lane & 15u, h = lane >> 4, n = i16, tk = n & 7u, pp = n >> 3;
   const u32 RB = (u32)amdc_row_bytes_k(KIND, nb);
-  const u32 rt0 = blockIdx.x * 64u, r0 = rt0 + 16u * w;
+  const u32 rt0 = blockIdx.x * 64u, r0 = rt0 + 16u * wr;
   auto clamp_row = [&](u32 r) { return (r < rows ? r : rows - 1u) - rt0; };
   // a workgroup-uniform resource over the tile's rows; a lane's row in the 32-bit offset
   const __amdgpu_buffer_rsrc_t rw = rsrc(W + (u64)rt0 * RB, (u32)min((u64)(rows - rt0) * RB, (u64)0xFFFFFFF0u));
-  const u32 wo = clamp_row(r0 + i16) * RB;                                    // row i16 (headers)
-  const u32 wl0 = clamp_row(r0 + (lane >> 3)) * RB, wl1 = clamp_row(r0 + 8u + (lane >> 3)) * RB; // the plane loads' rows
-  const u32 lcol = lane & 7u, g0 = lcol ^ v8_swz(lane >> 3), g1 = lcol ^ v8_swz(8u + (lane >> 3));
+  const u32 wo = clamp_row(r0 + i16) * RB; // row i16 (headers)
+  // the plane loads: one wave: rows lane / 8 and 8 + lane / 8, column lane & 7 (2 instructions); split
+  // pairs: row lane / 4, column lane & 3 of the wave's half (1 instruction); column c of row i holds
+  // super-group c ^ swz(i) of the wave's columns
+  auto swz = [](u32 i) -> u32 { return WS == 1 ? v8_swz(i) : (i >> 1) & 3u; };
+  const u32 wl0 = WS == 1 ? clamp_row(r0 + (lane >> 3)) * RB : clamp_row(r0 + (lane >> 2)) * RB;
+  const u32 wl1 = clamp_row(r0 + 8u + (lane >> 3)) * RB;
+  const u32 g0 = WS == 1 ? (lane & 7u) ^ v8_swz(lane >> 3) : CW * wp + ((lane & 3u) ^ swz(lane >> 2));
+  const u32 g1 = (lane & 7u) ^ v8_swz(8u + (lane >> 3));
   const u32 xn = (u32)min((u64)T * xs, (u64)0xFFFFFFF0u);
   const __amdgpu_buffer_rsrc_t rxq = rsrc(xq, xn); // the T Q8 rows
   constexpr u32 OOB = 0xFFFFFFF0u;                 // an offset past every resource: the load returns zeros
@@ -2332,132 +2370,145 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
     if (s == 2u) return sw2[NS > 2 ? w : 0u];
     return sw3[NS > 2 ? w : 0u];
   };
-  // step k of tile t into slot s: chunk c = plane k (Q4) or 2k + c (Q8_0); rows 8j + lane / 8, column lane & 7
+  // step k of tile t into slot s: chunk c = plane k (Q4) or 2k + c (Q8_0)
+  // The compiler does not order LDS reads against these loads into the LDS: the fences keep every read
+  // of a slot's previous step ahead of its refill.
   auto issue = [&](u32 t, u32 k, u32 s, bool on) {
     const u32 gt = on ? gtile(t) : 0u; // off: every load out of range (zeros into the slot)
+    __asm__ volatile("" ::: "memory");
 #pragma unroll
     for (u32 c = 0; c < SC; c++) {
       const u32 pl = SC == 1u ? k : 2u * k + c;
       const u32 base = (KIND == AMDC_Q8_0 ? 2048u : 1024u) * t + 16u * ng + 16u * pl * gt;
       lds_t *d = (lds_t *)(slot(s) + 128u * c);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, d, 16, g0 < gt ? wl0 + base + 16u * g0 : OOB, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_t *)(slot(s) + 128u * c + 64u), 16, g1 < gt ? wl1 + base + 16u * g1 : OOB, 0, 0, 0);
+      if constexpr (WS == 1)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_t *)(slot(s) + 128u * c + 64u), 16, g1 < gt ? wl1 + base + 16u * g1 : OOB, 0, 0, 0);
     }
+    __asm__ volatile("" ::: "memory");
   };
-  // activations of tile t in registers (thread: 2 NH of the 16-byte halves, 2 NH of the (block, token) scale
-  // pairs); the lane offsets of tile 0 computed once: tile t adds 2048 t (halves), 4 t (scales), 128 t
+  // activations of tile t in registers (thread: the 16-byte halves and (block, token) scale pairs i = tid +
+  // c NTH); the lane offsets of tile 0 computed once: tile t adds 2048 t (halves), 4 t (scales), 128 t
   // (headers), and a load is valid while its block of the tile is under lim(t)
-  u32x4 ra4[4 * NH];
-  float rd[2 * NH];
-  u32 rx[2 * NH];
-  u32x4 rh[2]; // the next tile's headers of row i16, super-groups h, h + 4
-  u32 xo[4 * NH], xb[4 * NH], so[2 * NH], sbl[2 * NH];
+  constexpr u32 NC4 = 4u * NH / WS, NCS = 2u * NH / WS, NQH = 2u / WS; // halves, scale pairs, headers per thread
+  constexpr u32 NFT = NC4 + 2u * NCS + NQH, DPS = SC * (WS == 1 ? 2u : 1u); // loads of fetch_tile, of one ring step
+  constexpr u32 FP = 1u; // fetch_tile goes out after plane FP's ring step (plane 0's LDS reads do not wait for it)
+  u32x4 ra4[NC4];
+  float rd[NCS];
+  u32 rx[NCS];
+  u32x4 rh[NQH]; // the next tile's headers of row i16: super-groups h + 4 (q + wp) (one wave: h, h + 4)
+  u32 xo[NC4], xb[NC4], so[NCS], sbl[NCS];
 #pragma unroll
-  for (u32 c = 0; c < 4u * NH; c++) {
-    const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7;
+  for (u32 c = 0; c < NC4; c++) {
+    const u32 i = tid + c * NTH, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7;
     xo[c] = tok < T ? tok * xs + 32u * bl + 16u * half : OOB;
     xb[c] = tok < T ? bl : 64u;
   }
 #pragma unroll
-  for (u32 c = 0; c < 2u * NH; c++) {
-    const u32 i = tid + c * NT, tok = i & (NTK - 1u), bl = i / NTK;
+  for (u32 c = 0; c < NCS; c++) {
+    const u32 i = tid + c * NTH, tok = i & (NTK - 1u), bl = i / NTK;
     so[c] = tok * xs + 4u * bl;
     sbl[c] = tok < T ? bl : 64u;
   }
-  auto fetch_tile = [&](u32 t) {
-    const u32 lim = min(8u * gtile(t), nb - 64u * t); // blocks of tile t
+  auto hgl = [&](u32 q) { return h + 4u * (q + (WS > 1 ? wp : 0u)); }; // the super-group of header q
+  auto fetch_tile = [&](u32 t, bool on) {
+    const u32 lim = on ? min(8u * gtile(t), nb - 64u * t) : 0u; // blocks of tile t (off: every load out of range)
 #pragma unroll
-    for (u32 c = 0; c < 4u * NH; c++)
+    for (u32 c = 0; c < NC4; c++)
       ra4[c] = __builtin_amdgcn_raw_buffer_load_b128(rxq, xb[c] < lim ? xo[c] + 2048u * t : OOB, 0, 0);
 #pragma unroll
-    for (u32 c = 0; c < 2u * NH; c++) {
+    for (u32 c = 0; c < NCS; c++) {
       const bool ok = sbl[c] < lim;
       rd[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxq, ok ? so[c] + 32u * nb + 256u * t : OOB, 0, 0));
       rx[c] = __builtin_amdgcn_raw_buffer_load_b32(rxq, ok ? so[c] + 36u * nb + 256u * t : OOB, 0, 0);
     }
 #pragma unroll
-    for (u32 q = 0; q < 2u; q++) {
-      const u32 gl = h + 4u * q;
+    for (u32 q = 0; q < NQH; q++) {
+      const u32 gl = hgl(q);
       rh[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, 8u * gl < lim ? wo + 16u * (8u * t + gl) : OOB, 0, 0);
     }
   };
-  u32x4 hc[2];   // the current tile's headers (rh is refilled with the next tile's during this one)
-  float dd[2][2]; // Q4_K: d, dmin of hc[q]
-  // the scale table of plane k into buffer k & 1: this lane's entries (super-groups h, h + 4 of row i16);
+  u32x4 hc[NQH];    // the current tile's headers (rh is refilled with the next tile's during this one)
+  float dd[NQH][2]; // Q4_K: d, dmin of hc[q]
+  // the scale table of plane k into buffer k & 1: this lane's entries (its headers' super-groups, row i16);
   // the same products as the decode GEMV's (exact: an f16 times a 6-bit integer)
   auto scales = [&](u32 k) {
 #pragma unroll
-    for (u32 q = 0; q < 2u; q++) {
-      const u32 gl = h + 4u * q;
+    for (u32 q = 0; q < NQH; q++) {
+      const u32 gx = hgl(q) & (CW - 1u);
       if (K4) {
-        ssc[w][k & 1u][gl][i16] = dd[q][0] * (float)q4k_sc(hc[q], k);
-        smn[K4 ? w : 0u][k & 1u][gl][i16] = -(dd[q][1] * (float)q4k_mn(hc[q], k));
+        ssc[w][k & 1u][gx][i16] = dd[q][0] * (float)q4k_sc(hc[q], k);
+        smn[K4 ? w : 0u][k & 1u][gx][i16] = -(dd[q][1] * (float)q4k_mn(hc[q], k));
       } else {
-        ssc[w][k & 1u][gl][i16] = h2f(hword(hc[q], k >> 1) >> (16u * (k & 1u)));
+        ssc[w][k & 1u][gx][i16] = h2f(hword(hc[q], k >> 1) >> (16u * (k & 1u)));
       }
     }
   };
   auto stage_tile = [&]() {
 #pragma unroll
-    for (u32 c = 0; c < 4u * NH; c++) { // block (gl, k) of token tok: quarter 2 (gl & 1) + half of column tok % 8 + 8 (gl & 1)
-      const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, gl = bl >> 3, k = bl & 7u;
+    for (u32 c = 0; c < NC4; c++) { // block (gl, k) of token tok: quarter 2 (gl & 1) + half of column tok % 8 + 8 (gl & 1)
+      const u32 i = tid + c * NTH, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, gl = bl >> 3, k = bl & 7u;
       const u32 q_ = 2u * (gl & 1u) + half;
       sB[tok >> 3][(gl >> 1) + 4u * k][q_][((tok & 7u) + 8u * (gl & 1u)) ^ v8_bswz(k, q_)] = ra4[c];
     }
 #pragma unroll
-    for (u32 c = 0; c < 2u * NH; c++) {
-      const u32 i = tid + c * NT, tok = i & (NTK - 1u), bl = i / NTK;
+    for (u32 c = 0; c < NCS; c++) {
+      const u32 i = tid + c * NTH, tok = i & (NTK - 1u), bl = i / NTK;
       sda[bl][tok] = rd[c];
       sxa[bl][tok] = K4 ? rd[c] * (float)(int)rx[c] : __builtin_bit_cast(float, rx[c]);
     }
 #pragma unroll
-    for (u32 q = 0; q < 2u; q++) {
+    for (u32 q = 0; q < NQH; q++) {
       hc[q] = rh[q];
       if (K4) dd[q][0] = h2f(hc[q].x), dd[q][1] = h2f(hc[q].x >> 16);
     }
     scales(0u);
   };
-  float lf[NH][4][4]; // the leaves: [token half][pair p: super-group 2 p + pp][row 4 h + v]
-  // the MFMAs of plane step k (pairs of the tile) from slot s: pair p + 1's MFMAs go out before pair
-  // p's results are used (two result sets live)
-  auto plane = [&](u32 k, u32 npair, u32 s) {
+  float lf[NH][NPW][4]; // the leaves: [token half][the wave's pair pl (pair NPW wp + pl): super-group 2 p + pp][row 4 h + v]
+  // the MFMAs of plane step k (the wave's pairs of the tile) from slot s: pair pl + 1's MFMAs go out before
+  // pair pl's results are used (two result sets live)
+  // Every pair is computed, also past a partial tile's super-groups: their weights, activations and
+  // scales are zeros, so their leaves stay +0 (the value of a leaf not visited), and the code has no
+  // branch (the loads and MFMAs of consecutive planes can overlap).
+  auto plane = [&](u32 k, u32 s) {
+    const u32 pw0 = WS > 1 ? NPW * wp : 0u; // the wave's first pair
     const u32x4 *sl = slot(s);
     const u32 cs = SC == 2u ? 128u * (h & 1u) : 0u; // Q8_0: lanes h odd read the second half plane
     v4i c[NH][2];
-    auto mfma = [&](u32 p) {
-      const u32x4 wq = sl[cs + 8u * i16 + ((2u * p + (h >> 1)) ^ v8_swz(i16))];
+    auto mfma = [&](u32 pl) {
+      const u32 p = pw0 + pl;
+      const u32x4 wq = sl[cs + CW * i16 + ((2u * pl + (h >> 1)) ^ swz(i16))];
       const u32x4 a = KIND == AMDC_Q8_0 ? wq : (wq >> (4u * (h & 1u))) & 0x0F0F0F0Fu;
 #pragma unroll
       for (u32 th = 0; th < (u32)NH; th++) {
         const u32x4 bq = sB[th][p + 4u * k][h][n ^ v8_bswz(k, h)];
-        c[th][p & 1u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, bq), (v4i){0, 0, 0, 0}, 0, 0, 0);
+        c[th][pl & 1u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, bq), (v4i){0, 0, 0, 0}, 0, 0, 0);
       }
     };
-    mfma(0u); // npair >= 1
+    mfma(0u);
 #pragma unroll
-    for (u32 p = 0; p < 4u; p++) {
-      if (p >= npair) break;
-      if (p + 1u < npair) mfma(p + 1u);
-      if (p == 0u && k + 1u < 8u) scales(k + 1u); // the next plane's table, while the MFMAs run
-      const u32 gl = 2u * p + pp, bl = 8u * gl + k; // this lane's super-group and block (column pp)
-      const v4f s4 = *(const v4f *)&ssc[w][k & 1u][gl][4u * h];
+    for (u32 pl = 0; pl < NPW; pl++) {
+      if (pl + 1u < NPW) mfma(pl + 1u);
+      if (pl == 0u && k + 1u < 8u) scales(k + 1u); // the next plane's table, while the MFMAs run
+      const u32 gl = 2u * (pw0 + pl) + pp, bl = 8u * gl + k; // this lane's super-group and block (column pp)
+      const v4f s4 = *(const v4f *)&ssc[w][k & 1u][gl & (CW - 1u)][4u * h];
       v4f m4 = {};
-      if (K4) m4 = *(const v4f *)&smn[K4 ? w : 0u][k & 1u][gl][4u * h];
+      if (K4) m4 = *(const v4f *)&smn[K4 ? w : 0u][k & 1u][gl & (CW - 1u)][4u * h];
 #pragma unroll
       for (u32 th = 0; th < (u32)NH; th++) {
-        const v4i cp = c[th][p & 1u];
+        const v4i cp = c[th][pl & 1u];
         const float da = sda[bl][tk + 8u * th];
         if (KIND == AMDC_Q4_0) {
           const u32 as = __builtin_bit_cast(u32, sxa[bl][tk + 8u * th]);
 #pragma unroll
-          for (u32 v = 0; v < 4u; v++) lf[th][p][v] += (s4[v] * da) * (float)(int)((u32)cp[v] - 8u * as);
+          for (u32 v = 0; v < 4u; v++) lf[th][pl][v] += (s4[v] * da) * (float)(int)((u32)cp[v] - 8u * as);
         } else if (KIND == AMDC_Q8_0) {
 #pragma unroll
-          for (u32 v = 0; v < 4u; v++) lf[th][p][v] += (s4[v] * da) * (float)cp[v];
+          for (u32 v = 0; v < 4u; v++) lf[th][pl][v] += (s4[v] * da) * (float)cp[v];
         } else {
           const float xa = sxa[bl][tk + 8u * th];
 #pragma unroll
-          for (u32 v = 0; v < 4u; v++) lf[th][p][v] = __builtin_fmaf(m4[v], xa, __builtin_fmaf(s4[v] * (float)cp[v], da, lf[th][p][v]));
+          for (u32 v = 0; v < 4u; v++) lf[th][pl][v] = __builtin_fmaf(m4[v], xa, __builtin_fmaf(s4[v] * (float)cp[v], da, lf[th][pl][v]));
         }
       }
     }
@@ -2474,53 +2525,78 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
   // used, the slot is reloaded with step k + NS (of this tile or the next)
   // the zero quarters of the B operands (column n: the quarters of the other block's half of K)
 #pragma unroll
-  for (u32 c = 0; c < 4u * NH; c++) {
-    const u32 i = tid + c * NT, n_ = i & 15u, qz = (i >> 4) & 1u, pk = (i >> 5) & 31u, th = i >> 10;
+  for (u32 c = 0; c < NC4; c++) {
+    const u32 i = tid + c * NTH, n_ = i & 15u, qz = (i >> 4) & 1u, pk = (i >> 5) & 31u, th = i >> 10;
     const u32 q_ = 2u * (1u - (n_ >> 3)) + qz;
     sB[th][pk][q_][n_ ^ v8_bswz(pk >> 2, q_)] = (u32x4)(0u);
   }
   if (t0 < t1) {
-    fetch_tile(t0);
+    fetch_tile(t0, true);
 #pragma unroll
     for (u32 k = 0; k < (u32)NS; k++) issue(t0, k, k, true);
   }
   for (u32 t = t0; t < t1; t++) {
     const bool more = t + 1u < t1;
-    const u32 npair = (gtile(t) + 1u) >> 1;
     v8_barrier(); // the previous tile's readers are done
     stage_tile();
     v8_barrier();
 #pragma unroll
     for (u32 th = 0; th < (u32)NH; th++)
 #pragma unroll
-      for (u32 p = 0; p < 4u; p++)
+      for (u32 p = 0; p < NPW; p++)
 #pragma unroll
         for (u32 v = 0; v < 4u; v++) lf[th][p][v] = 0.0f;
-    if (more) fetch_tile(t + 1u); // in flight during this tile
 #pragma unroll
     for (u32 k = 0; k < 8u; k++) {
-      plane(k, npair, k % (u32)NS);
+      // step k's loads into its slot have landed: issued after them are the NS - 1 later steps' and, for
+      // steps FP + 1 .. FP + NS, the next tile's activation loads (issued after plane FP's step)
+      vm_wait((NS - 1u) * DPS + (k > FP && k <= FP + (u32)NS ? NFT : 0u));
+      plane(k, k % (u32)NS);
       // issued also after the range's last tile (as zeros), so that the waits count statically
       if (k + (u32)NS < 8u) issue(t, k + (u32)NS, k % (u32)NS, true);
       else issue(t + 1u, k + (u32)NS - 8u, k % (u32)NS, more);
+      if (k == FP) fetch_tile(t + 1u, more); // in flight during this tile (issued also past the range)
     }
-    // the tile's subtree: super-groups (2p, 2p + 1) across the two columns, then ((0 + 1) + (2 + 3)),
-    // then into the tree over tiles (c: the tiles before this one in the range)
+    // the tile's subtree: super-groups (2p, 2p + 1) across the two columns, then ((0 + 1) + (2 + 3))
+    // (split pairs: the second wave's (2 + 3) through the LDS), then into the tree over tiles (c: the
+    // tiles before this one in the range)
+    float x[NH][4];
+#pragma unroll
+    for (u32 th = 0; th < (u32)NH; th++)
+#pragma unroll
+      for (u32 v = 0; v < 4u; v++) {
+        float pr[NPW];
+#pragma unroll
+        for (u32 p = 0; p < NPW; p++) pr[p] = lf[th][p][v] + dpp<0x128>(lf[th][p][v]); // row_ror:8
+        x[th][v] = NPW == 4u ? (pr[0] + pr[1]) + (pr[2 % NPW] + pr[3 % NPW]) : pr[0] + pr[1];
+      }
+    if constexpr (WS > 1) {
+      if (wp) {
+#pragma unroll
+        for (u32 th = 0; th < (u32)NH; th++)
+#pragma unroll
+          for (u32 v = 0; v < 4u; v++) sx[wr][th][v][lane] = x[th][v];
+      }
+      v8_barrier();
+      if (!wp) {
+#pragma unroll
+        for (u32 th = 0; th < (u32)NH; th++)
+#pragma unroll
+          for (u32 v = 0; v < 4u; v++) x[th][v] = x[th][v] + sx[wr][th][v][lane];
+      }
+    }
     const u32 c = t - t0;
 #pragma unroll
     for (u32 th = 0; th < (u32)NH; th++) {
 #pragma unroll
       for (u32 v = 0; v < 4u; v++) {
-        float pr[4];
-#pragma unroll
-        for (u32 p = 0; p < 4u; p++) pr[p] = lf[th][p][v] + dpp<0x128>(lf[th][p][v]); // row_ror:8
-        float x = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+        float xv = x[th][v];
         if (c & 1u) {
-          x = st[0][th][v] + x;
-          if (c & 2u) out[th][v] = st[1][th][v] + x; // a range of 4 tiles is complete
-          else st[1][th][v] = x;
+          xv = st[0][th][v] + xv;
+          if (c & 2u) out[th][v] = st[1][th][v] + xv; // a range of 4 tiles is complete
+          else st[1][th][v] = xv;
         } else {
-          st[0][th][v] = x;
+          st[0][th][v] = xv;
         }
       }
     }
@@ -2533,6 +2609,7 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
 #pragma unroll
       for (u32 v = 0; v < 4u; v++) out[th][v] = cnt == 3u ? st[1][th][v] + st[0][th][v] : cnt == 2u ? st[1][th][v] : st[0][th][v];
   }
+  if (WS > 1 && wp) return; // the first wave of the rows holds the sums
 #pragma unroll
   for (u32 th = 0; th < (u32)NH; th++) {
     const u32 tt = tk + 8u * th;
@@ -2554,36 +2631,36 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
   }
 }
 
-extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_0_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+extern "C" __global__ __launch_bounds__(512) void amdc_gemv_q4_0_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *part, u32 tps) {
-  gemv8_body<AMDC_Q4_0, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
+  gemv8_body<AMDC_Q4_0, 2, 1, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
 }
-extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+extern "C" __global__ __launch_bounds__(512) void amdc_gemv_q4_k_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *part, u32 tps) {
-  gemv8_body<AMDC_Q4_K, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
+  gemv8_body<AMDC_Q4_K, 2, 1, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
 }
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *part, u32 tps) {
-  gemv8_body<AMDC_Q8_0, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
+  gemv8_body<AMDC_Q8_0, 2, 1, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
 }
 // the same for up to 16 vectors (two token halves per MFMA A operand)
-extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_0_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+extern "C" __global__ __launch_bounds__(512) void amdc_gemv_q4_0_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *part, u32 tps) {
-  gemv8_body<AMDC_Q4_0, 2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
+  gemv8_body<AMDC_Q4_0, 2, 2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
 }
-extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
+extern "C" __global__ __launch_bounds__(512) void amdc_gemv_q4_k_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *part, u32 tps) {
-  gemv8_body<AMDC_Q4_K, 2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
+  gemv8_body<AMDC_Q4_K, 2, 2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
 }
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
                                                                    float *part, u32 tps) {
-  gemv8_body<AMDC_Q8_0, 1, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
+  gemv8_body<AMDC_Q8_0, 1, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
 }
 
 // The verify GEMV for Q6_K (T <= 8). A Q6_K weight's scale changes every 16
