@@ -674,6 +674,11 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
       if (est < best) best = est, tps = S;
     }
   }
+  /* T <= 8, at most 3 tiles of K, and 3/4 to 1 workgroup per CU: unsplit (no reduction launch), all
+     rows in one round. Measured on MI355X (T = 8, us): 16384 x 5120 Q4_K 18.2 unsplit against 20.1
+     split 3. (Wider workgroups of 80 or 96 rows, to fit 17408 rows in one round, measured slower:
+     24.8 against 21-22 split, their extra waves share the SIMDs.) */
+  if (T <= 8u && nt <= 3u && t_ksplit <= 0 && wgs <= cus && 4u * wgs >= 3u * cus) tps = 4u;
   const u32 ks = (nt + tps - 1u) / tps;
   float *part = NULL;
   if (ks > 1u) {

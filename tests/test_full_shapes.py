@@ -90,7 +90,10 @@ def test_c2_decode(dev, orc, rows, cols):
     decode_case(dev, orc, Q4K, rows, cols, seed=rows + cols + 1)
 
 
-C3 = [(Q4K, 17408, 5120), (Q4K, 5120, 17408), (Q40, 11008, 4096)]
+C3 = [(Q4K, 17408, 5120), (Q4K, 5120, 17408), (Q40, 11008, 4096),
+      # the unsplit one-round T = 8 launches: 6 row groups per workgroup (250 workgroups), 4 (256),
+      # 5 with a ragged last workgroup and a partial tile of K (nb = 65)
+      (Q40, 24000, 4096), (Q4K, 16384, 5120), (Q40, 19990, 2080)]
 
 
 @pytest.mark.parametrize("kind,rows,cols", C3, ids=[f"k{k}-{r}x{c}" for k, r, c in C3])
