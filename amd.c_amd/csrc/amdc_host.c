@@ -910,17 +910,10 @@ static int gemv_x(int kind, const char *op, const void *w, const float *x, float
     if ((rc = amdc_quant_q8(x, q8, nb, 1u, 0u, 0u, stream))) return rc;
     return gemv_t(kind, op, w, q8, y, rows, nb, bias, res, 1u, 0u, 0u, 0u, stream);
   }
-  /* the single-shot form with two super-groups per lane (its lanes halved because one per lane would
-     need over 3 workgroups per CU) quantizes the vector once per 32 rows and runs in rounds; the
-     persistent form on 2 workgroups per CU, bit-equal, measured faster there (MI355X, us):
-     22016 x 4096 Q4_0 11.85 against 12.3, 32000 x 4096 Q4_0 15.0 against 15.6-16.0 */
-  const u32 cus = g_cus > 0 ? (u32)g_cus : 256u;
-  const int x1p = t_form == 0 && t_lanes <= 0 && t_wgs <= 0 && (ng + gemvs_lanes(ng, rows, 1) - 1u) / gemvs_lanes(ng, rows, 1) >= 2u &&
-                  (ng + L - 1u) / L == 1u;
-  if ((t_form == 0 || t_form == 3) && !x1p) return gemvs_launch(kind, w, x, 1, y, rows, nb, bias, res, q8, stream);
+  if (t_form == 0 || t_form == 3) return gemvs_launch(kind, w, x, 1, y, rows, nb, bias, res, q8, stream);
   /* every workgroup quantizes the whole vector first: a persistent grid of at most 3 workgroups
      per CU (each loops over row groups) pays that once per slot */
-  const u32 cap = (x1p ? 2u : 3u) * cus;
+  const u32 cap = 3u * (g_cus > 0 ? (u32)g_cus : 256u);
   const unsigned grid = t_wgs > 0 && (u32)t_wgs < nrg ? (unsigned)t_wgs : nrg < cap ? nrg : cap;
   void *args[] = {&w, &x, &y, &rows, &nb, &bias, &res, (void *)&L, &q8};
   return launch(kind == AMDC_KIND_Q4_K ? K_GEMV_Q4K_X1 : K_GEMV_Q4_X1, grid, 1, 320u * ng, stream, args);
