@@ -568,13 +568,29 @@ __device__ __forceinline__ void gemvs_body(const uint8_t *__restrict__ W, const 
   // (MI355X: 22016 x 4096 Q4_0 12.2 -> 11.7 us, 32000 x 4096 15.6 -> 14.9 us)
   Item it[NI];
   constexpr u32 NI0 = FQ && NI >= 2u ? 1u : NI; // items issued before the quantization
+  // the workgroup-per-CU kernels (QCN) with one item per lane: its header and first 4 planes before the
+  // quantization, the other 4 after (MI355X: c1 wqkv 7.5 -> 7.2 us, down 9.3 -> 8.85 us; the 16-row
+  // single-shot kernel measured slower so, 4.9 -> 5.5 us on 4096 x 4096)
+  constexpr bool SPLIT1 = FQ && QCN > 0u && NI == 1u && (KIND == AMDC_Q4_0 || KIND == AMDC_Q4_K);
+  if constexpr (SPLIT1) {
+    const u32 g = l < ng ? l : 0u;
+    it[0].h = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_header_off(g)));
 #pragma unroll
-  for (u32 i = 0; i < NI0; i++) load_item<KIND>(it[i], wr, ng, l + L * i, l + L * i < ng);
+    for (u32 k = 0; k < 4u; k++) it[0].n[k] = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_nib_off(ng, g, k)));
+  } else {
+#pragma unroll
+    for (u32 i = 0; i < NI0; i++) load_item<KIND>(it[i], wr, ng, l + L * i, l + L * i < ng);
+  }
   if (FQ) {
     fq.quant(0, nb, ng, s_lo, s_hi, s_d, s_as, q8out);
     for (u32 b0 = fq.bp * QC; b0 < nblk; b0 += fq.bp * QC) {
       fq.load(xf, nb, b0);
       fq.quant(b0, nb, ng, s_lo, s_hi, s_d, s_as, q8out);
+    }
+    if constexpr (SPLIT1) {
+      const u32 g = l < ng ? l : 0u;
+#pragma unroll
+      for (u32 k = 4; k < 8u; k++) it[0].n[k] = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_nib_off(ng, g, k)));
     }
 #pragma unroll
     for (u32 i = NI0; i < NI; i++) load_item<KIND>(it[i], wr, ng, l + L * i, l + L * i < ng);
