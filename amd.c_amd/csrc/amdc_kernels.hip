@@ -561,22 +561,28 @@ __device__ __forceinline__ void gemvs_body(const uint8_t *__restrict__ W, const 
     fq.load(xf, nb, 0);
     __asm__ volatile("" ::: "memory"); // the activation loads ahead of the weight loads
   }
-  // with the quantization fused and two or more items per lane, only the first item's loads go out
-  // before the quantization: issuing a load stalls while the memory pipeline is full, and with every
-  // item in flight the quantization started microseconds late (a wall-clock timeline of 22016 x 4096:
-  // 4.2 us to issue the loads); the first items of all workgroups keep the memory busy meanwhile
-  // (MI355X: 22016 x 4096 Q4_0 12.2 -> 11.7 us, 32000 x 4096 15.6 -> 14.9 us)
+  // with the quantization fused, part of the weight loads go out after the quantization: issuing a
+  // load stalls while the memory pipeline is full, and with every item in flight the quantization
+  // started microseconds late (a wall-clock timeline of 22016 x 4096: 4.2 us to issue the loads); the
+  // loads issued first by all workgroups keep the memory busy meanwhile, and the items issued later
+  // are not live during the quantization (the two-item Q4_0 kernel: 157 -> 126 VGPRs, 4 workgroups
+  // per CU)
   Item it[NI];
   constexpr u32 NI0 = FQ && NI >= 2u ? 1u : NI; // items issued before the quantization
-  // the workgroup-per-CU kernels (QCN) with one item per lane: its header and first 4 planes before the
-  // quantization, the other 4 after (MI355X: c1 wqkv 7.5 -> 7.2 us, down 9.3 -> 8.85 us; the 16-row
-  // single-shot kernel measured slower so, 4.9 -> 5.5 us on 4096 x 4096)
-  constexpr bool SPLIT1 = FQ && QCN > 0u && NI == 1u && (KIND == AMDC_Q4_0 || KIND == AMDC_Q4_K);
-  if constexpr (SPLIT1) {
+  // Of the first item, only the header and PB nibble planes go out before the quantization (the rest
+  // after it): the workgroup-per-CU kernels with one item per lane and the single-shot kernels with
+  // two or more. Swept on MI355X (c1 Q4_0, us): wqkv 12288 x 4096 7.5 / 6.8 / 7.5 with 4 / 2 / 0
+  // planes of the workgroup-per-CU kernel, down 4096 x 11008 8.96 / 8.5; wgu 22016 x 4096 and lm_head
+  // 32000 x 4096 on the two-item kernel 11.9 + 14.3 with all 8 planes of item 0, 11.0 + 13.9 with 2,
+  // 10.4 + 15.0 with 4. The 16-row one-item single-shot kernel keeps its whole item before (4.9 against
+  // 5.5 us with 4 planes).
+  constexpr bool SPL = FQ && (KIND == AMDC_Q4_0 || KIND == AMDC_Q4_K) && ((QCN > 0u && NI == 1u) || (QCN == 0u && NI >= 2u));
+  constexpr u32 PB = 2u;
+  if constexpr (SPL) {
     const u32 g = l < ng ? l : 0u;
     it[0].h = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_header_off(g)));
 #pragma unroll
-    for (u32 k = 0; k < 4u; k++) it[0].n[k] = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_nib_off(ng, g, k)));
+    for (u32 k = 0; k < PB; k++) it[0].n[k] = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_nib_off(ng, g, k)));
   } else {
 #pragma unroll
     for (u32 i = 0; i < NI0; i++) load_item<KIND>(it[i], wr, ng, l + L * i, l + L * i < ng);
@@ -587,10 +593,10 @@ __device__ __forceinline__ void gemvs_body(const uint8_t *__restrict__ W, const 
       fq.load(xf, nb, b0);
       fq.quant(b0, nb, ng, s_lo, s_hi, s_d, s_as, q8out);
     }
-    if constexpr (SPLIT1) {
+    if constexpr (SPL) {
       const u32 g = l < ng ? l : 0u;
 #pragma unroll
-      for (u32 k = 4; k < 8u; k++) it[0].n[k] = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_nib_off(ng, g, k)));
+      for (u32 k = PB; k < 8u; k++) it[0].n[k] = __builtin_nontemporal_load((const u32x4 *)(wr + amdc_nib_off(ng, g, k)));
     }
 #pragma unroll
     for (u32 i = NI0; i < NI; i++) load_item<KIND>(it[i], wr, ng, l + L * i, l + L * i < ng);
