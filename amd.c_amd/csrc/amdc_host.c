@@ -298,6 +298,7 @@ static const char *const kname[K_N] = {
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
+static int g_occ[K_N]; /* resident workgroups per CU, looked up at a kernel's first use (0: not yet) */
 static int g_open, g_cus;
 static int t_lanes = -1, t_unroll = -1, t_wgs = -1, t_gemm = -1, t_gemm_min = -1, t_ksplit = -1;
 static u32 x_fuse_nb = 128; /* amdc_gemv_q4_x / _q4k_x: the largest nb quantized inside the GEMV */
@@ -398,6 +399,7 @@ int amdc_open(const char *hsaco) {
   }
   HIPCALL(H.ModuleLoad(&g_mod, hsaco));
   for (int k = 0; k < K_N; k++) HIPCALL(H.ModuleGetFunction(&g_k[k], g_mod, kname[k]));
+  memset(g_occ, 0, sizeof g_occ);
   /* the module-API lookup of a device variable (hipGetSymbolAddress of a code object loaded with
      hipModuleLoad); with device 0 current. Host code uses this address, never the name. */
   HIPCALL(H.ModuleGetGlobal(&g_scratch, &g_scratch_bytes, g_mod, "scratch"));
@@ -1028,23 +1030,39 @@ static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *x
     void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs};
     return launch(n == 128u ? K_GEMM_N128 : K_GEMM_N64, (unsigned)grid, 1, 0, stream, args);
   }
-  /* the f16-MFMA kernel: 128 tokens per workgroup when there are that many;
-   * the K split doubles until the workgroups number three per CU (measured
-   * best on the c4 shapes: 17408 x 5120 split 2, 5120 x 17408 split 8) */
+  /* the f16-MFMA kernel: 128 tokens per workgroup when there are that many */
   const u32 ng = amdc_ngroups(nb), cus = g_cus > 0 ? (u32)g_cus : 256u;
   /* 64-token tiles for Q4_0 at any T (its 128-token kernel holds 284 VGPRs, one wave per SIMD:
      measured 150 / 188 TOPS against 140 / 169 on 11008 x 4096 / 4096 x 11008, T = 256) */
   const int v = t_gemm >= 3 ? t_gemm - 3 : (T > 64u && kind != AMDC_KIND_Q4_0 ? 0 : 1);
-  u32 ks = t_ksplit > 0 ? (u32)t_ksplit : 0u;
-  if (!ks) {
-    const u64 tiles = (u64)((rows + gh[v].mr - 1u) / gh[v].mr) * ((T + gh[v].nt - 1u) / gh[v].nt);
-    ks = 1;
-    while (ks < 16u && tiles * ks < 3u * cus && ng >= 4u * ks) ks <<= 1;
+  const int kk = kind == AMDC_KIND_Q8_0 ? (v ? K_GEMMH_Q8_N64 : K_GEMMH_Q8_N128)
+                 : kind == AMDC_KIND_Q6_K ? (v ? K_GEMMH_Q6K_N64 : K_GEMMH_Q6K_N128)
+                 : kind == AMDC_KIND_Q4_0 ? (v ? K_GEMMH_Q4_N64 : K_GEMMH_Q4_N128)
+                                          : gh[v].k;
+  const u32 ntt = (T + gh[v].nt - 1u) / gh[v].nt, tiles = (rows + gh[v].mr - 1u) / gh[v].mr * ntt;
+  /* the schedule: whole rounds of resident workgroups (occupancy x CUs) run
+   * their tiles over the whole K; the tiles left over (whole row tiles) are
+   * split in K so that they fill one more round (a 544-tile matrix on 512
+   * slots ran at 221-242 TOPS, a 512-tile one at 323). A tuning K split
+   * splits every tile instead. */
+  u32 nfull, ks;
+  if (t_ksplit > 0) {
+    nfull = 0, ks = (u32)t_ksplit;
+  } else {
+    if (!g_occ[kk] && (H.OccupancyMaxActiveBlocks(&g_occ[kk], g_k[kk], (int)gh[v].threads, 0) != 0 || g_occ[kk] < 1))
+      g_occ[kk] = 1;
+    const u64 cap = (u64)g_occ[kk] * cus;
+    nfull = (u32)((u64)tiles / cap * cap / ntt * ntt);
+    const u32 tail = tiles - nfull;
+    ks = tail ? (u32)(cap / tail) : 1u;
+    if (ks < 1u) ks = 1u;
   }
   if (ks > ng) ks = ng;
   if (ks > 16u) ks = 16u; /* amdc_gemm_reduce adds at most 16 splits */
+  if (ks == 1u) nfull = tiles;
+  const u32 r0 = nfull / ntt * gh[v].mr, trows = rows - r0; /* the split tail's rows */
   const u32 Tp = (T + 127u) / 128u * 128u, K = 32u * nb;
-  const size_t xh_b = (size_t)Tp * K * 2u, sc_b = (size_t)nb * Tp * 4u, part_b = ks > 1u ? (size_t)ks * T * rows * 4u : 0u;
+  const size_t xh_b = (size_t)Tp * K * 2u, sc_b = (size_t)nb * Tp * 4u, part_b = ks > 1u ? (size_t)ks * T * trows * 4u : 0u;
   uint8_t *ws = NULL;
   rc = ws_take(xh_b + 2u * sc_b + part_b, (void **)&ws);
   if (rc) return rc;
@@ -1053,18 +1071,16 @@ static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *x
   void *pa[] = {&xq, &nb, &T, &xs, &xh, &da, &xa, (void *)&Tp};
   rc = launch(K_Q8_PREP, (unsigned)((np + 255u) / 256u), 1, 0, stream, pa);
   if (rc) return rc;
-  const u64 grid = (u64)((rows + gh[v].mr - 1u) / gh[v].mr) * ((T + gh[v].nt - 1u) / gh[v].nt);
+  const u64 grid = (u64)nfull + (u64)(tiles - nfull) * ks;
   if (grid > 0x7FFFFFFFull) return fail(AMDC_EINVAL, "%s: grid too large", op);
-  void *ga[] = {&w, &xh, &da, &xa, &y, &rows, &nb, &bias, &res, &T, (void *)&Tp, &ys, &rs, &part};
-  const int kk = kind == AMDC_KIND_Q8_0 ? (v ? K_GEMMH_Q8_N64 : K_GEMMH_Q8_N128)
-                 : kind == AMDC_KIND_Q6_K ? (v ? K_GEMMH_Q6K_N64 : K_GEMMH_Q6K_N128)
-                 : kind == AMDC_KIND_Q4_0 ? (v ? K_GEMMH_Q4_N64 : K_GEMMH_Q4_N128)
-                                          : gh[v].k;
+  void *ga[] = {&w, &xh, &da, &xa, &y, &rows, &nb, &bias, &res, &T, (void *)&Tp, &ys, &rs, &part, &nfull, &ks};
   g_last_k = kk;
-  HIPCALL(H.ModuleLaunchKernel(g_k[kk], (unsigned)grid, ks, 1, gh[v].threads, 1, 1, 0, stream, ga, NULL));
-  if (ks > 1u) {
-    const u64 n = (u64)rows * T;
-    void *ra[] = {&part, &ks, &y, &rows, &T, &bias, &res, &ys, &rs};
+  HIPCALL(H.ModuleLaunchKernel(g_k[kk], (unsigned)grid, 1, 1, gh[v].threads, 1, 1, 0, stream, ga, NULL));
+  if (ks > 1u) { /* the tail rows: y, bias and res from row r0 */
+    const u64 n = (u64)trows * T;
+    float *yt = y + r0;
+    const float *bt = bias ? bias + r0 : NULL, *rt = res ? res + r0 : NULL;
+    void *ra[] = {&part, &ks, &yt, (void *)&trows, &T, &bt, &rt, &ys, &rs};
     return launch(K_GEMM_REDUCE, (unsigned)((n + 255u) / 256u), 1, 0, stream, ra);
   }
   return AMDC_OK;

@@ -1968,13 +1968,17 @@ __device__ __forceinline__ void a_frag_q6(u32 w0, u32 w1, u32 hw, u32 h, int sc,
 // two, so the prefetched registers alternate instead of being copied). All
 // global addresses are a workgroup-uniform base plus a 32-bit lane offset.
 // Inside a block all MFMAs are issued before their results are used.
-// Split K (gridDim.y > 1): super-blocks [g0, g1) per split; the partial sums
-// go to part[split][t][r] and amdc_gemm_reduce adds them in split order.
+// Schedule (nfull, nks): blocks [0, nfull) are tiles 0 .. nfull - 1 over the
+// whole K, written to y; the other blocks, nfull + j, are the tail tiles,
+// tile nfull + j % tail and K split j / tail of nks (super-blocks [g0, g1)),
+// whose partial sums go to part[split][t][r - r0] (r0 the tail's first row,
+// row stride rows - r0) for amdc_gemm_reduce to add in split order. nfull is
+// a whole number of row tiles; nfull = 0 splits every tile.
 template <int NJ, int KIND>
 __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const _Float16 *__restrict__ xh, const float *__restrict__ DA,
                                            const float *__restrict__ XA, float *__restrict__ y, u32 rows, u32 nb,
                                            const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 Tp, u32 ys, u32 rs,
-                                           float *__restrict__ part) {
+                                           float *__restrict__ part, u32 nfull, u32 nsplit) {
   constexpr u32 NTH = 256u, MR = 64u, NTT = 32u * NJ;
   constexpr u32 BSTR = 72u; // halves per token per stage: 2 blocks x 32 + 8 of padding
   __shared__ __attribute__((aligned(16))) _Float16 sb[2][NTT * BSTR];
@@ -1984,9 +1988,12 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
   __shared__ __attribute__((aligned(16))) float sdw[PB ? 4 : 1][2][8][16]; // per wave: d [row tile][block][row]
   const u32 ng = KIND == AMDC_Q8_0 || KIND == AMDC_Q4_0 ? amdc_ngroups(nb) : nb >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6, wm = w & 1u, wn = w >> 1;
   const u32 i16 = lane & 15u, h = lane >> 4;
-  const u32 ntt = (T + NTT - 1u) / NTT, tt = blockIdx.x % ntt, rt = blockIdx.x / ntt;
+  const u32 ntt = (T + NTT - 1u) / NTT, b = blockIdx.x, full = b < nfull;
+  const u32 tail = (rows + MR - 1u) / MR * ntt - nfull, tj = b - nfull; // tail tiles; a tail block's index among the tail blocks
+  const u32 tile = full ? b : nfull + tj % tail, tt = tile % ntt, rt = tile / ntt;
   const u32 tbase = tt * NTT, twave = 16u * NJ * wn;
-  const u32 ks = blockIdx.y, nks = gridDim.y, g0 = ng * ks / nks, g1 = ng * (ks + 1u) / nks;
+  const u32 ks = full ? 0u : tj / tail, nks = full ? 1u : nsplit, g0 = ng * ks / nks, g1 = ng * (ks + 1u) / nks;
+  const u32 r0 = nfull / ntt * MR; // the tail's first row
   const u32 RB = (u32)amdc_row_bytes_k(KIND, nb), K2 = 64u * nb; // bytes per weight row, per activation row
   // uniform bases (buffer resources), 32-bit lane offsets
   const uint8_t *wbase = W + (u64)rt * MR * RB;
@@ -2205,8 +2212,8 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
       for (u32 v = 0; v < 4u; v++) {
         const u32 r = rt * MR + 32u * wm + 16u * i + 4u * h + v;
         if (r >= rows) continue;
-        if (part) {
-          part[((u64)ks * T + tk) * rows + r] = acc[i][j][v];
+        if (!full) {
+          part[((u64)ks * T + tk) * (rows - r0) + (r - r0)] = acc[i][j][v];
         } else {
           float o = acc[i][j][v];
           if (bias) o = o + bias[r];
@@ -2220,8 +2227,8 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
 #define GEMMH_KERNEL(NAME, NJ, KIND)                                                                                               \
   extern "C" __global__ __launch_bounds__(256) void NAME(const uint8_t *W, const _Float16 *xh, const float *DA, const float *XA,  \
                                                          float *y, u32 rows, u32 nb, const float *bias, const float *res, u32 T,  \
-                                                         u32 Tp, u32 ys, u32 rs, float *part) {                                   \
-    gemmh_body<NJ, KIND>(W, xh, DA, XA, y, rows, nb, bias, res, T, Tp, ys, rs, part);                                             \
+                                                         u32 Tp, u32 ys, u32 rs, float *part, u32 nfull, u32 nsplit) {            \
+    gemmh_body<NJ, KIND>(W, xh, DA, XA, y, rows, nb, bias, res, T, Tp, ys, rs, part, nfull, nsplit);                              \
   }
 GEMMH_KERNEL(amdc_gemmh_m64_n128, 4, AMDC_Q4_K)
 GEMMH_KERNEL(amdc_gemmh_m64_n64, 2, AMDC_Q4_K)
