@@ -314,6 +314,7 @@ static unsigned g_ws_old_n;
  * amdc_op_gemv_noalloc (g_ws_fixed set) every workspace request is served from it, and a request
  * larger than it is an error; otherwise it is unused. */
 static void *g_scratch;
+static u32 *g_split_cnt; /* the kernels' split_count array (device address) */
 static size_t g_scratch_bytes;
 static int g_ws_fixed;
 
@@ -405,6 +406,13 @@ int amdc_open(const char *hsaco) {
   HIPCALL(H.ModuleGetGlobal(&g_scratch, &g_scratch_bytes, g_mod, "scratch"));
   if (!g_scratch || g_scratch_bytes < AMDC_SCRATCH_BYTES)
     return fail(AMDC_EHIP, "amdc_kernels.hsaco: scratch array of %zu bytes, expected %zu", g_scratch_bytes, (size_t)AMDC_SCRATCH_BYTES);
+  {
+    size_t cb = 0;
+    HIPCALL(H.ModuleGetGlobal((void **)&g_split_cnt, &cb, g_mod, "split_count"));
+    if (!g_split_cnt || cb < AMDC_SPLIT_TILES * sizeof(u32))
+      return fail(AMDC_EHIP, "amdc_kernels.hsaco: split_count array of %zu bytes, expected %zu", cb, AMDC_SPLIT_TILES * sizeof(u32));
+    HIPCALL(H.Memset(g_split_cnt, 0, AMDC_SPLIT_TILES * sizeof(u32))); /* each launch leaves them at 0 again */
+  }
   HIPCALL(H.DeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, 0));
   if (t_lanes < 0) t_lanes = envi("AMDC_GEMV_L", 0);
   if (t_unroll < 0) t_unroll = envi("AMDC_GEMV_U", 0);
@@ -427,7 +435,7 @@ void amdc_close(void) {
   if (g_open && g_ws) H.Free(g_ws);
   for (unsigned i = 0; g_open && i < g_ws_old_n; i++) H.Free(g_ws_old[i]);
   g_ws = NULL, g_ws_bytes = 0, g_ws_old_n = 0;
-  g_scratch = NULL, g_scratch_bytes = 0;
+  g_scratch = NULL, g_scratch_bytes = 0, g_split_cnt = NULL;
   if (g_open && g_mod) H.ModuleUnload(g_mod);
   g_mod = NULL;
   g_open = 0;
@@ -687,7 +695,12 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
     int rc = ws_take((size_t)ks * T * rows * 4u, (void **)&part);
     if (rc) return rc;
   }
-  void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs, &part, &tps};
+  /* T <= 8: a split's last workgroup of each row tile adds the partial sums, no reduction launch
+     (MI355X, us: 11008 x 4096 Q4_0 12.8 against 13.4, 5120 x 17408 Q4_K 20.7 against 21.0-21.2);
+     the 16-vector kernels, one workgroup per CU in several rounds, keep the launch (17408 x 5120
+     Q4_K 35.3 against 36.4-36.7 in-kernel: the arrival's round trips delay the next round) */
+  u32 *cnt = ks > 1u && T <= 8u && wgs <= AMDC_SPLIT_TILES ? g_split_cnt : NULL;
+  void *args[] = {&w, &xq, &y, &rows, &nb, &bias, &res, &T, &xs, &ys, &rs, &part, &tps, &cnt};
   const int v16 = T > 8u; /* the 16-vector form */
   const int k = kind == AMDC_KIND_Q6_K ? (v16 ? K_GEMV_Q6K_V16 : K_GEMV_Q6K_V8)
                 : kind == AMDC_KIND_Q4_K ? (v16 ? K_GEMV_Q4K_V16 : K_GEMV_Q4K_V8)
@@ -697,7 +710,7 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
   /* Q4_0 / Q4_K: 8 waves, two per 16 rows, each with half of a tile's super-group pairs */
   const unsigned nth = kind == AMDC_KIND_Q4_0 || kind == AMDC_KIND_Q4_K ? 512u : 256u;
   HIPCALL(H.ModuleLaunchKernel(g_k[k], wgs, ks, 1, nth, 1, 1, 0, stream, args, NULL));
-  if (ks > 1u) {
+  if (ks > 1u && !cnt) {
     const u64 n = (u64)rows * T;
     void *ra[] = {&part, (void *)&ks, &y, &rows, &T, &bias, &res, &ys, &rs};
     return launch(K_GEMM_REDUCE, (unsigned)((n + 255u) / 256u), 1, 0, stream, ra);

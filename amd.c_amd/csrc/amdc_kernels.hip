@@ -2246,10 +2246,11 @@ GEMMH_KERNEL(amdc_gemmh_q4_0_m64_n64, 2, AMDC_Q4_0)
 // default case reads 16 splits). The verify kernels' K ranges are aligned
 // subtrees of their tile tree, so this tree completes it; for the GEMM any
 // fixed order would do.
-template <u32 N> __device__ __forceinline__ float split_sum(const float *__restrict__ part, u64 step, u64 i) {
+template <u32 N, bool AT = false> __device__ __forceinline__ float split_sum(const float *__restrict__ part, u64 step, u64 i) {
   float v[N];
 #pragma unroll
-  for (u32 k = 0; k < N; k++) v[k] = part[k * step + i];
+  for (u32 k = 0; k < N; k++)
+    v[k] = AT ? __hip_atomic_load(part + k * step + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : part[k * step + i];
 #pragma unroll
   for (u32 m = N; m > 1u; m = (m + 1u) / 2u) {
 #pragma unroll
@@ -2259,35 +2260,83 @@ template <u32 N> __device__ __forceinline__ float split_sum(const float *__restr
   return v[0];
 }
 
+template <bool AT = false>
+__device__ __forceinline__ float split_sum_n(const float *__restrict__ part, u32 nks, u64 step, u64 i) {
+  switch (nks) {
+  case 1: return split_sum<1, AT>(part, step, i);
+  case 2: return split_sum<2, AT>(part, step, i);
+  case 3: return split_sum<3, AT>(part, step, i);
+  case 4: return split_sum<4, AT>(part, step, i);
+  case 5: return split_sum<5, AT>(part, step, i);
+  case 6: return split_sum<6, AT>(part, step, i);
+  case 7: return split_sum<7, AT>(part, step, i);
+  case 8: return split_sum<8, AT>(part, step, i);
+  case 9: return split_sum<9, AT>(part, step, i);
+  case 10: return split_sum<10, AT>(part, step, i);
+  case 11: return split_sum<11, AT>(part, step, i);
+  case 12: return split_sum<12, AT>(part, step, i);
+  case 13: return split_sum<13, AT>(part, step, i);
+  case 14: return split_sum<14, AT>(part, step, i);
+  case 15: return split_sum<15, AT>(part, step, i);
+  default: return split_sum<16, AT>(part, step, i);
+  }
+}
+
 extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *__restrict__ part, u32 nks, float *__restrict__ y, u32 rows,
                                                                    u32 T, const float *__restrict__ bias, const float *__restrict__ res,
                                                                    u32 ys, u32 rs) {
   const u64 i = (u64)blockIdx.x * NT + threadIdx.x;
   if (i >= (u64)rows * T) return;
   const u32 t = (u32)(i / rows), r = (u32)(i - (u64)t * rows);
-  const u64 step = (u64)rows * T;
-  float o;
-  switch (nks) {
-  case 1: o = split_sum<1>(part, step, i); break;
-  case 2: o = split_sum<2>(part, step, i); break;
-  case 3: o = split_sum<3>(part, step, i); break;
-  case 4: o = split_sum<4>(part, step, i); break;
-  case 5: o = split_sum<5>(part, step, i); break;
-  case 6: o = split_sum<6>(part, step, i); break;
-  case 7: o = split_sum<7>(part, step, i); break;
-  case 8: o = split_sum<8>(part, step, i); break;
-  case 9: o = split_sum<9>(part, step, i); break;
-  case 10: o = split_sum<10>(part, step, i); break;
-  case 11: o = split_sum<11>(part, step, i); break;
-  case 12: o = split_sum<12>(part, step, i); break;
-  case 13: o = split_sum<13>(part, step, i); break;
-  case 14: o = split_sum<14>(part, step, i); break;
-  case 15: o = split_sum<15>(part, step, i); break;
-  default: o = split_sum<16>(part, step, i); break;
-  }
+  float o = split_sum_n(part, nks, (u64)rows * T, i);
   if (bias) o = o + bias[r];
   if (res) o = res[(u64)t * rs + r] + o;
   y[(u64)t * ys + r] = o;
+}
+
+// Split K without a reduction launch (the verify kernels when the host passes
+// the counters): each workgroup of a row tile stores its partial sums, then
+// arrives on the tile's counter; the last of the nks to arrive adds the
+// tile's partial sums (split_sum's tree, as amdc_gemm_reduce) and writes y,
+// and sets the counter back to 0 for the next launch. Launches that use the
+// counters must not overlap.
+// Memory order: the partial sums are stored and loaded as agent-scope relaxed
+// atomics (split_put, split_sum's loads), which the hardware performs at the
+// agent's coherence point instead of in one XCD's L2 (the workgroups of a
+// tile run on different XCDs); every thread waits for its stores' completion
+// before the barrier that precedes the arrival, and the last workgroup loads
+// after the barrier that follows it. No cache-wide writeback or invalidation
+// is needed (agent-scope fences, one per workgroup, made the launch 2x slower).
+__device__ __align__(256) u32 split_count[AMDC_SPLIT_TILES];
+
+__device__ __forceinline__ void split_put(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+__device__ __forceinline__ bool split_arrive(u32 *cnt, u32 nks) {
+  __shared__ u32 s_last;
+  __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this thread's partial stores are complete
+  __syncthreads();
+  if (threadIdx.x == 0u) {
+    const u32 old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old + 1u == nks;
+    if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last ? 1u : 0u;
+  }
+  __syncthreads();
+  return s_last != 0u;
+}
+
+// The last workgroup's sums: rows [rt0, rt0 + 64) of every token, NTH threads.
+template <u32 NTH>
+__device__ __forceinline__ void split_finish(const float *__restrict__ part, u32 nks, float *__restrict__ y, u32 rows, u32 rt0, u32 T,
+                                             const float *__restrict__ bias, const float *__restrict__ res, u32 ys, u32 rs) {
+  for (u32 e = threadIdx.x; e < 64u * T; e += NTH) {
+    const u32 t = e >> 6, r = rt0 + (e & 63u);
+    if (r >= rows) continue;
+    float o = split_sum_n<true>(part, nks, (u64)rows * T, (u64)t * rows + r);
+    if (bias) o = o + bias[r];
+    if (res) o = res[(u64)t * rs + r] + o;
+    y[(u64)t * ys + r] = o;
+  }
 }
 
 // ------------------------------------------------------------------ verify GEMV on int8 MFMA (T <= 8)
@@ -2382,7 +2431,7 @@ __device__ __forceinline__ u32 v8_bswz(u32 k, u32 q) { return ((k << 1) | (q & 1
 template <int KIND, int NS, int NH, int WS>
 __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
                                            u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 xs, u32 ys,
-                                           u32 rs, float *__restrict__ part, u32 tps) {
+                                           u32 rs, float *__restrict__ part, u32 tps, u32 *__restrict__ arrive) {
   constexpr u32 SC = KIND == AMDC_Q8_0 ? 2u : 1u; // 2 KB chunks (planes of 16 rows) per step
   static_assert(WS == 1 || SC == 1, "the pair split is built for the nibble kinds");
   constexpr bool K4 = KIND == AMDC_Q4_K;
@@ -2673,17 +2722,16 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
 #pragma unroll
       for (u32 v = 0; v < 4u; v++) out[th][v] = cnt == 3u ? st[1][th][v] + st[0][th][v] : cnt == 2u ? st[1][th][v] : st[0][th][v];
   }
-  if (WS > 1 && wp) return; // the first wave of the rows holds the sums
 #pragma unroll
   for (u32 th = 0; th < (u32)NH; th++) {
     const u32 tt = tk + 8u * th;
-    if (pp == 0u && tt < T) {
+    if (!(WS > 1 && wp) && pp == 0u && tt < T) { // the first wave of the rows holds the sums
 #pragma unroll
       for (u32 v = 0; v < 4u; v++) {
         const u32 r = r0 + 4u * h + v;
         if (r >= rows) continue;
         if (part) {
-          part[((u64)ks * T + tt) * rows + r] = out[th][v];
+          split_put(&part[((u64)ks * T + tt) * rows + r], out[th][v]);
         } else {
           float o = out[th][v];
           if (bias) o = o + bias[r];
@@ -2693,38 +2741,40 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
       }
     }
   }
+  if (part && arrive && split_arrive(arrive + blockIdx.x, gridDim.y))
+    split_finish<NTH>(part, gridDim.y, y, rows, rt0, T, bias, res, ys, rs);
 }
 
 extern "C" __global__ __launch_bounds__(512) void amdc_gemv_q4_0_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *part, u32 tps) {
-  gemv8_body<AMDC_Q4_0, 2, 1, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
+                                                                   float *part, u32 tps, u32 *cnt) {
+  gemv8_body<AMDC_Q4_0, 2, 1, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps, cnt);
 }
 extern "C" __global__ __launch_bounds__(512) void amdc_gemv_q4_k_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *part, u32 tps) {
-  gemv8_body<AMDC_Q4_K, 2, 1, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
+                                                                   float *part, u32 tps, u32 *cnt) {
+  gemv8_body<AMDC_Q4_K, 2, 1, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps, cnt);
 }
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *part, u32 tps) {
-  gemv8_body<AMDC_Q8_0, 2, 1, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
+                                                                   float *part, u32 tps, u32 *cnt) {
+  gemv8_body<AMDC_Q8_0, 2, 1, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps, cnt);
 }
 // the same for up to 16 vectors (two token halves per MFMA A operand)
 extern "C" __global__ __launch_bounds__(512) void amdc_gemv_q4_0_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *part, u32 tps) {
-  gemv8_body<AMDC_Q4_0, 2, 2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
+                                                                   float *part, u32 tps, u32 *cnt) {
+  gemv8_body<AMDC_Q4_0, 2, 2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps, cnt);
 }
 extern "C" __global__ __launch_bounds__(512) void amdc_gemv_q4_k_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *part, u32 tps) {
-  gemv8_body<AMDC_Q4_K, 2, 2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
+                                                                   float *part, u32 tps, u32 *cnt) {
+  gemv8_body<AMDC_Q4_K, 2, 2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps, cnt);
 }
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *part, u32 tps) {
-  gemv8_body<AMDC_Q8_0, 1, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
+                                                                   float *part, u32 tps, u32 *cnt) {
+  gemv8_body<AMDC_Q8_0, 1, 2, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps, cnt);
 }
 
 // The verify GEMV for Q6_K (T <= 8). A Q6_K weight's scale changes every 16
@@ -2751,7 +2801,7 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v16(const uint8
 template <int NQ, int NS>
 __device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y,
                                                u32 rows, u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T,
-                                               u32 xs, u32 ys, u32 rs, float *__restrict__ part, u32 tps) {
+                                               u32 xs, u32 ys, u32 rs, float *__restrict__ part, u32 tps, u32 *__restrict__ arrive) {
   constexpr u32 NTK = 4u * NQ; // tokens per launch: NQ groups of 4
   typedef __attribute__((address_space(3))) void lds_t;
   constexpr u32 CH = 128u; // u32x4 per 2 KB chunk (16 rows x 128 bytes)
@@ -2926,7 +2976,7 @@ __device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, co
         const u32 r = r0 + 4u * h + v;
         if (r >= rows) continue;
         if (part) {
-          part[((u64)ks * T + tk) * rows + r] = acc[th][v];
+          split_put(&part[((u64)ks * T + tk) * rows + r], acc[th][v]);
         } else {
           float o = acc[th][v];
           if (bias) o = o + bias[r];
@@ -2936,16 +2986,18 @@ __device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, co
       }
     }
   }
+  if (part && arrive && split_arrive(arrive + blockIdx.x, gridDim.y))
+    split_finish<256u>(part, gridDim.y, y, rows, rt0, T, bias, res, ys, rs);
 }
 
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v8(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                    const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                   float *part, u32 tps) {
-  gemv8_q6k_body<2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
+                                                                   float *part, u32 tps, u32 *cnt) {
+  gemv8_q6k_body<2, 2>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps, cnt);
 }
 // up to 16 vectors: four token groups per A operand, a ring of one step (72 KB of LDS, 2 workgroups per CU)
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_v16(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
                                                                     const float *bias, const float *res, u32 T, u32 xs, u32 ys, u32 rs,
-                                                                    float *part, u32 tps) {
-  gemv8_q6k_body<4, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps);
+                                                                    float *part, u32 tps, u32 *cnt) {
+  gemv8_q6k_body<4, 1>(W, xq, y, rows, nb, bias, res, T, xs, ys, rs, part, tps, cnt);
 }

@@ -65,6 +65,8 @@ enum { AMDC_Q4_0 = 0, AMDC_Q8_0 = 2, AMDC_Q4_K = 3, AMDC_Q6_K = 4 }; /* the refe
 /* The size of the kernels' fixed workspace (the device array `scratch`); the same definition as
  * in include/amdc_q4.h, where the host reads it. */
 #define AMDC_SCRATCH_BYTES ((size_t)64 << 20)
+/* per-tile arrival counters of the split-K verify launches that add their own partial sums */
+#define AMDC_SPLIT_TILES 4096u
 
 AMDC_INLINE uint32_t amdc_ngroups(uint32_t nb) { return (nb + 7u) >> 3; }
 AMDC_INLINE uint64_t amdc_row_bytes(uint32_t nb) { return 144ull * amdc_ngroups(nb); }

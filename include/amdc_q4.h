@@ -20,7 +20,7 @@
  * a host that wants that calls ie_die(amdc_last_error())).
  * Not re-entrant: one thread drives the library (as src/hip.c). The operators
  * that use the library's device workspace (the GEMMs, the split-K multi-vector
- * GEMV, amdc_gemv_*_x with q8 NULL above the fused size) share it: work of
+ * GEMV and its per-tile arrival counters, amdc_gemv_*_x with q8 NULL above the fused size) share it: work of
  * theirs queued on different streams, or in graphs replayed on them, must be
  * ordered (one stream, or an event between), or their results race. The same
  * holds for amdc_op_gemv_noalloc and its fixed workspace. */

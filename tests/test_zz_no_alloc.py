@@ -90,8 +90,8 @@ def test_noalloc_graph_capture(dev):
 
 
 def test_noalloc_rejects_oversize(dev):
-    """5120 x 17408 Q4_K at T = 1024 needs about 77 MB of workspace (64 MiB available): an error, no launch."""
-    c = Case(dev, synth.KIND_Q4_K, 5120, 17408, 1024, seed=5)
+    """5120 x 17408 Q4_K at T = 2048 needs about 97 MB of workspace (64 MiB available): an error, no launch."""
+    c = Case(dev, synth.KIND_Q4_K, 5120, 17408, 2048, seed=5)
     c.Y.fill(0x7F)
     with pytest.raises(dev.AmdcError, match="scratch array holds"):
         c.run(dev.op_gemv_noalloc)
