@@ -1080,9 +1080,8 @@ static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *x
   rc = ws_take(xh_b + 2u * sc_b + part_b, (void **)&ws);
   if (rc) return rc;
   void *xh = ws, *da = ws + xh_b, *xa = ws + xh_b + sc_b, *part = ks > 1u ? (void *)(ws + xh_b + 2u * sc_b) : NULL;
-  const u64 np = (u64)nb * Tp;
   void *pa[] = {&xq, &nb, &T, &xs, &xh, &da, &xa, (void *)&Tp};
-  rc = launch(K_Q8_PREP, (unsigned)((np + 255u) / 256u), 1, 0, stream, pa);
+  rc = launch(K_Q8_PREP, (unsigned)((nb + 7u) / 8u * (Tp / 32u)), 1, 0, stream, pa); /* 8 blocks x 32 tokens per workgroup */
   if (rc) return rc;
   const u64 grid = (u64)nfull + (u64)(tiles - nfull) * ks;
   if (grid > 0x7FFFFFFFull) return fail(AMDC_EINVAL, "%s: grid too large", op);

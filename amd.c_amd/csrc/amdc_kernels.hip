@@ -1850,29 +1850,41 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 extern "C" __global__ __launch_bounds__(256) void amdc_q8_prep(const uint8_t *__restrict__ xq, u32 nb, u32 T, u32 xs,
                                                                _Float16 *__restrict__ xh, float *__restrict__ da, float *__restrict__ xa,
                                                                u32 Tp) {
-  const u64 i = (u64)blockIdx.x * NT + threadIdx.x;
-  if (i >= (u64)nb * Tp) return;
-  const u32 t = (u32)(i / nb), b = (u32)(i - (u64)t * nb);
-  u32x4 o[4] = {(u32x4)(0u), (u32x4)(0u), (u32x4)(0u), (u32x4)(0u)};
-  float d = 0.0f, x = 0.0f;
-  if (t < T) {
-    const uint8_t *xt = xq + (u64)t * xs;
-    const u32x4 lo = *(const u32x4 *)(xt + 32u * b), hi = *(const u32x4 *)(xt + 32u * b + 16u);
-    const u32 w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  // a workgroup: 8 blocks x 32 tokens; thread (token tid / 8, block tid % 8) converts its block (a
+  // token's 8 blocks are 256 contiguous bytes of xq and 512 of xh), and the scales go to da / xa
+  // through the LDS, 32 consecutive tokens of a block per store
+  constexpr u32 BB = 8u, TT = 32u;
+  __shared__ float sd[2][BB][TT + 1u];
+  const u32 nbb = (nb + BB - 1u) / BB, b0 = (blockIdx.x % nbb) * BB, t0 = (blockIdx.x / nbb) * TT;
+  const u32 tl = threadIdx.x / BB, bl = threadIdx.x % BB, t = t0 + tl, b = b0 + bl;
+  if (b < nb) {
+    u32x4 o[4] = {(u32x4)(0u), (u32x4)(0u), (u32x4)(0u), (u32x4)(0u)};
+    float d = 0.0f, x = 0.0f;
+    if (t < T) {
+      const uint8_t *xt = xq + (u64)t * xs;
+      const u32x4 lo = *(const u32x4 *)(xt + 32u * b), hi = *(const u32x4 *)(xt + 32u * b + 16u);
+      const u32 w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
-    for (u32 k = 0; k < 16u; k++) {
-      const int e0 = (int)(int8_t)(w[k >> 1] >> (16u * (k & 1u))), e1 = (int)(int8_t)(w[k >> 1] >> (16u * (k & 1u) + 8u));
-      const u32 v = (u32)__builtin_bit_cast(unsigned short, (_Float16)e0) | ((u32)__builtin_bit_cast(unsigned short, (_Float16)e1) << 16);
-      o[k >> 2][k & 3u] = v;
+      for (u32 k = 0; k < 16u; k++) {
+        const int e0 = (int)(int8_t)(w[k >> 1] >> (16u * (k & 1u))), e1 = (int)(int8_t)(w[k >> 1] >> (16u * (k & 1u) + 8u));
+        const u32 v = (u32)__builtin_bit_cast(unsigned short, (_Float16)e0) | ((u32)__builtin_bit_cast(unsigned short, (_Float16)e1) << 16);
+        o[k >> 2][k & 3u] = v;
+      }
+      d = ((const float *)(xt + 32u * nb))[b];
+      x = d * (float)(int)((const u32 *)(xt + 36u * nb))[b];
     }
-    d = ((const float *)(xt + 32u * nb))[b];
-    x = d * (float)(int)((const u32 *)(xt + 36u * nb))[b];
-  }
-  u32x4 *dst = (u32x4 *)(xh + ((u64)t * nb + b) * 32u);
+    u32x4 *dst = (u32x4 *)(xh + ((u64)t * nb + b) * 32u);
 #pragma unroll
-  for (u32 k = 0; k < 4u; k++) dst[k] = o[k];
-  da[(u64)b * Tp + t] = d;
-  xa[(u64)b * Tp + t] = x;
+    for (u32 k = 0; k < 4u; k++) dst[k] = o[k];
+    sd[0][bl][tl] = d;
+    sd[1][bl][tl] = x;
+  }
+  __syncthreads();
+  const u32 tw = threadIdx.x % TT, bw = threadIdx.x / TT; // 32 tokens of block b0 + bw
+  if (b0 + bw < nb) {
+    da[(u64)(b0 + bw) * Tp + t0 + tw] = sd[0][bw][tw];
+    xa[(u64)(b0 + bw) * Tp + t0 + tw] = sd[1][bw][tw];
+  }
 }
 
 // Four nibbles (bytes 0..15 of n) -> two f16 pairs (1024 + q): each byte
