@@ -1996,6 +1996,7 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
   __shared__ __attribute__((aligned(16))) _Float16 sb[2][NTT * BSTR];
   __shared__ __attribute__((aligned(16))) float sda[2][2][NTT];
   __shared__ __attribute__((aligned(16))) float sxa[2][8][NTT]; // d_a asum of a super-block's 8 blocks, by parity
+  __shared__ float sspare[2][2u * NTT < NTH ? NTH : 1u];
   constexpr bool PB = KIND == AMDC_Q8_0 || KIND == AMDC_Q4_0;     // a d per (row, block): applied per block
   __shared__ __attribute__((aligned(16))) float sdw[PB ? 4 : 1][2][8][16]; // per wave: d [row tile][block][row]
   const u32 ng = KIND == AMDC_Q8_0 || KIND == AMDC_Q4_0 ? amdc_ngroups(nb) : nb >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6, wm = w & 1u, wn = w >> 1;
@@ -2052,10 +2053,13 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
       const u32 ch = tid + c * NTH;
       *(u32x4 *)(&sb[bf][(ch >> 3) * BSTR + 8u * (ch & 7u)]) = rb[c];
     }
-    if (tid < 2u * NTT) {
-      sda[bf][tid / NTT][tid % NTT] = rd;
-      sxa[(s >> 2) & 1u][2u * (s & 3u) + tid / NTT][tid % NTT] = rxv; // the next super-block writes the other half
-    }
+    // every thread stores (threads past 2 NTT into a spare word): with the store conditional the
+    // compiler moved the d_a loads into its branch, after the stage's compute, and waited for them there
+    const bool hv = tid < 2u * NTT;
+    float *pd = hv ? &sda[bf][tid / NTT][tid % NTT] : &sspare[0][tid];
+    float *px = hv ? &sxa[(s >> 2) & 1u][2u * (s & 3u) + tid / NTT][tid % NTT] : &sspare[1][tid]; // the next super-block writes the other half
+    *pd = rd;
+    *px = rxv;
   };
   // the lane's 8 weight bytes (nibbles, or int8), 2 blocks x 2 row tiles, and
   // for Q6_K the high-bit word of its half
