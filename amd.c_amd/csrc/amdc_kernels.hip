@@ -2444,6 +2444,18 @@ __device__ __forceinline__ void vm_wait(u32 n) {
 // (k, q) stay a permutation of 16 consecutive columns.
 __device__ __forceinline__ u32 v8_bswz(u32 k, u32 q) { return ((k << 1) | (q & 1u)) & 15u; }
 
+// A 16-byte-per-lane load into the LDS (lane i's bytes at d + 16 i; d wave-uniform) through an
+// inline-asm buffer load, out of the compiler's sight: the compiler waits for every in-flight load into
+// the LDS (vmcnt 0) before an LDS read it cannot tell apart from the load's target, which drained the
+// verify kernels' weight ring twice per tile. gemv8_body waits for these loads itself (vm_wait,
+// from the fixed issue order); the compiler's own vmcnt waits for its register loads only grow
+// stronger with loads it does not count (loads complete in issue order). m0 is set and used inside
+// the one statement.
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, __attribute__((address_space(3))) void *d, u32 voff) {
+  const u32 m = __builtin_amdgcn_readfirstlane((u32)(__UINTPTR_TYPE__)d);
+  __asm__ volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m), "v"(voff), "s"(rs) : "memory", "m0");
+}
+
 template <int KIND, int NS, int NH, int WS>
 __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
                                            u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 xs, u32 ys,
@@ -2510,9 +2522,9 @@ __device__ __forceinline__ void gemv8_body(const uint8_t *__restrict__ W, const 
       const u32 pl = SC == 1u ? k : 2u * k + c;
       const u32 base = (KIND == AMDC_Q8_0 ? 2048u : 1024u) * t + 16u * ng + 16u * pl * gt;
       lds_t *d = (lds_t *)(slot(s) + 128u * c);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, d, 16, g0 < gt ? wl0 + base + 16u * g0 : OOB, 0, 0, 0);
+      lds_load16(rw, d, g0 < gt ? wl0 + base + 16u * g0 : OOB);
       if constexpr (WS == 1)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_t *)(slot(s) + 128u * c + 64u), 16, g1 < gt ? wl1 + base + 16u * g1 : OOB, 0, 0, 0);
+        lds_load16(rw, (lds_t *)(slot(s) + 128u * c + 64u), g1 < gt ? wl1 + base + 16u * g1 : OOB);
     }
     __asm__ volatile("" ::: "memory");
   };
