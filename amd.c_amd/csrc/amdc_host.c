@@ -1055,7 +1055,7 @@ static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *x
   const u32 ntt = (T + gh[v].nt - 1u) / gh[v].nt, tiles = (rows + gh[v].mr - 1u) / gh[v].mr * ntt;
   /* the schedule: whole rounds of resident workgroups (occupancy x CUs) run
    * their tiles over the whole K; the tiles left over (whole row tiles) are
-   * split in K so that they fill one more round (a 544-tile matrix on 512
+   * split in K to fill part of one more round (a 544-tile matrix on 512
    * slots ran at 221-242 TOPS, a 512-tile one at 323). A tuning K split
    * splits every tile instead. */
   u32 nfull, ks;
@@ -1067,7 +1067,9 @@ static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *x
     const u64 cap = (u64)g_occ[kk] * cus;
     nfull = (u32)((u64)tiles / cap * cap / ntt * ntt);
     const u32 tail = tiles - nfull;
-    ks = tail ? (u32)(cap / tail) : 1u;
+    /* after whole rounds the tail fills half a round (MI355X, 17408 x 5120 T = 256: a tail of 32
+       tiles in 8 splits 302 TOPS, in 16 292); alone, a whole round */
+    ks = tail ? (u32)(cap / ((nfull ? 2u : 1u) * tail)) : 1u;
     if (ks < 1u) ks = 1u;
   }
   if (ks > ng) ks = ng;
