@@ -563,8 +563,8 @@ __device__ __forceinline__ void gemvs_body(const uint8_t *__restrict__ W, const 
   }
   // the Q8 vector's first NSV chunks of the staging loop loaded ahead of the weights: loads complete in
   // issue order, so staged after them the vector waited for every weight load (MI355X: 5120 x 17408
-  // Q4_K 19.7-20.1 -> 18.6-19.3 us)
-  constexpr u32 NSV = 2u;
+  // Q4_K 19.7-20.1 -> 18.6-19.3 us; with 3 chunks, all of its 544 blocks, 14.8-15.2 -> 14.5 us)
+  constexpr u32 NSV = NI >= 2u ? 3u : 2u;
   u32x4 vlo[NSV], vhi[NSV];
   float vd[NSV];
   u32 vas[NSV];
