@@ -665,8 +665,14 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
   /* split K up to one tile of 8 super-groups per workgroup while the grid is under 4 workgroups
      per CU: each workgroup's tile is a chain of dependent loads, so more of them in flight win
      (MI355X, T = 8: 5120 x 17408 Q4_K 23.6 us at 9 splits against 29.7 at 4) */
+  /* Q4_0 / Q4_K at T <= 8 (8-wave workgroups, 2 per CU): up to about one round of resident workgroups (10 %
+     over: 17408 x 5120 Q4_K T = 8 in 2 splits, 544 workgroups, 20.2 us against 21.1 in 3; the other
+     c3 shapes as fast as at their former split) */
+  const int q4 = (kind == AMDC_KIND_Q4_0 || kind == AMDC_KIND_Q4_K) && T <= 8u, kv = K_GEMV_Q4K_V8;
+  if (q4 && !g_occ[kv] && (H.OccupancyMaxActiveBlocks(&g_occ[kv], g_k[kv], 512, 0) != 0 || g_occ[kv] < 1)) g_occ[kv] = 1;
+  const u64 cap = q4 ? (u64)g_occ[kv] * cus * 11u / 10u : 4ull * cus;
   u32 want = 1;
-  while (want < nt && (u64)wgs * (want + 1u) <= 4u * cus) want++;
+  while (want < nt && (u64)wgs * (want + 1u) <= cap) want++;
   if (t_ksplit > 0) want = (u32)t_ksplit < nt ? (u32)t_ksplit : nt;
   if (want > 16u) want = 16u; /* amdc_gemm_reduce adds at most 16 ranges */
   u32 tps = 1;

@@ -2450,10 +2450,11 @@ __device__ __forceinline__ u32 v8_bswz(u32 k, u32 q) { return ((k << 1) | (q & 1
 // verify kernels' weight ring twice per tile. gemv8_body waits for these loads itself (vm_wait,
 // from the fixed issue order); the compiler's own vmcnt waits for its register loads only grow
 // stronger with loads it does not count (loads complete in issue order). m0 is set and used inside
-// the one statement.
+// the one statement; it is a reserved register the compiler does not let a clobber list preserve, and
+// the kernels that use this hold nothing else in it (their built code sets m0 only here).
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, __attribute__((address_space(3))) void *d, u32 voff) {
   const u32 m = __builtin_amdgcn_readfirstlane((u32)(__UINTPTR_TYPE__)d);
-  __asm__ volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m), "v"(voff), "s"(rs) : "memory", "m0");
+  __asm__ volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m), "v"(voff), "s"(rs) : "memory");
 }
 
 template <int KIND, int NS, int NH, int WS>
