@@ -656,16 +656,19 @@ static int ws_take(size_t n, void **p);
 
 /* The verify GEMV on int8 MFMA (T <= 16): 64 rows per workgroup, K split
  * over aligned ranges of tiles (64 blocks each): for T <= 8 until the
- * workgroups fill the CUs four times, for T > 8 by an estimate of the time. A range holds S tiles, S a power of two <= 4, so that its
- * sum is a subtree of the super-group tree (the kernels' order, equal to the
- * decode GEMV's) and amdc_gemm_reduce's tree over the ranges completes it. */
+ * workgroups fill the resident slots about once (Q4 kinds) or the CUs four
+ * times (Q8_0, Q6_K), for T > 8 by an estimate of the time. A range holds S
+ * tiles, S a power of two <= 4, so that its sum is a subtree of the
+ * super-group tree (the kernels' order, equal to the decode GEMV's) and the
+ * split sums' tree over the ranges (in the kernel for T <= 8, else
+ * amdc_gemm_reduce) completes it. */
 static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                         const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
   const u32 nt = (amdc_ngroups(nb) + 7u) / 8u, wgs = (rows + 63u) / 64u, cus = g_cus > 0 ? (u32)g_cus : 256u;
-  /* split K up to one tile of 8 super-groups per workgroup while the grid is under 4 workgroups
-     per CU: each workgroup's tile is a chain of dependent loads, so more of them in flight win
-     (MI355X, T = 8: 5120 x 17408 Q4_K 23.6 us at 9 splits against 29.7 at 4) */
-  /* Q4_0 / Q4_K at T <= 8 (8-wave workgroups, 2 per CU): up to about one round of resident workgroups (10 %
+  /* split K up to one tile of 8 super-groups per workgroup while the grid is under the cap: each
+     workgroup's tile is a chain of dependent loads, so more of them in flight win (MI355X, T = 8:
+     5120 x 17408 Q4_K 23.6 us at 9 splits against 29.7 at 4, on the 4-wave kernel).
+     Q4_0 / Q4_K at T <= 8 (8-wave workgroups, 2 per CU): up to about one round of resident workgroups (10 %
      over: 17408 x 5120 Q4_K T = 8 in 2 splits, 544 workgroups, 20.2 us against 21.1 in 3; the other
      c3 shapes as fast as at their former split) */
   const int q4 = (kind == AMDC_KIND_Q4_0 || kind == AMDC_KIND_Q4_K) && T <= 8u, kv = K_GEMV_Q4K_V8;
