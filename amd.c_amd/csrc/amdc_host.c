@@ -698,6 +698,9 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
      split 3. (Wider workgroups of 80 or 96 rows, to fit 17408 rows in one round, measured slower:
      24.8 against 21-22 split, their extra waves share the SIMDs.) */
   if (T <= 8u && nt <= 3u && t_ksplit <= 0 && wgs <= cus && 4u * wgs >= 3u * cus) tps = 4u;
+  /* T <= 8, 2 tiles of K and at least half a workgroup per CU: unsplit (MI355X, T = 8, us: 11008 x
+     4096 Q8_0 14.3 against 15.2-15.4 in 2 splits, Q4_0 12.2 against 12.3) */
+  if (T <= 8u && nt == 2u && t_ksplit <= 0 && 2u * wgs >= cus) tps = 2u;
   const u32 ks = (nt + tps - 1u) / tps;
   float *part = NULL;
   if (ks > 1u) {
