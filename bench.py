@@ -6,8 +6,9 @@ configuration's GEMV set, dispatched as the reference engine runs it: for c1
 are loaded as one matrix (wqkv = [wq; wk; wv], wgu = [wgate; wup], as
 src/model.c:696, 955 concat_mats), so a step is x -> qkv, o, gate_up, down,
 lm_head: 5 GEMVs, each on an f32 vector quantized to Q8 first (inside the
-GEMV's own launch where nb <= 128, else by a separate amdc_quant_q8 launch:
-6 launches). The same set as 8 separate GEMVs with 5 separate quantizations
+GEMV's own launch: the short rows in every workgroup, down (nb = 344) once
+per CU in the workgroup-per-CU form; 5 launches, as launches_per_step
+reports). The same set as 8 separate GEMVs with 5 separate quantizations
 is timed too (ms_per_step_unmerged). Weight copies are rotated so that the
 weights streamed per step come from HBM (the copies total >= 2 GB, far above
 the 256 MB Infinity Cache). value = weight bytes of the step (the reference's
