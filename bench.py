@@ -548,8 +548,8 @@ def main():
         traffic_child(a.seed)
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build runs on one GPU; the GEMV path shards by rows across GPUs by design only "
-              "(see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py: this build measures one GPU; across GPUs the GEMV path would shard each matrix by rows "
+              "(no multi-GPU run is built). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     amdc.open_device()
     print(f"bench: {amdc.cu_count()} CUs", file=sys.stderr, flush=True)
