@@ -2003,7 +2003,11 @@ __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const 
   const u32 i16 = lane & 15u, h = lane >> 4;
   const u32 ntt = (T + NTT - 1u) / NTT, b = blockIdx.x, full = b < nfull;
   const u32 tail = (rows + MR - 1u) / MR * ntt - nfull, tj = b - nfull; // tail tiles; a tail block's index among the tail blocks
-  const u32 tile = full ? b : nfull + tj % tail, tt = tile % ntt, rt = tile / ntt;
+  // whole-K tiles: the ntt token tiles of a row tile go to one XCD (workgroups are dealt to the 8 XCDs
+  // in turn), 8 workgroups apart, so that the second reads the row tile's weights from that XCD's L2
+  const u32 xg = 8u * ntt, xq = b / xg, xj = b % xg;
+  const u32 tile = full ? (ntt > 1u && nfull % xg == 0u ? (8u * xq + xj % 8u) * ntt + xj / 8u : b) : nfull + tj % tail;
+  const u32 tt = tile % ntt, rt = tile / ntt;
   const u32 tbase = tt * NTT, twave = 16u * NJ * wn;
   const u32 ks = full ? 0u : tj / tail, nks = full ? 1u : nsplit, g0 = ng * ks / nks, g1 = ng * (ks + 1u) / nks;
   const u32 r0 = nfull / ntt * MR; // the tail's first row
