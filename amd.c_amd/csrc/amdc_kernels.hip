@@ -2426,16 +2426,18 @@ __device__ __forceinline__ void v8_barrier() {
 // Wait until at most n vector memory loads of the wave are in flight (gfx9 s_waitcnt: vmcnt in bits
 // 3:0 and 15:14, expcnt and lgkmcnt at their maxima). The loads complete in order, so this is how a
 // wave knows that its loads into the LDS issued before the last n have landed. n is a constant once
-// the caller's loop is unrolled.
+// the caller's loop is unrolled. expcnt(6) marks these waits in the built code (these kernels have no
+// exports, so it waits for nothing): tests/test_isa.py finds them there and checks each count against
+// the vector memory instructions the compiler actually issued.
 __device__ __forceinline__ void vm_wait(u32 n) {
   __asm__ volatile("" ::: "memory");
   switch (n) {
 #define VMW(N)                                                                                                                     \
-  case N: __builtin_amdgcn_s_waitcnt(0x0F70 | ((N) & 15) | (((N) >> 4) << 14)); break;
+  case N: __builtin_amdgcn_s_waitcnt(0x0F60 | ((N) & 15) | (((N) >> 4) << 14)); break;
     VMW(0) VMW(1) VMW(2) VMW(3) VMW(4) VMW(5) VMW(6) VMW(7) VMW(8) VMW(9) VMW(10) VMW(11) VMW(12) VMW(13) VMW(14) VMW(15)
     VMW(16) VMW(17) VMW(18) VMW(19) VMW(20) VMW(21) VMW(22) VMW(23) VMW(24) VMW(25) VMW(26) VMW(27) VMW(28) VMW(29) VMW(30)
 #undef VMW
-  default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  default: __builtin_amdgcn_s_waitcnt(0x0F60); break;
   }
   __asm__ volatile("" ::: "memory");
 }
@@ -2455,10 +2457,12 @@ __device__ __forceinline__ u32 v8_bswz(u32 k, u32 q) { return ((k << 1) | (q & 1
 // from the fixed issue order); the compiler's own vmcnt waits for its register loads only grow
 // stronger with loads it does not count (loads complete in issue order). m0 is set and used inside
 // the one statement; it is a reserved register the compiler does not let a clobber list preserve, and
-// the kernels that use this hold nothing else in it (their built code sets m0 only here).
+// the kernels that use this hold nothing else in it (their built code sets m0 only here). An SALU write
+// of m0 needs one wait state before a buffer load with lds = 1 reads it (the gfx9 hazard the compiler
+// covers with s_nop 0 for its own LDS loads; the assembler does not insert it into inline asm).
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, __attribute__((address_space(3))) void *d, u32 voff) {
   const u32 m = __builtin_amdgcn_readfirstlane((u32)(__UINTPTR_TYPE__)d);
-  __asm__ volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m), "v"(voff), "s"(rs) : "memory");
+  __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m), "v"(voff), "s"(rs) : "memory");
 }
 
 template <int KIND, int NS, int NH, int WS>
