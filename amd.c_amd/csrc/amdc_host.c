@@ -276,7 +276,8 @@ enum {
   K_GEMVM_Q4 = K_GEMVXS_Q4 + 8, /* amdc_gemv_q4_0_m1, amdc_gemv_q4_k_m1 */
   K_CHAIN_S = K_GEMVM_Q4 + 2, /* amdc_chain_s_q4_0, amdc_chain_s_q4_k */
   K_GEMVXW_Q4 = K_CHAIN_S + 2, /* amdc_gemv_q4_0_xw1, amdc_gemv_q4_k_xw1, _xw2 */
-  K_N = K_GEMVXW_Q4 + 3
+  K_GEMVK_Q4 = K_GEMVXW_Q4 + 3, /* amdc_gemv_q4_0_k, _xk, amdc_gemv_q4_k_k, _xk */
+  K_N = K_GEMVK_Q4 + 4
 };
 static const char *const kname[K_N] = {
     "amdc_quant_q8",           "amdc_dots_q4_0",          "amdc_dots_q4_k",          "amdc_gemm_q4_k_n128",
@@ -294,7 +295,8 @@ static const char *const kname[K_N] = {
     "amdc_gemv_q4_0_xs1",      "amdc_gemv_q4_0_xs2",      "amdc_gemv_q4_0_xs3",      "amdc_gemv_q4_0_xs4",
     "amdc_gemv_q4_k_xs1",      "amdc_gemv_q4_k_xs2",      "amdc_gemv_q4_k_xs3",      "amdc_gemv_q4_k_xs4",
     "amdc_gemv_q4_0_m1",       "amdc_gemv_q4_k_m1",       "amdc_chain_s_q4_0",       "amdc_chain_s_q4_k",
-    "amdc_gemv_q4_0_xw1",      "amdc_gemv_q4_k_xw1",      "amdc_gemv_q4_k_xw2"};
+    "amdc_gemv_q4_0_xw1",      "amdc_gemv_q4_k_xw1",      "amdc_gemv_q4_k_xw2",      "amdc_gemv_q4_0_k",
+    "amdc_gemv_q4_0_xk",       "amdc_gemv_q4_k_k",        "amdc_gemv_q4_k_xk"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -450,7 +452,7 @@ int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kern
   if (gemm_kernel < 0 || gemm_kernel > 4) return fail(AMDC_EINVAL, "gemm kernel %d: 0..4", gemm_kernel);
   if (gemm_ksplit < 0 || gemm_ksplit > 16) return fail(AMDC_EINVAL, "gemm ksplit %d: 0..16", gemm_ksplit);
   if (gemv_wgs < 0) return fail(AMDC_EINVAL, "gemv workgroups %d", gemv_wgs);
-  if (gemv_form < 0 || gemv_form > 3) return fail(AMDC_EINVAL, "gemv form %d: 0..3", gemv_form);
+  if (gemv_form < 0 || gemv_form > 4) return fail(AMDC_EINVAL, "gemv form %d: 0..4", gemv_form);
   t_lanes = gemv_lanes, t_unroll = gemv_unroll, t_wgs = gemv_wgs, t_gemm = gemm_kernel, t_ksplit = gemm_ksplit, t_form = gemv_form;
   return AMDC_OK;
 }
@@ -789,6 +791,29 @@ static int gemvs_launch(int kind, const void *w, const void *in, int fq, float *
   return launch(k, nrg, 1, 320u * ng, stream, a);
 }
 
+/* The decode GEMV with K split (amdc_gemv_*_k on a Q8 vector, _xk on an f32 one): ranges of R
+ * super-groups (a power of two, 4..64), one per workgroup of 4 * 64 / R rows, ceil(ng / R) <= 16
+ * ranges; the partial sums in the library's workspace. Returns -1 (nothing launched) where R does
+ * not apply. */
+static int gemvk_launch(int kind, const void *w, const void *in, int fq, float *y, uint32_t rows, uint32_t nb, const float *bias,
+                        const float *res, uint8_t *q8, u32 R, void *stream) {
+  const u32 ng = amdc_ngroups(nb), S = (ng + R - 1u) / R, rpg = 4u * (64u / R), nrg = (rows + rpg - 1u) / rpg;
+  if (R < 4u || R > 64u || (R & (R - 1u)) || S > 16u || (S > 1u && nrg > AMDC_SPLIT_TILES)) return -1;
+  float *part = NULL;
+  if (S > 1u) {
+    int rc = ws_take((size_t)S * rows * 4u, (void **)&part);
+    if (rc) return rc;
+  }
+  u32 *cnt = g_split_cnt;
+  const int k = K_GEMVK_Q4 + (kind == AMDC_KIND_Q4_K ? 2 : 0) + (fq ? 1 : 0);
+  if (fq) {
+    void *a[] = {&w, &in, &y, &rows, &nb, &bias, &res, (void *)&R, &q8, &part, &cnt};
+    return launch(k, nrg, S, 320u * R, stream, a);
+  }
+  void *a[] = {&w, &in, &y, &rows, &nb, &bias, &res, (void *)&R, &part, &cnt};
+  return launch(k, nrg, S, 320u * R, stream, a);
+}
+
 static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
                        const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
   if (kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) {
@@ -827,8 +852,12 @@ static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uin
     return AMDC_OK;
   }
   const u32 ng = amdc_ngroups(nb), L = gemv_lanes(ng), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
+  if (t_form == 4) { /* tuning: the K-split form, ranges of t_lanes super-groups */
+    const int rc = gemvk_launch(kind, w, xq, 0, y, rows, nb, bias, res, NULL, t_lanes > 0 ? (u32)t_lanes : 8u, stream);
+    if (rc != -1) return rc;
+  }
   /* the single-shot kernels (form 3) by default: up to 256 super-groups per row */
-  const int form = t_form > 0 ? t_form : ng <= 256u ? 3 : 2;
+  const int form = t_form > 0 && t_form != 4 ? t_form : ng <= 256u ? 3 : 2;
   if (form == 3) return gemvs_launch(kind, w, xq, 0, y, rows, nb, bias, res, NULL, stream);
   if (form == 2 && (u64)rows * 144u * ng + 144u * ng < (1ull << 32)) {
     /* the decode kernel with buffer loads (32-bit offsets: matrices under 4 GiB), for long rows: up
@@ -923,12 +952,25 @@ static int gemv_x(int kind, const char *op, const void *w, const float *x, float
   if (rc) return rc;
   if (q8 && !aligned16(q8)) return fail(AMDC_EINVAL, "%s: q8 must be 16-byte aligned", op);
   const u32 ng = amdc_ngroups(nb), L = gemv_lanes(ng), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
+  if ((kind == AMDC_KIND_Q4_0 || kind == AMDC_KIND_Q4_K) && t_form == 4) { /* tuning: the K-split form */
+    rc = gemvk_launch(kind, w, x, 1, y, rows, nb, bias, res, q8, t_lanes > 0 ? (u32)t_lanes : 8u, stream);
+    if (rc != -1) return rc;
+  }
   u32 Lw, niw, nthw;
   if ((kind == AMDC_KIND_Q4_0 || kind == AMDC_KIND_Q4_K) && (t_form == 0 || t_form == 3) && t_lanes <= 0 && t_wgs <= 0 &&
       320u * ng <= GEMV_LDS_T1 && gemvxw_pick(kind, ng, rows, &Lw, &niw, &nthw)) {
     const u32 rpgw = (nthw / 64u) * (64u / Lw), gw = (rows + rpgw - 1u) / rpgw;
     void *a[] = {&w, &x, &y, &rows, &nb, &bias, &res, (void *)&Lw, &q8};
     return launch_nt(kind == AMDC_KIND_Q4_K ? K_GEMVXW_Q4 + (int)niw : K_GEMVXW_Q4, gw, 1, nthw, 320u * ng, stream, a);
+  }
+  if (kind == AMDC_KIND_Q4_K && nb > x_fuse_nb && rows <= 8192u && t_form == 0 && t_lanes <= 0 && t_wgs <= 0) {
+    /* long Q4_K rows on few rows: the K-split form, 8 super-groups per range, quantizing its slice in
+       every workgroup, instead of a quantize launch and the GEMV. Measured on MI355X (us, f32 input,
+       K-split at 4 / 8 / 16 / 32 super-groups per range against the two launches): 5120 x 17408 -- /
+       14.1 / 16.3 / 22.9 against 16.6; 34816 x 5120 27.6 (8) against 21.9, 6144 x 5120 and the Q4_0
+       shapes slower than their fused kernels, so only here. */
+    rc = gemvk_launch(kind, w, x, 1, y, rows, nb, bias, res, q8, 8u, stream);
+    if (rc != -1) return rc;
   }
   if (nb > x_fuse_nb || 320u * ng > GEMV_LDS_T1 || kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) {
     if (!q8) {

@@ -391,6 +391,9 @@ __device__ __forceinline__ float item_dot(const typename ItemOf<KIND>::type &it,
 template <u32 NC, u32 NTH = NT> struct FusedQ8T {
   static constexpr u32 BP = NTH / 8u; // blocks per pass
   u32 bp = BP;                         // ... at run time (a workgroup of blockDim.x < NTH threads: blockDim.x / 8)
+  // a K range of the vector (the split-K kernels): super-groups sgb .. of the row go to LDS columns
+  // 0 .., with column stride gc (0: the whole row, stride ng)
+  u32 sgb = 0u, gc = 0u;
   v4f xv[NC];
   __device__ __forceinline__ void load(const float *__restrict__ xf, u32 nb, u32 b0) {
     const u32 tid = threadIdx.x, e = tid & 7u;
@@ -402,7 +405,7 @@ template <u32 NC, u32 NTH = NT> struct FusedQ8T {
     }
   }
   __device__ __forceinline__ void quant(u32 b0, u32 nb, u32 ng, u32x4 *s_lo, u32x4 *s_hi, float *s_d, u32 *s_as, uint8_t *__restrict__ q8out) {
-    const u32 tid = threadIdx.x, e = tid & 7u, nblk = 8u * ng;
+    const u32 tid = threadIdx.x, e = tid & 7u, nblk = 8u * (sgb + (gc ? gc : ng)), st = gc ? gc : ng;
 #pragma unroll
     for (u32 c = 0; c < NC; c++) {
       if (b0 + bp * c >= nblk) break;
@@ -421,7 +424,7 @@ template <u32 NC, u32 NTH = NT> struct FusedQ8T {
       sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0x4E, 0xF, 0xF, false);
       sum += (u32)__builtin_amdgcn_update_dpp(0, (int)sum, 0x141, 0xF, 0xF, false);
       if (b < nblk) {
-        const u32 p = (b & 7u) * ng + (b >> 3);
+        const u32 p = (b & 7u) * st + (b >> 3) - sgb;
         ((u32 *)(e < 4u ? &s_lo[p] : &s_hi[p]))[e & 3u] = word;
         if (e == 0u) s_d[p] = d, s_as[p] = sum;
       }
@@ -2358,6 +2361,102 @@ __device__ __forceinline__ void split_finish(const float *__restrict__ part, u32
     y[(u64)t * ys + r] = o;
   }
 }
+
+
+// The decode GEMV with K split over gridDim.y (amdc_gemv_{q4_0,q4_k}_k / _xk: matrices of few rows
+// and long rows, which leave the CUs short of loads in flight): workgroup (row group, ks) takes the
+// super-groups [ks R, ks R + R) of its rows, R = L a power of two (one super-group per lane, L lanes
+// per row); it stages (_k) or quantizes from the f32 vector (_xk) only that slice of the vector, so
+// the per-workgroup prologue shrinks with the split; the range's leaves go through seg_sum (the
+// range's subtree of the row's super-group tree). The ranges' sums are stored as agent-scope atomics
+// (part[ks][r]) and the last workgroup of the row group to arrive on its counter adds them with
+// split_sum's tree (adjacent first), which completes the row tree: the bits of every other form.
+// gridDim.y = 1 writes y directly.
+template <int KIND, bool FQ>
+__device__ __forceinline__ void gemvk_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
+                                           u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 L,
+                                           const float *__restrict__ xf, uint8_t *__restrict__ q8out, float *__restrict__ part,
+                                           u32 *__restrict__ arrive) {
+  constexpr u32 NTH = 256u;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const u32 ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw;
+  const u32 sg0 = blockIdx.y * L, g = sg0 + l; // the range's first super-group, the lane's
+  const u64 RB = amdc_row_bytes(nb);
+  u32x4 *s_lo = (u32x4 *)smem;
+  u32x4 *s_hi = s_lo + 8u * L;
+  float *s_d = (float *)(s_hi + 8u * L);
+  u32 *s_as = (u32 *)(s_d + 8u * L);
+  const u32 r = blockIdx.x * rpg + wv * rpw + q;
+  const uint8_t *wr = W + (u64)(r < rows ? r : rows - 1u) * RB;
+  FusedQ8T<4u, NTH> fq;
+  fq.sgb = sg0, fq.gc = L;
+  if (FQ) {
+    fq.load(xf, nb, 8u * sg0);
+    __asm__ volatile("" ::: "memory"); // the activation loads ahead of the weight loads
+  }
+  Item it;
+  load_item<KIND>(it, wr, ng, g, g < ng);
+  if (FQ) {
+    const u32 bend = 8u * (sg0 + L);
+    fq.quant(8u * sg0, nb, ng, s_lo, s_hi, s_d, s_as, q8out);
+    for (u32 b0 = 8u * sg0 + fq.bp * 4u; b0 < bend; b0 += fq.bp * 4u) {
+      fq.load(xf, nb, b0);
+      fq.quant(b0, nb, ng, s_lo, s_hi, s_d, s_as, q8out);
+    }
+  } else {
+    for (u32 j = tid; j < 8u * L; j += NTH) { // block b = 8 (sg0 + j % L) + j / L of the row at LDS slot j
+      const u32 b = 8u * (sg0 + j % L) + j / L;
+      u32x4 lo = (u32x4)(0u), hi = (u32x4)(0u);
+      float d = 0.0f;
+      u32 as = 0;
+      if (b < nb) {
+        lo = *(const u32x4 *)(xq + 32u * b);
+        hi = *(const u32x4 *)(xq + 32u * b + 16u);
+        d = ((const float *)(xq + 32u * nb))[b];
+        as = ((const u32 *)(xq + 36u * nb))[b];
+      }
+      s_lo[j] = lo, s_hi[j] = hi, s_d[j] = d, s_as[j] = as;
+    }
+  }
+  __syncthreads();
+  const float leaf = item_dot<KIND>(it, l, L, s_lo, s_hi, s_d, s_as, 0.0f);
+  const float v = seg_sum(g < ng ? leaf : 0.0f, L);
+  if (gridDim.y == 1u) {
+    if (l == 0u && r < rows) {
+      float o = v;
+      if (bias) o = o + bias[r];
+      if (res) o = res[r] + o;
+      y[r] = o;
+    }
+    return;
+  }
+  if (l == 0u && r < rows) split_put(&part[(u64)blockIdx.y * rows + r], v);
+  if (split_arrive(arrive + blockIdx.x, gridDim.y)) {
+    for (u32 rr = tid; rr < rpg; rr += NTH) {
+      const u32 ro = blockIdx.x * rpg + rr;
+      if (ro >= rows) continue;
+      float o = split_sum_n<true>(part, gridDim.y, rows, ro);
+      if (bias) o = o + bias[ro];
+      if (res) o = res[ro] + o;
+      y[ro] = o;
+    }
+  }
+}
+
+#define GEMVK_KERNELS(KN, KIND)                                                                                                        \
+  extern "C" __global__ __launch_bounds__(256) void amdc_gemv_##KN##_k(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb, \
+                                                                        const float *bias, const float *res, u32 L, float *part,       \
+                                                                        u32 *cnt) {                                                    \
+    gemvk_body<KIND, false>(W, xq, y, rows, nb, bias, res, L, nullptr, nullptr, part, cnt);                                            \
+  }                                                                                                                                    \
+  extern "C" __global__ __launch_bounds__(256) void amdc_gemv_##KN##_xk(const uint8_t *W, const float *x, float *y, u32 rows, u32 nb,  \
+                                                                         const float *bias, const float *res, u32 L, uint8_t *q8,       \
+                                                                         float *part, u32 *cnt) {                                      \
+    gemvk_body<KIND, true>(W, nullptr, y, rows, nb, bias, res, L, x, q8, part, cnt);                                                   \
+  }
+GEMVK_KERNELS(q4_0, AMDC_Q4_0)
+GEMVK_KERNELS(q4_k, AMDC_Q4_K)
 
 // ------------------------------------------------------------------ verify GEMV on int8 MFMA (T <= 8)
 

@@ -263,7 +263,9 @@ int amdc_block_dots(int kind, const void *w, const uint8_t *xq, int32_t *out, ui
  * the GEMM's K split (1..16); the decode kernel's form when gemv_unroll is 0
  * (1: the persistent pipelined form, 2: the buffer-load form that keeps the
  * next super-group in flight, 3: the single-shot form, one row group per
- * workgroup with all its loads issued at once; 0: form 3 up to 256
+ * workgroup with all its loads issued at once, 4: the K-split form, ranges of
+ * gemv_lanes super-groups (8 when 0) over the workgroups, the ranges' sums
+ * added by the last to arrive, Q4_0 / Q4_K; 0: form 3 up to 256
  * super-groups per row, else form 2). Also read once from the environment: AMDC_GEMV_L,
  * AMDC_GEMV_U, AMDC_GEMV_WG, AMDC_GEMM_KERNEL, AMDC_GEMM_KSPLIT,
  * AMDC_GEMV_FORM. */

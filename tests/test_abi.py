@@ -40,7 +40,7 @@ def test_dynamic_symbols():
 def test_kernel_names_in_code_object():
     host = open(os.path.join(ROOT, "amd.c_amd", "csrc", "amdc_host.c")).read()
     names = re.findall(r'"(amdc_(?:quant|gemv|gemm|dots|probe|q8|chain|rmsnorm|swiglu)\w*)"', host)
-    assert len(names) == 61
+    assert len(names) == 65
     blob = open(amdc.HSACO_PATH, "rb").read()
     for n in names:
         assert n.encode() in blob, n
@@ -61,7 +61,7 @@ def test_bad_arguments_rejected_before_launch():
     assert rc != 0
     assert L.amdc_set_tuning(3, 0, 0, 0, 0, 0) == 1 and b"power of two" in L.amdc_last_error()
     assert L.amdc_set_tuning(0, 0, 0, 9, 0, 0) == 1
-    assert L.amdc_set_tuning(0, 0, 0, 0, 0, 4) == 1
+    assert L.amdc_set_tuning(0, 0, 0, 0, 0, 5) == 1
     assert L.amdc_set_tuning(0, 0, 0, 0, 0, 0) == 0
 
 

@@ -4,7 +4,7 @@ The reference's multi-token kernels give each token exactly the bits of the
 single-token kernel (kernels/ie_kernels.c:481-482, checked by its
 tools/gemv_eq.c), which its MTP speculative decode relies on to emit exactly
 the greedy tokens (README.md:515-522). Here every decode form (persistent first
-form, second form, single-shot form, at any lane count, and the fused-quantization forms) and the int8-MFMA
+form, second form, single-shot form, K-split form, at any lane count, and the fused-quantization forms) and the int8-MFMA
 verify kernels (T = 1..16, any K split) follow the super-group tree order, so
 on ordinary (rounding) data they all return the same bits; the oracle check
 of these values is in test_gpu_parity.py. Q6_K's verify kernel joins a
@@ -63,6 +63,41 @@ def test_decode_forms_equal(dev, kind, rows, nb):
                 Y.fill(0xFF)
                 dev.gemv_x(kind, W, X, Y, rows, nb)
                 assert np.array_equal(Y.download(np.uint32), ref), ("gemv_x", form, lanes)
+        if kind in (0, 3):  # the K-split form (form 4): ranges of 4 .. 64 super-groups, Q8 and f32 input
+            for lanes in (4, 8, 16, 32, 64):
+                dev.set_tuning(form=4, lanes=lanes)
+                for fx in (False, True):
+                    Y.fill(0xFF)
+                    if fx:
+                        dev.gemv_x(kind, W, X, Y, rows, nb)
+                    else:
+                        dev.gemv(kind, W, Q, Y, rows, nb)
+                    assert np.array_equal(Y.download(np.uint32), ref), ("split", lanes, fx)
+    finally:
+        dev.set_tuning()
+
+
+@pytest.mark.parametrize("kind,rows,nb", [(0, 4096, 344), (3, 5120, 544), (3, 1000, 160), (0, 700, 13)])
+def test_gemv_ksplit_epilogue_and_q8(dev, kind, rows, nb):
+    """The K-split form with bias and residual (added once, by the last range to arrive) and the Q8 copy of
+    its f32 input (each range writes its slice) equal quant_q8 + the single-shot GEMV, on two calls in a
+    row (the tile counters are left at zero)."""
+    W, X, Q, xs = setup(dev, kind, rows, nb, 1, seed=rows)
+    g = np.random.default_rng(rows)
+    B = dev.DevBuf.of(g.standard_normal(rows).astype(np.float32))
+    R = dev.DevBuf.of(g.standard_normal(rows).astype(np.float32))
+    Y, Y2, Q2 = dev.DevBuf(4 * rows), dev.DevBuf(4 * rows), dev.DevBuf(xs)
+    dev.gemv(kind, W, Q, Y, rows, nb, bias=B, res=R)
+    want = Y.download(np.uint32)
+    try:
+        for lanes in (8, 16):
+            dev.set_tuning(form=4, lanes=lanes)
+            for rep in range(2):
+                Y2.fill(0xFF)
+                Q2.fill(0xFF)
+                dev.gemv_x(kind, W, X, Y2, rows, nb, bias=B, res=R, q8=Q2)
+                assert np.array_equal(Y2.download(np.uint32), want), (lanes, rep)
+                assert np.array_equal(Q2.download(np.uint8)[:40 * nb], Q.download(np.uint8)[:40 * nb]), (lanes, rep)
     finally:
         dev.set_tuning()
 
