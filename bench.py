@@ -304,6 +304,46 @@ def prefill_set(steps, seed, timer):
     return out
 
 
+def ceiling_set(seed, timer):
+    """The practical ceiling of each decode launch: a plain read (amdc_probe_read, 16-byte loads, 4 in
+    flight per lane, the best of several grid sizes) of exactly the launch's weight bytes, timed like
+    the GEMVs (one graph of back-to-back launches over rotating copies of >= 1 GB), beside the GEMV on
+    a Q8 vector (amdc_gemv_q4 / _q4k) and on the f32 vector (amdc_gemv_q4_x / _q4k_x, the step's call),
+    for the merged matrices of the c0 / c1 / c2 steps."""
+    out = {}
+    scratch = amdc.DevBuf(4 * 65536)
+    for cname in ("c1", "c2"):
+        cfg = synth.CONFIGS[cname]
+        kind = cfg["kind"]
+        for gi, (name, r, c, _) in enumerate(merged_groups(cfg["shapes"])):
+            if (r, c) in [(v["rows"], v["cols"]) for v in out.values()]:
+                continue
+            nb, b = c // 32, wbytes(r, c, kind)
+            M = Mats(kind, [(name, r, c)], seed + gi, min_bytes=1 << 30)
+            X = amdc.DevBuf.of(synth.activations(1, c, seed + 7)[0])
+            Q, Y = amdc.DevBuf(q8_stride(nb)), amdc.DevBuf(4 * r)
+            amdc.quant_q8(X, Q, nb)
+            rd = {}
+            for grid in (256, 512, 1024, 2048, 4096):
+                rd[grid] = timer.per_launch_ms(lambda j, s, g=grid: amdc.probe_read(M.dev[j % M.copies][0], b // 16 * 16, scratch, g,
+                                                                                    stream=s), M.copies)
+            grid = min(rd, key=rd.get)
+            tq = timer.per_launch_ms(lambda j, s: amdc.gemv(kind, M.dev[j % M.copies][0], Q, Y, r, nb, stream=s), M.copies)
+            kq = amdc.last_kernel()
+            amdc.gemv_x(kind, M.dev[0][0], X, Y, r, nb)
+            kx = amdc.last_kernel()
+            if "_x" not in kx:
+                kx = "amdc_quant_q8 + " + kx
+            tx = timer.per_launch_ms(lambda j, s: amdc.gemv_x(kind, M.dev[j % M.copies][0], X, Y, r, nb, stream=s), M.copies)
+            us = lambda t: round(t * 1e3, 3)
+            out[f"{cname}:{name}"] = {"rows": r, "cols": c, "bytes": b, "read_us": us(rd[grid]), "read_grid": grid,
+                                      "read_hbm_frac": round(b / rd[grid] / 1e6 / HBM_PEAK_GBS, 4),
+                                      "gemv_q8_us": us(tq), "gemv_q8_kernel": kq, "gemv_q8_of_read": round(rd[grid] / tq, 3),
+                                      "gemv_f32_us": us(tx), "gemv_f32_kernel": kx, "gemv_f32_of_read": round(rd[grid] / tx, 3)}
+            del M
+    return out
+
+
 def k8_set(seed, timer):
     """The Q8_0 and Q6_K decode GEMVs at the sizes they have in the c1 / c2 models (the Q6_K
     matrices of a Q4_K_M file: ffn_down, attn_v, lm_head; Q8_0 projections): us per launch and the
@@ -537,8 +577,8 @@ def main():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--quick", action="store_true", help="headline only (no c0/c2/c3/c4 detail, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--sets", default="c0,c2,c3,c4,producers,k8,load",
-                    help="detail sets to run after the headline (comma list of c0, c2, c3, c4, producers, k8, load)")
+    ap.add_argument("--sets", default="c0,c2,c3,c4,producers,ceiling,k8,load",
+                    help="detail sets to run after the headline (comma list of c0, c2, c3, c4, producers, ceiling, k8, load)")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run the probe copy kernel over 256 MiB 3 times (the FETCH_SIZE / WRITE_SIZE yardstick)")
     ap.add_argument("--no-traffic", action="store_true", help="no rocprofv3 counter passes (roofline.traffic null)")
@@ -577,6 +617,7 @@ def main():
     for key, name, fn in (("c3", "c3", lambda: verify_set(a.steps, a.seed + 2000, timer)),
                           ("c4", "c4", lambda: prefill_set(a.steps, a.seed + 3000, timer)),
                           ("producers", "producers", lambda: producers_set(timer)),
+                          ("ceiling", "decode_ceiling", lambda: ceiling_set(a.seed + 6000, timer)),
                           ("k8", "q8_0_q6_k", lambda: k8_set(a.seed + 4000, timer)),
                           ("load", "gguf_load", lambda: load_set(a.seed + 5000))):
         if key in sets:
