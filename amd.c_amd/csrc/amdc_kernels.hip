@@ -2924,15 +2924,17 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q8_0_v16(const uint8
 //     t (4 tokens per MFMA, two MFMAs for 8), zeros in the other quarters (LDS
 //     holds only the nonzero quarter of each column; the other lanes use 0)
 // so that C[r][4 q + t] is the exact half dot sum (q - 32) a of ie_q6k_dots for
-// quarter q. Per element acc = fma(s C, d_a, acc), s = d sc of the quarter (the
-// reference's fma(fma(s1, d1, s0 d0), d_a, acc), src/cpu.c:142, regrouped);
-// the four quarters of a token are joined at the end (row_ror 8, then 4).
+// quarter q. The float steps are the decode GEMV's, in its order (bit-equal to
+// it): the lanes of quarter 0 (2) take quarter 1's (3's) dot from the lane 4
+// columns up and apply leaf = fma(fma(s1, d1, s0 d0), d_a, leaf) per block
+// (src/cpu.c:142, s = d sc), a leaf per super-group; the tile's 8 leaves join
+// as ((g0 + g1) + (g2 + g3)) + ... (row_ror:8 for the pairs), and the tiles of
+// a range and the ranges as gemv8_body's (the super-group tree).
 // Tiles of 8 super-groups as gemv8_body: activations and d_a staged in LDS in
 // B form. The weights go into LDS as in gemv8_body, in whole 128-byte lines: a
 // ring step is the nibble planes 2m, 2m + 1 and high-bit plane m of the wave's
-// 16 rows (6 KB), 2 steps per wave. The scales: each wave's table of sc + 128
-// per (sub-block, half, row) in bytes and d per (super-group, row); s = d sc
-// is formed as fma(d, sc + 128, -128 d), the same single rounding as d * sc.
+// 16 rows (6 KB), 2 steps per wave. The scales: each wave's table of the int8
+// sc per (sub-block, half, row) and d per (super-group, row); s = d sc (exact).
 // Split K over gridDim.y.
 template <int NQ, int NS>
 __device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y,
@@ -2945,7 +2947,7 @@ __device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, co
   __shared__ __attribute__((aligned(16))) u32x4 sw1[NS > 1 ? 4 : 1][NS > 1 ? 3u * CH : 1u];
   __shared__ __attribute__((aligned(16))) u32x4 sB[NQ][32][16]; // [token group][pair p + 4 k][column]: the column's nonzero quarter
   __shared__ __attribute__((aligned(16))) float sda[64][NTK];      // d_a [sub-block][token]
-  __shared__ __attribute__((aligned(16))) uint8_t ssc[4][64][2][16]; // per wave: sc + 128 [sub-block][half][row]
+  __shared__ __attribute__((aligned(16))) uint8_t ssc[4][64][2][16]; // per wave: the int8 sc [sub-block][half][row]
   __shared__ __attribute__((aligned(16))) float sd[4][8][16];        // per wave: d [super-group][row]
   const u32 ng = nb >> 3, nt = (ng + 7u) >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
   const u32 i16 = lane & 15u, h = lane >> 4, n = i16, qn = n >> 2, tq = n & 3u;
@@ -2964,22 +2966,31 @@ __device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, co
     if (s == 0u || NS == 1) return sw0[w];
     return sw1[NS > 1 ? w : 0u];
   };
-  // step m of tile t into slot s (off: every load out of range)
+  // step m of tile t into slot s (off: every load out of range). The slot was read by the planes just
+  // before: the wave's LDS reads are complete (lgkmcnt 0) and ordered before the refill (the compiler
+  // does not order LDS reads against these loads into the LDS; with a ring of one step the last reads
+  // sit right before the refill)
   auto issue = [&](u32 t, u32 m, u32 s, bool on) {
     const u32 gt = on ? gtile(t) : 0u;
+    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
+    __asm__ volatile("" ::: "memory");
 #pragma unroll
     for (u32 c = 0; c < 3u; c++) {
       const u32 base = c < 2u ? 16u * ng + D + 1024u * t + 16u * (2u * m + c) * gt : 144u * ng + D + 512u * t + 16u * m * gt;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_t *)(slot(s) + CH * c), 16, g0 < gt ? wl0 + base + 16u * g0 : OOB, 0, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_t *)(slot(s) + CH * c + 64u), 16, g1 < gt ? wl1 + base + 16u * g1 : OOB, 0, 0, 0);
     }
+    __asm__ volatile("" ::: "memory");
   };
   u32x4 ra4[2 * NQ];
   float rd[NQ];
   u32x4 rh[2];
   u32 rdd[2];
-  auto fetch_tile = [&](u32 t) {
-    const u32 gt = gtile(t);
+  // the tile's activations, d_a and headers into registers (on false: every load past the resource,
+  // zeros, so that the loads in flight count statically)
+  constexpr u32 NFT = 3u * NQ + 4u; // its loads
+  auto fetch_tile = [&](u32 t, bool on) {
+    const u32 gt = on ? gtile(t) : 0u;
 #pragma unroll
     for (u32 c = 0; c < 2u * NQ; c++) {
       const u32 i = tid + c * NT, half = i & 1u, bl = (i >> 1) & 63u, tok = i >> 7, b = 64u * t + bl;
@@ -3019,57 +3030,72 @@ __device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, co
       for (u32 k = 0; k < 8u; k++)
 #pragma unroll
         for (u32 e = 0; e < 2u; e++)
-          ssc[w][8u * gl + k][e][i16] = (uint8_t)((hword(rh[q], k >> 1) >> (16u * (k & 1u) + 8u * e)) + 128u);
+          ssc[w][8u * gl + k][e][i16] = (uint8_t)(hword(rh[q], k >> 1) >> (16u * (k & 1u) + 8u * e));
     }
   };
-  float acc[NQ][4] = {};
+  float lf[NQ][4][4]; // the leaves: [token group][pair p: super-group 2 p + qn / 2 (lanes of an even quarter qn)][row 4 h + v]
   const u32 nth = (T + 3u) >> 2; // token groups with tokens (group 0 always: T >= 1)
-  v4f d4[4], n4[4];                 // d and -128 d of this lane's output rows, super-group 2 p + qn / 2
+  v4f d4[4];                        // d of this lane's output rows, super-group 2 p + qn / 2
   // the MFMAs of plane k = 2 m + e from slot s
   auto plane = [&](u32 m, u32 e, u32 npair, u32 s) {
     const u32 k = 2u * m + e;
     const u32x4 *sl = slot(s);
-    v4i c[NQ][4];
+    v4i c[NQ][2];
     const u32 sft = 4u * (h & 1u);
+    auto mfma = [&](u32 p) {
+      const u32 col = (2u * p + (h >> 1)) ^ v8_swz(i16);
+      const u32x4 wq = sl[CH * e + 8u * i16 + col];
+      const u32 hq = ((const u32 *)(sl + 2u * CH + 8u * i16 + col))[2u * e + (h & 1u)];
+      u32 a[4];
 #pragma unroll
-    for (u32 p = 0; p < 4u; p++) { // the MFMAs of the plane first
-      if (p < npair) {
-        const u32 col = (2u * p + (h >> 1)) ^ v8_swz(i16);
-        const u32x4 wq = sl[CH * e + 8u * i16 + col];
-        const u32 hq = ((const u32 *)(sl + 2u * CH + 8u * i16 + col))[2u * e + (h & 1u)];
-        u32 a[4];
-#pragma unroll
-        for (u32 i = 0; i < 4u; i++) {
-          const u32 v = ((wq[i] >> sft) & 0x0F0F0F0Fu) | (((hq >> (2u * i)) & 0x03030303u) << 4);
-          a[i] = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
-        }
-        const v4i av = {(int)a[0], (int)a[1], (int)a[2], (int)a[3]};
-#pragma unroll
-        for (u32 th = 0; th < (u32)NQ; th++)
-          if (th == 0u || th < nth)
-            c[th][p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, h == qn ? __builtin_bit_cast(v4i, sB[th][p + 4u * k][n]) : (v4i){0, 0, 0, 0},
-                                                             (v4i){0, 0, 0, 0}, 0, 0, 0);
+      for (u32 i = 0; i < 4u; i++) {
+        const u32 v = ((wq[i] >> sft) & 0x0F0F0F0Fu) | (((hq >> (2u * i)) & 0x03030303u) << 4);
+        a[i] = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
       }
-    }
+      const v4i av = {(int)a[0], (int)a[1], (int)a[2], (int)a[3]};
+#pragma unroll
+      for (u32 th = 0; th < (u32)NQ; th++)
+        if (th == 0u || th < nth)
+          c[th][p & 1u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, h == qn ? __builtin_bit_cast(v4i, sB[th][p + 4u * k][n]) : (v4i){0, 0, 0, 0},
+                                                                 (v4i){0, 0, 0, 0}, 0, 0, 0);
+    };
+    // pair p + 1's MFMAs go out before pair p's results are used (two result sets live)
+    mfma(0u);
 #pragma unroll
     for (u32 p = 0; p < 4u; p++) {
       if (p >= npair) break;
-      const u32 bl = 8u * (2u * p + (qn >> 1)) + k; // this lane's sub-block (column quarter qn)
-      const u32 sc4 = *(const u32 *)&ssc[w][bl][qn & 1u][4u * h];
-      v4f s4;
+      if (p + 1u < npair) mfma(p + 1u);
+      // the lanes of an even quarter qn (half 0 of super-group 2 p + qn / 2) take half 1's dot from the
+      // lane 4 columns up (row_ror:12) and apply the decode GEMV's block step, src/cpu.c:142:
+      // leaf = fma(fma(s1, d1, s0 d0), d_a, leaf), s = d sc (the lanes of odd quarters compute unused values)
+      const u32 bl = 8u * (2u * p + (qn >> 1)) + k; // this lane's sub-block
+      const u32 sc0 = *(const u32 *)&ssc[w][bl][0][4u * h], sc1 = *(const u32 *)&ssc[w][bl][1][4u * h];
+      v4f s0, s1;
 #pragma unroll
-      for (u32 v = 0; v < 4u; v++) s4[v] = __builtin_fmaf(d4[p][v], (float)((sc4 >> (8u * v)) & 0xFFu), n4[p][v]); // v_cvt_f32_ubyte<v>
+      for (u32 v = 0; v < 4u; v++) {
+        s0[v] = d4[p][v] * (float)(int)(int8_t)(sc0 >> (8u * v)); // d sc, exact (as the decode GEMV's dsc * sc)
+        s1[v] = d4[p][v] * (float)(int)(int8_t)(sc1 >> (8u * v));
+      }
 #pragma unroll
       for (u32 th = 0; th < (u32)NQ; th++) {
         if (th > 0u && th >= nth) break;
         const float da = sda[bl][tq + 4u * th];
 #pragma unroll
-        for (u32 v = 0; v < 4u; v++) acc[th][v] = __builtin_fmaf(s4[v] * (float)c[th][p][v], da, acc[th][v]);
+        for (u32 v = 0; v < 4u; v++) {
+          const int d0 = c[th][p & 1u][v], d1 = __builtin_amdgcn_update_dpp(0, d0, 0x12C, 0xF, 0xF, false); // row_ror:12: column n + 4
+          lf[th][p][v] = __builtin_fmaf(__builtin_fmaf(s1[v], (float)d1, s0[v] * (float)d0), da, lf[th][p][v]);
+        }
       }
     }
   };
+  // the tree over the range's tiles, as gemv8_body: st[j] a pending subtree of 2^j tiles, out the range's sum
+  float st[2][NQ][4], out[NQ][4];
+#pragma unroll
+  for (u32 th = 0; th < (u32)NQ; th++)
+#pragma unroll
+    for (u32 v = 0; v < 4u; v++) out[th][v] = 0.0f, st[0][th][v] = st[1][th][v] = 0.0f;
   if (t0 < t1) {
-    fetch_tile(t0);
+    fetch_tile(t0, true);
 #pragma unroll
     for (u32 m = 0; m < (u32)NS; m++) issue(t0, m, m, true);
   }
@@ -3082,26 +3108,61 @@ __device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, co
 #pragma unroll
     for (u32 p = 0; p < 4u; p++) {
       d4[p] = *(const v4f *)&sd[w][2u * p + (qn >> 1)][4u * h];
-      n4[p] = -128.0f * d4[p];
     }
-    if (more) fetch_tile(t + 1u);
+#pragma unroll
+    for (u32 th = 0; th < (u32)NQ; th++)
+#pragma unroll
+      for (u32 p = 0; p < 4u; p++)
+#pragma unroll
+        for (u32 v = 0; v < 4u; v++) lf[th][p][v] = 0.0f;
 #pragma unroll
     for (u32 m = 0; m < 4u; m++) {
+      // step m's loads into its slot have landed: issued after them, in this fixed order, are the next
+      // step's 6 (NS = 2) and, for steps 1 and 2 (NS = 2) or 1 (NS = 1), the next tile's activation loads
+      // (issued after step 0). The compiler's own waits are not relied on: it takes a 1 KB load into the
+      // LDS for a 16-byte store and moved the high-bit word read of a freshly refilled slot above its
+      // wait (with a one-step ring that read the previous step's bits)
+      vm_wait(NS == 2 ? 6u + (m == 1u || m == 2u ? NFT : 0u) : (m == 1u ? NFT : 0u));
       plane(m, 0u, npair, m % (u32)NS);
       plane(m, 1u, npair, m % (u32)NS);
       // issued also after the range's last tile (as zeros), so that the waits count statically
       if (m + (u32)NS < 4u) issue(t, m + (u32)NS, m % (u32)NS, true);
       else issue(t + 1u, m + (u32)NS - 4u, m % (u32)NS, more);
+      if (m == 0u) fetch_tile(t + 1u, more); // in flight during this tile (issued also past the range)
     }
+    // the tile's subtree: super-groups (2 p, 2 p + 1) from quarters 0 and 2 (row_ror:8), then ((0 + 1) + (2 + 3)),
+    // then into the tree over tiles (c: the tiles before this one in the range)
+    const u32 c = t - t0;
+#pragma unroll
+    for (u32 th = 0; th < (u32)NQ; th++)
+#pragma unroll
+      for (u32 v = 0; v < 4u; v++) {
+        float pr[4];
+#pragma unroll
+        for (u32 p = 0; p < 4u; p++) pr[p] = lf[th][p][v] + dpp<0x128>(lf[th][p][v]); // row_ror:8
+        float xv = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+        if (c & 1u) {
+          xv = st[0][th][v] + xv;
+          if (c & 2u) out[th][v] = st[1][th][v] + xv; // a range of 4 tiles is complete
+          else st[1][th][v] = xv;
+        } else {
+          st[0][th][v] = xv;
+        }
+      }
   }
-  // join the four quarters of each token (columns t, t + 4, t + 8, t + 12 of a row of 16 lanes)
+  // a range of fewer than 4 tiles: its pending subtrees, from the lowest level up (zero tiles past the range)
+  const u32 cnt = t1 > t0 ? t1 - t0 : 0u;
+  if (cnt < 4u) {
+#pragma unroll
+    for (u32 th = 0; th < (u32)NQ; th++)
+#pragma unroll
+      for (u32 v = 0; v < 4u; v++) out[th][v] = cnt == 3u ? st[1][th][v] + st[0][th][v] : cnt == 2u ? st[1][th][v] : st[0][th][v];
+  }
+  float acc[NQ][4];
 #pragma unroll
   for (u32 th = 0; th < (u32)NQ; th++)
 #pragma unroll
-    for (u32 v = 0; v < 4u; v++) {
-      acc[th][v] += dpp<0x128>(acc[th][v]); // row_ror:8
-      acc[th][v] += dpp<0x124>(acc[th][v]); // row_ror:4
-    }
+    for (u32 v = 0; v < 4u; v++) acc[th][v] = out[th][v];
   if (qn == 0u) {
 #pragma unroll
     for (u32 th = 0; th < (u32)NQ; th++) {

@@ -89,9 +89,16 @@ class Timer:
 
     def __init__(self):
         self.S = amdc.Stream()
+        self.kept = []
 
     def graph(self, fn):
-        return amdc.Graph(self.S, fn)
+        # every graph stays alive until the process ends: a profiler's graph-launch hook (rocprofv3
+        # --kernel-trace) may still hold a replayed graph when its Python object would be collected,
+        # and destroying the executable graph under it is the one use-after-free a run of this file
+        # can cause (the library destroys nothing a replay still uses: replay_ms synchronizes first)
+        g = amdc.Graph(self.S, fn)
+        self.kept.append(g)
+        return g
 
     def replay_ms(self, graphs, reps, warmup=2):
         """ms per replay of the graphs, launched round robin back to back (reps replays)."""
@@ -234,7 +241,8 @@ def gemv_set(cfg_name, steps, warmup, seed, timer):
             "ms_per_step_launches": ms_launches, "ms_per_step_chain": ms_chain["streaming"],
             "ms_per_step_chain_persistent": ms_chain["persistent"],
             "step_form": "chain" if ms_chain["streaming"] <= ms_launches else "launches",
-            "launches_per_step": len(launches), "per_shape": per, "step_launches": launches,
+            "launches_per_step": sum(2 if l["kernel"].startswith("amdc_quant_q8 + ") else 1 for l in launches),
+            "per_shape": per, "step_launches": launches,
             "dominant_kernel": dom, "dominant_launches": kt[dom][2],
             "dominant_bytes_per_launch": kt[dom][1] / kt[dom][2], "dominant_us_per_launch": kt[dom][0] / kt[dom][2],
             "dominant_GBps": kt[dom][1] / kt[dom][0] / 1e3,

@@ -5,11 +5,9 @@ single-token kernel (kernels/ie_kernels.c:481-482, checked by its
 tools/gemv_eq.c), which its MTP speculative decode relies on to emit exactly
 the greedy tokens (README.md:515-522). Here every decode form (persistent first
 form, second form, single-shot form, K-split form, at any lane count, and the fused-quantization forms) and the int8-MFMA
-verify kernels (T = 1..16, any K split) follow the super-group tree order, so
-on ordinary (rounding) data they all return the same bits; the oracle check
-of these values is in test_gpu_parity.py. Q6_K's verify kernel joins a
-block's two half sums in another order (within the 1e-5 bound, not bit-equal)
-and is left out.
+verify kernels (T = 1..16, any K split, all four kinds) follow the super-group
+tree order, so on ordinary (rounding) data they all return the same bits; the
+oracle check of these values is in test_gpu_parity.py and test_gpu_k8.py.
 """
 import numpy as np
 import pytest
@@ -25,7 +23,7 @@ def q8_stride(nb):
 
 # (kind, rows, nb): ragged rows, Q4_0 partial super-groups (nb % 8 != 0), short and long rows, a partial last tile
 SHAPES = [(0, 70, 13), (0, 130, 43), (0, 200, 128), (0, 150, 344), (0, 33, 511), (3, 90, 40), (3, 130, 160),
-          (3, 77, 544), (3, 64, 1024), (2, 100, 100), (2, 70, 344)]
+          (3, 77, 544), (3, 64, 1024), (2, 100, 100), (2, 70, 344), (4, 100, 160), (4, 70, 544), (4, 64, 40), (4, 130, 1024)]
 
 
 def setup(dev, kind, rows, nb, T, seed):

@@ -14,7 +14,8 @@ what the kernels rely on but the compiler cannot see:
   write of m0 that addresses it and the load (the gfx9 hazard); in the verify
   kernels whose LDS loads are inline asm (lds_load16), m0 is written only right
   before such a load;
-* the explicit waits of those kernels (vm_wait, marked by expcnt(6)): a plane's
+* the explicit waits of those kernels and of the Q6_K verify kernels (vm_wait,
+  marked by expcnt(6)): a plane's
   ring slot was filled by a load into the LDS issued one ring step earlier,
   and the count n of the wait must leave that load complete, i.e. at least n
   vector memory instructions were issued after it. The check walks the
@@ -32,15 +33,22 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HSACO = os.path.join(ROOT, "amd.c_amd", "amdc_kernels.hsaco")
 LLVM = "/opt/rocm/llvm/bin"
 
-# kernels whose loads into the LDS are inline asm, with (ring steps, LDS loads per ring step):
-# gemv8_body<KIND, NS, NH, WS>: NS steps, SC * (2 if WS == 1 else 1) loads per step
+# kernels whose loads into the LDS are inline asm, with (ring steps, LDS loads per ring step, explicit
+# waits per tile): gemv8_body<KIND, NS, NH, WS>: NS steps, SC * (2 if WS == 1 else 1) loads per step,
+# a wait per plane
 INLINE_LDS = {
-    "amdc_gemv_q4_0_v8": (2, 1),
-    "amdc_gemv_q4_k_v8": (2, 1),
-    "amdc_gemv_q8_0_v8": (2, 4),
-    "amdc_gemv_q4_0_v16": (2, 1),
-    "amdc_gemv_q4_k_v16": (2, 1),
-    "amdc_gemv_q8_0_v16": (1, 4),
+    "amdc_gemv_q4_0_v8": (2, 1, 8),
+    "amdc_gemv_q4_k_v8": (2, 1, 8),
+    "amdc_gemv_q8_0_v8": (2, 4, 8),
+    "amdc_gemv_q4_0_v16": (2, 1, 8),
+    "amdc_gemv_q4_k_v16": (2, 1, 8),
+    "amdc_gemv_q8_0_v16": (1, 4, 8),
+}
+# kernels whose loads into the LDS are the compiler's builtin but whose ring reads wait explicitly:
+# gemv8_q6k_body<NQ, NS>: NS steps of 6 loads, a wait per step (4 per tile)
+BUILTIN_LDS = {
+    "amdc_gemv_q6_k_v8": (2, 6, 4),
+    "amdc_gemv_q6_k_v16": (1, 6, 4),
 }
 
 
@@ -172,10 +180,10 @@ def _check_waits(name, seq, marks, ns, dps):
 
 def test_explicit_waits_cover_the_ring(code):
     funcs, _ = code
-    for k, (ns, dps) in INLINE_LDS.items():
+    for k, (ns, dps, nw) in {**INLINE_LDS, **BUILTIN_LDS}.items():
         ins = funcs[k]
         marked = [i for i, (_, mn, ops) in enumerate(ins) if mn == "s_waitcnt" and "expcnt(6)" in ops]
-        assert len(marked) == 8, f"{k}: {len(marked)} marked waits (one per plane of a tile expected)"
+        assert len(marked) == nw, f"{k}: {len(marked)} marked waits ({nw} per tile expected)"
         # the tile loop: the backward branch whose range holds the marked waits
         loops = [(_target(ins, i), i) for i, (_, mn, _) in enumerate(ins) if mn.startswith(("s_branch", "s_cbranch"))]
         loops = [(s, e) for s, e in loops if s is not None and s <= marked[0] and marked[-1] < e]
