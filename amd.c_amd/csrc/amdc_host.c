@@ -543,23 +543,53 @@ int amdc_graph_begin(void *stream) {
   HIPCALL(H.StreamBeginCapture(stream, hipStreamCaptureModeRelaxed));
   return AMDC_OK;
 }
+/* The handle of amdc_graph_end: the executable graph and the graph it was instantiated from. The
+ * template stays alive until amdc_graph_destroy: HIP allows destroying it right after
+ * instantiation, but a tool that intercepts graph launches (a profiler's launch hook) may look an
+ * executable graph's nodes up through it, so nothing a replay can reach is freed before the
+ * executable graph itself. */
+typedef struct {
+  hipGraphExec_t x;
+  hipGraph_t g;
+} amdc_graph_t;
+
 int amdc_graph_end(void *stream, void **exec) {
   NEED_OPEN();
+  if (!exec) return fail(AMDC_EINVAL, "graph_end: exec is NULL");
+  *exec = NULL;
   hipGraph_t g = NULL;
   HIPCALL(H.StreamEndCapture(stream, &g));
-  const hipError_t e = H.GraphInstantiate(exec, g, NULL, NULL, 0);
-  H.GraphDestroy(g);
-  if (e) return fail(AMDC_EHIP, "hipGraphInstantiate: %s (%d)", H.GetErrorString(e), e);
+  amdc_graph_t *h = (amdc_graph_t *)calloc(1, sizeof *h);
+  if (!h) {
+    H.GraphDestroy(g);
+    return fail(AMDC_EHIP, "graph_end: out of host memory");
+  }
+  const hipError_t e = H.GraphInstantiate(&h->x, g, NULL, NULL, 0);
+  if (e) {
+    H.GraphDestroy(g);
+    free(h);
+    return fail(AMDC_EHIP, "hipGraphInstantiate: %s (%d)", H.GetErrorString(e), e);
+  }
+  h->g = g;
+  *exec = h;
   return AMDC_OK;
 }
 int amdc_graph_launch(void *exec, void *stream) {
   NEED_OPEN();
-  HIPCALL(H.GraphLaunch(exec, stream));
+  if (!exec) return fail(AMDC_EINVAL, "graph_launch: exec is NULL");
+  HIPCALL(H.GraphLaunch(((amdc_graph_t *)exec)->x, stream));
   return AMDC_OK;
 }
+/* Waits for the device first (a replay still queued keeps running on what it holds), then frees
+ * the executable graph and its template. */
 int amdc_graph_destroy(void *exec) {
   NEED_OPEN();
-  HIPCALL(H.GraphExecDestroy(exec));
+  if (!exec) return AMDC_OK;
+  amdc_graph_t *h = (amdc_graph_t *)exec;
+  HIPCALL(H.DeviceSynchronize());
+  const hipError_t e1 = H.GraphExecDestroy(h->x), e2 = H.GraphDestroy(h->g);
+  free(h);
+  if (e1 || e2) return fail(AMDC_EHIP, "graph_destroy: %s", H.GetErrorString(e1 ? e1 : e2));
   return AMDC_OK;
 }
 

@@ -105,8 +105,12 @@ int amdc_stream_sync(void *stream);
  * fork/join of independent operators, also inside a graph capture. */
 int amdc_stream_wait_event(void *stream, void *ev);
 int amdc_graph_begin(void *stream);
+/* *exec: an opaque handle (the executable graph and its template, both kept
+ * until amdc_graph_destroy). */
 int amdc_graph_end(void *stream, void **exec);
 int amdc_graph_launch(void *exec, void *stream);
+/* Waits for the device, then frees the graph (NULL: nothing). Not inside a
+ * capture. */
 int amdc_graph_destroy(void *exec);
 
 /* ---------------------------------------------------------------- operators */
