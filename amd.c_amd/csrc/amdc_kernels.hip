@@ -3035,7 +3035,6 @@ __device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, co
   };
   float lf[NQ][4][4]; // the leaves: [token group][pair p: super-group 2 p + qn / 2 (lanes of an even quarter qn)][row 4 h + v]
   const u32 nth = (T + 3u) >> 2; // token groups with tokens (group 0 always: T >= 1)
-  v4f d4[4];                        // d of this lane's output rows, super-group 2 p + qn / 2
   // the MFMAs of plane k = 2 m + e from slot s
   auto plane = [&](u32 m, u32 e, u32 npair, u32 s) {
     const u32 k = 2u * m + e;
@@ -3069,12 +3068,15 @@ __device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, co
       // lane 4 columns up (row_ror:12) and apply the decode GEMV's block step, src/cpu.c:142:
       // leaf = fma(fma(s1, d1, s0 d0), d_a, leaf), s = d sc (the lanes of odd quarters compute unused values)
       const u32 bl = 8u * (2u * p + (qn >> 1)) + k; // this lane's sub-block
+      // d of this lane's 4 rows, read per pair (kept in registers for the 4 pairs it costs the kernel the
+      // 256-VGPR limit of two waves per SIMD: 264 VGPRs)
+      const v4f dp = *(const v4f *)&sd[w][2u * p + (qn >> 1)][4u * h];
       const u32 sc0 = *(const u32 *)&ssc[w][bl][0][4u * h], sc1 = *(const u32 *)&ssc[w][bl][1][4u * h];
       v4f s0, s1;
 #pragma unroll
       for (u32 v = 0; v < 4u; v++) {
-        s0[v] = d4[p][v] * (float)(int)(int8_t)(sc0 >> (8u * v)); // d sc, exact (as the decode GEMV's dsc * sc)
-        s1[v] = d4[p][v] * (float)(int)(int8_t)(sc1 >> (8u * v));
+        s0[v] = dp[v] * (float)(int)(int8_t)(sc0 >> (8u * v)); // d sc, exact (as the decode GEMV's dsc * sc)
+        s1[v] = dp[v] * (float)(int)(int8_t)(sc1 >> (8u * v));
       }
 #pragma unroll
       for (u32 th = 0; th < (u32)NQ; th++) {
@@ -3105,10 +3107,6 @@ __device__ __forceinline__ void gemv8_q6k_body(const uint8_t *__restrict__ W, co
     v8_barrier(); // the previous tile's readers are done
     stage_tile();
     v8_barrier();
-#pragma unroll
-    for (u32 p = 0; p < 4u; p++) {
-      d4[p] = *(const v4f *)&sd[w][2u * p + (qn >> 1)][4u * h];
-    }
 #pragma unroll
     for (u32 th = 0; th < (u32)NQ; th++)
 #pragma unroll
