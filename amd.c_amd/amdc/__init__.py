@@ -126,15 +126,17 @@ ABI = {
     "amdc_chain_launch": (C.c_int, [_P, _P]),
     "amdc_chain_check": (C.c_int, [_P]),
     "amdc_chain_destroy": (C.c_int, [_P]),
+    "amdc_chain_record_begin": (C.c_int, [_P]),
+    "amdc_chain_record_end": (C.c_int, [_P, C.c_int, C.POINTER(_P)]),
 }
 
-CHAIN_QUANT, CHAIN_GEMV, CHAIN_GEMV_X = 0, 1, 2
+CHAIN_QUANT, CHAIN_GEMV, CHAIN_GEMV_X, CHAIN_RMSNORM_Q8, CHAIN_SWIGLU_Q8 = 0, 1, 2, 3, 4
 
 
 class ChainOp(C.Structure):
     """amdc_chain_op of include/amdc_q4.h."""
     _fields_ = [("type", C.c_int), ("kind", C.c_int), ("sync", C.c_int), ("rows", _U32), ("nb", _U32),
-                ("w", _P), ("x", _P), ("q", _P), ("xq", _P), ("y", _P), ("bias", _P), ("res", _P)]
+                ("w", _P), ("x", _P), ("q", _P), ("xq", _P), ("y", _P), ("bias", _P), ("res", _P), ("eps", C.c_float)]
 
 
 class AmdcError(RuntimeError):
@@ -453,6 +455,17 @@ def chain_gemv_x(kind, w, x, y, rows, nb, bias=None, res=None, sync=True):
     return ChainOp(CHAIN_GEMV_X, kind, int(sync), rows, nb, _p(w), _p(x), None, None, _p(y), _p(bias), _p(res))
 
 
+def chain_rmsnorm_q8(x, w, y, nb, eps, q=None, sync=True):
+    """An RMSNorm + Q8 operation of a chain (amdc_rmsnorm_q8 of one token): x, w -> y and, with q, its Q8 copy."""
+    return ChainOp(CHAIN_RMSNORM_Q8, 0, int(sync), 0, nb, _p(w), _p(x), _p(q), None, _p(y), None, None, eps)
+
+
+def chain_swiglu_q8(a, b, nb, q=None, sync=True):
+    """A SwiGLU + Q8 operation of a chain (amdc_swiglu_q8 of one token): a = silu(a) b in place and, with q,
+    its Q8 copy."""
+    return ChainOp(CHAIN_SWIGLU_Q8, 0, int(sync), 0, nb, None, _p(b), _p(q), None, _p(a), None, None, 0.0)
+
+
 CHAIN_AUTO, CHAIN_PERSISTENT, CHAIN_STREAMING = 0, 1, 2
 
 
@@ -480,10 +493,38 @@ class Chain:
     def trace_words(self):
         return lib().amdc_chain_trace_words(self.h)
 
+    @classmethod
+    def _adopt(cls, h):
+        c = cls.__new__(cls)
+        c.h = h
+        return c
+
     def __del__(self):
         if getattr(self, "h", None) and _lib is not None:
             lib().amdc_chain_destroy(self.h)
             self.h = None
+
+
+class ChainRecorder:
+    """amdc_chain_record_begin / _end as a context: the recordable operators called on `stream` inside the
+    block are appended to a chain instead of launched; `.chain` holds it after the block."""
+
+    def __init__(self, stream, form=CHAIN_AUTO):
+        self.stream, self.form, self.chain = stream, form, None
+
+    def __enter__(self):
+        _check(lib().amdc_chain_record_begin(self.stream.s))
+        return self
+
+    def __exit__(self, et, ev, tb):
+        h = _P()
+        rc = lib().amdc_chain_record_end(self.stream.s, self.form, C.byref(h))
+        if et is None:
+            _check(rc)
+            self.chain = Chain._adopt(h)
+        elif h.value:
+            lib().amdc_chain_destroy(h)
+        return False
 
 
 # ---------------------------------------------------------------- GGUF files (include/amdc_gguf.h)

@@ -304,6 +304,16 @@ static int g_occ[K_N]; /* resident workgroups per CU, looked up at a kernel's fi
 static int g_open, g_cus;
 static int t_lanes = -1, t_unroll = -1, t_wgs = -1, t_gemm = -1, t_gemm_min = -1, t_ksplit = -1;
 static u32 x_fuse_nb = 128; /* amdc_gemv_q4_x / _q4k_x: the largest nb quantized inside the GEMV */
+/* The chain recorder (amdc_chain_record_begin / _end): while it is on, the recordable operators
+ * called on its stream append chain operations instead of launching; every other launch on that
+ * stream is refused. */
+static struct {
+  int on;
+  void *stream;
+  amdc_chain_op *ops;
+  u32 n, cap, seg0;
+  int err; /* an operator refused while recording: record_end reports it */
+} g_rec;
 static int t_form = 0;      /* decode GEMV: 1 = amdc_gemv_*_p1, 2 = amdc_gemv_*_p2, 0 = by shape */
 /* The GEMM's device workspace (prepared activations, split-K partial sums): grown on demand;
  * the smaller ones it replaced stay allocated until amdc_close (see ws_reserve). */
@@ -433,6 +443,8 @@ int amdc_open(const char *hsaco) {
 static void stage_free(void);
 
 void amdc_close(void) {
+  free(g_rec.ops);
+  memset(&g_rec, 0, sizeof g_rec);
   if (g_open) stage_free();
   if (g_open && g_ws) H.Free(g_ws);
   for (unsigned i = 0; g_open && i < g_ws_old_n; i++) H.Free(g_ws_old[i]);
@@ -596,7 +608,19 @@ int amdc_graph_destroy(void *exec) {
 /* ---------------------------------------------------------------- launches */
 
 static int g_last_k = -1; /* the kernel of the last launch (amdc_last_kernel) */
+static int rec_on(void *stream) { return g_rec.on && stream == g_rec.stream; }
+static int rec_put(const amdc_chain_op *o);
+static int rec_gemv(int kind, const void *w, const uint8_t *xq, float *y, u32 rows, u32 nb, const float *bias, const float *res) {
+  const amdc_chain_op o = {.type = AMDC_CHAIN_GEMV, .kind = kind, .rows = rows, .nb = nb, .w = w, .xq = xq, .y = y, .bias = bias, .res = res};
+  return rec_put(&o);
+}
+static int rec_refuse(int k) {
+  g_rec.err = 1;
+  return fail(AMDC_EINVAL, "%s cannot be recorded into a chain (amdc_chain_record_begin is on for this stream)", k >= 0 ? kname[k] : "this operator");
+}
+
 static int launch_nt(int k, unsigned gx, unsigned gy, unsigned nt, unsigned lds, void *stream, void **args) {
+  if (rec_on(stream)) return rec_refuse(k);
   g_last_k = k;
   HIPCALL(H.ModuleLaunchKernel(g_k[k], gx, gy, 1, nt, 1, 1, lds, stream, args, NULL));
   return AMDC_OK;
@@ -613,6 +637,10 @@ int amdc_quant_q8(const float *x, uint8_t *q, uint32_t nb, uint32_t T, uint32_t 
   if (T > 1 && (xs % 4u || qs % 4u || xs < 128u * nb || qs < 40u * nb))
     return fail(AMDC_EINVAL, "quant_q8: strides xs %u, qs %u too small or unaligned for nb %u", xs, qs, nb);
   if (T > 65535u) return fail(AMDC_EINVAL, "quant_q8: T %u > 65535", T);
+  if (rec_on(stream) && T == 1u) {
+    const amdc_chain_op o = {.type = AMDC_CHAIN_QUANT, .nb = nb, .x = x, .q = q};
+    return rec_put(&o);
+  }
   void *args[] = {&x, &q, &nb, &xs, &qs};
   return launch(K_QUANT, (nb + 7u) / 8u, T, 0, stream, args);
 }
@@ -625,6 +653,10 @@ int amdc_rmsnorm_q8(const float *x, const float *w, float *y, uint32_t n, float 
   if (T > 1u && (xs % 4u || ys % 4u || xs < 4u * n || ys < 4u * n || (q && qs < 40u * (n / 32u))))
     return fail(AMDC_EINVAL, "rmsnorm_q8: strides xs %u, ys %u, qs %u too small or unaligned for n %u", xs, ys, qs, n);
   if (T > 65535u) return fail(AMDC_EINVAL, "rmsnorm_q8: T %u > 65535", T);
+  if (rec_on(stream) && T == 1u) {
+    const amdc_chain_op o = {.type = AMDC_CHAIN_RMSNORM_Q8, .nb = n / 32u, .w = w, .x = x, .q = q, .y = y, .eps = eps};
+    return rec_put(&o);
+  }
   void *args[] = {&x, &w, &y, &n, &eps, &q, &xs, &ys, &qs};
   return launch(K_RMSNORM_Q8, (n / 32u + 7u) / 8u, T, 0, stream, args);
 }
@@ -636,6 +668,10 @@ int amdc_swiglu_q8(float *a, const float *b, uint32_t n, uint8_t *q, uint32_t T,
   if (T > 1u && (as % 4u || as < 4u * n || (q && qs < 40u * (n / 32u))))
     return fail(AMDC_EINVAL, "swiglu_q8: strides as %u, qs %u too small or unaligned for n %u", as, qs, n);
   if (T > 65535u) return fail(AMDC_EINVAL, "swiglu_q8: T %u > 65535", T);
+  if (rec_on(stream) && T == 1u) {
+    const amdc_chain_op o = {.type = AMDC_CHAIN_SWIGLU_Q8, .nb = n / 32u, .x = b, .q = q, .y = a};
+    return rec_put(&o);
+  }
   void *args[] = {&a, &b, &n, &q, &as, &qs};
   return launch(K_SWIGLU_Q8, (n + 255u) / 256u, T, 0, stream, args);
 }
@@ -753,6 +789,7 @@ static int gemv8_launch(int kind, const void *w, const uint8_t *xq, float *y, ui
   g_last_k = k;
   /* Q4_0 / Q4_K: 8 waves, two per 16 rows, each with half of a tile's super-group pairs */
   const unsigned nth = kind == AMDC_KIND_Q4_0 || kind == AMDC_KIND_Q4_K ? 512u : 256u;
+  if (rec_on(stream)) return rec_refuse(k);
   HIPCALL(H.ModuleLaunchKernel(g_k[k], wgs, ks, 1, nth, 1, 1, 0, stream, args, NULL));
   if (ks > 1u && !cnt) {
     const u64 n = (u64)rows * T;
@@ -912,6 +949,7 @@ int amdc_gemv_q4(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint
                  void *stream) {
   NEED_OPEN();
   int rc = check_mat("gemv_q4", AMDC_KIND_Q4_0, w, xq, y, rows, nb);
+  if (!rc && rec_on(stream)) return rec_gemv(AMDC_KIND_Q4_0, w, xq, y, rows, nb, bias, res);
   return rc ? rc : gemv_launch(AMDC_KIND_Q4_0, w, xq, y, rows, nb, bias, res, 1, 0, 0, 0, stream);
 }
 
@@ -919,6 +957,7 @@ int amdc_gemv_q4k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uin
                   void *stream) {
   NEED_OPEN();
   int rc = check_mat("gemv_q4k", AMDC_KIND_Q4_K, w, xq, y, rows, nb);
+  if (!rc && rec_on(stream)) return rec_gemv(AMDC_KIND_Q4_K, w, xq, y, rows, nb, bias, res);
   return rc ? rc : gemv_launch(AMDC_KIND_Q4_K, w, xq, y, rows, nb, bias, res, 1, 0, 0, 0, stream);
 }
 
@@ -981,6 +1020,20 @@ static int gemv_x(int kind, const char *op, const void *w, const float *x, float
   int rc = check_mat(op, kind, w, (const uint8_t *)x, y, rows, nb);
   if (rc) return rc;
   if (q8 && !aligned16(q8)) return fail(AMDC_EINVAL, "%s: q8 must be 16-byte aligned", op);
+  if (rec_on(stream)) {
+    /* with q8: the quantization into q8 (which the caller may read) and the GEMV on it; without: one
+       operation that quantizes in every workgroup (Q4_0 / Q4_K) */
+    if (q8) {
+      const amdc_chain_op o = {.type = AMDC_CHAIN_QUANT, .nb = nb, .x = x, .q = q8};
+      return (rc = rec_put(&o)) ? rc : rec_gemv(kind, w, q8, y, rows, nb, bias, res);
+    }
+    if (kind != AMDC_KIND_Q4_0 && kind != AMDC_KIND_Q4_K) {
+      g_rec.err = 1;
+      return fail(AMDC_EINVAL, "%s: pass q8 to record a Q8_0 / Q6_K GEMV of an f32 vector", op);
+    }
+    const amdc_chain_op o = {.type = AMDC_CHAIN_GEMV_X, .kind = kind, .rows = rows, .nb = nb, .w = w, .x = x, .y = y, .bias = bias, .res = res};
+    return rec_put(&o);
+  }
   const u32 ng = amdc_ngroups(nb), L = gemv_lanes(ng), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
   if ((kind == AMDC_KIND_Q4_0 || kind == AMDC_KIND_Q4_K) && t_form == 4) { /* tuning: the K-split form */
     rc = gemvk_launch(kind, w, x, 1, y, rows, nb, bias, res, q8, t_lanes > 0 ? (u32)t_lanes : 8u, stream);
@@ -1042,6 +1095,7 @@ int amdc_gemv_q8(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint
                  void *stream) {
   NEED_OPEN();
   int rc = check_mat("gemv_q8", AMDC_KIND_Q8_0, w, xq, y, rows, nb);
+  if (!rc && rec_on(stream)) return rec_gemv(AMDC_KIND_Q8_0, w, xq, y, rows, nb, bias, res);
   return rc ? rc : gemv_launch(AMDC_KIND_Q8_0, w, xq, y, rows, nb, bias, res, 1, 0, 0, 0, stream);
 }
 
@@ -1049,6 +1103,7 @@ int amdc_gemv_q6k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uin
                   void *stream) {
   NEED_OPEN();
   int rc = check_mat("gemv_q6k", AMDC_KIND_Q6_K, w, xq, y, rows, nb);
+  if (!rc && rec_on(stream)) return rec_gemv(AMDC_KIND_Q6_K, w, xq, y, rows, nb, bias, res);
   return rc ? rc : gemv_launch(AMDC_KIND_Q6_K, w, xq, y, rows, nb, bias, res, 1, 0, 0, 0, stream);
 }
 
@@ -1173,6 +1228,7 @@ static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *x
   if (grid > 0x7FFFFFFFull) return fail(AMDC_EINVAL, "%s: grid too large", op);
   void *ga[] = {&w, &xh, &da, &xa, &y, &rows, &nb, &bias, &res, &T, (void *)&Tp, &ys, &rs, &part, &nfull, &ks};
   g_last_k = kk;
+  if (rec_on(stream)) return rec_refuse(kk);
   HIPCALL(H.ModuleLaunchKernel(g_k[kk], (unsigned)grid, 1, 1, gh[v].threads, 1, 1, 0, stream, ga, NULL));
   if (ks > 1u) { /* the tail rows: y, bias and res from row r0 */
     const u64 n = (u64)trows * T;
@@ -1222,6 +1278,7 @@ int amdc_op_gemv(int kind, const void *w, const uint8_t *xq, float *y, uint32_t 
   NEED_OPEN();
   if (T == 1u) {
     int rc = check_mat("op_gemv", kind, w, xq, y, rows, nb);
+    if (!rc && rec_on(stream)) return rec_gemv(kind, w, xq, y, rows, nb, bias, res);
     return rc ? rc : gemv_launch(kind, w, xq, y, rows, nb, bias, res, 1, 0, 0, 0, stream);
   }
   if (use_gemm(T, rows, nb)) return gemm_launch(kind, "op_gemv", w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
@@ -1301,19 +1358,40 @@ static span span_of(const void *p, u64 n) {
   return r;
 }
 static int spans_meet(span a, span b) { return a.lo < a.hi && b.lo < b.hi && a.lo < b.hi && b.lo < a.hi; }
-/* The bytes a (validated) chain operation writes (*w) and reads (r, returns how many ranges). */
-static unsigned chain_spans(const chain_dev_op *e, const amdc_chain_op *o, span *w, span r[4]) {
-  if (e->type == 0u) { /* quantize: 32 nb floats -> 40 nb Q8 bytes */
-    *w = span_of(o->q, 40ull * o->nb);
+/* The bytes a (validated) chain operation writes (w[0], w[1]: an empty range where unused) and reads (r,
+   returns how many ranges). */
+static unsigned chain_spans(const amdc_chain_op *o, span *w, span r[4]) {
+  if (o->type == AMDC_CHAIN_QUANT) { /* quantize: 32 nb floats -> 40 nb Q8 bytes */
+    w[0] = span_of(o->q, 40ull * o->nb), w[1] = span_of(NULL, 0);
     r[0] = span_of(o->x, 128ull * o->nb);
     return 1;
   }
-  *w = span_of(o->y, 4ull * o->rows);
+  if (o->type == AMDC_CHAIN_RMSNORM_Q8 || o->type == AMDC_CHAIN_SWIGLU_Q8) { /* RMSNorm (x, w -> y, q), SwiGLU (y, x -> y, q) */
+    w[0] = span_of(o->y, 128ull * o->nb);
+    w[1] = span_of(o->q, 40ull * o->nb);
+    r[0] = span_of(o->x, 128ull * o->nb);
+    r[1] = span_of(o->type == AMDC_CHAIN_RMSNORM_Q8 ? o->w : NULL, 128ull * o->nb);
+    return 2;
+  }
+  w[0] = span_of(o->y, 4ull * o->rows), w[1] = span_of(NULL, 0);
   r[0] = o->type == AMDC_CHAIN_GEMV_X ? span_of(o->x, 128ull * o->nb) : span_of(o->xq, 40ull * o->nb);
   r[1] = span_of(o->w, (u64)o->rows * amdc_row_bytes_k(o->kind, o->nb));
   r[2] = span_of(o->bias, 4ull * o->rows);
   r[3] = span_of(o->res, 4ull * o->rows);
   return 4;
+}
+
+/* Two operations that may not run concurrently: one writes bytes the other reads or writes. */
+static int chain_clash(const amdc_chain_op *a, const amdc_chain_op *b) {
+  span wa[2], wb[2], ra[4], rb[4];
+  const unsigned na = chain_spans(a, wa, ra), nb = chain_spans(b, wb, rb);
+  int clash = 0;
+  for (unsigned i = 0; i < 2u; i++) {
+    for (unsigned j = 0; j < 2u; j++) clash |= spans_meet(wa[i], wb[j]);
+    for (unsigned j = 0; j < na; j++) clash |= spans_meet(ra[j], wb[i]);
+    for (unsigned j = 0; j < nb; j++) clash |= spans_meet(rb[j], wa[i]);
+  }
+  return clash;
 }
 
 int amdc_chain_create(const amdc_chain_op *ops, uint32_t n, void **chain) { return amdc_chain_create_form(ops, n, AMDC_CHAIN_AUTO, chain); }
@@ -1351,18 +1429,23 @@ int amdc_chain_create_form(const amdc_chain_op *ops, uint32_t n, int form, void 
       }
       e->rows = o->rows, e->a = o->w, e->b = fq ? (void *)o->x : (void *)o->xq, e->y = o->y, e->bias = o->bias, e->res = o->res;
       if (!rc && need > lds) lds = need;
+    } else if (o->type == AMDC_CHAIN_RMSNORM_Q8 || o->type == AMDC_CHAIN_SWIGLU_Q8) {
+      const int rn = o->type == AMDC_CHAIN_RMSNORM_Q8;
+      if (!o->x || !o->y || !o->nb || (rn && !o->w))
+        rc = fail(AMDC_EINVAL, "chain op %u: %s needs x, y%s and nb", k, rn ? "rmsnorm" : "swiglu", rn ? ", w" : "");
+      else if ((u64)o->nb * 128u >= (1ull << 31)) rc = fail(AMDC_EINVAL, "chain op %u: nb %u too large", k, o->nb);
+      else if (rn && !(o->eps >= 0.0f)) rc = fail(AMDC_EINVAL, "chain op %u: eps must be >= 0", k);
+      else if (!rn && o->y == o->x) rc = fail(AMDC_EINVAL, "chain op %u: swiglu's x and y must differ", k);
+      float eps = rn ? o->eps : 0.0f;
+      e->type = rn ? 7u : 8u, e->a = o->x, e->b = o->q, e->y = o->y, e->bias = rn ? (const float *)o->w : NULL;
+      memcpy(&e->pad, &eps, 4);
     } else {
       rc = fail(AMDC_EINVAL, "chain op %u: type %d", k, o->type);
     }
     /* two operations of one segment (no sync between) run concurrently: neither may write bytes
        the other reads or writes */
     for (u32 j = seg0; j < k && !rc; j++) {
-      span wk, wj, rk[4], rj[4];
-      const unsigned nk = chain_spans(&d[k], &ops[k], &wk, rk), nj = chain_spans(&d[j], &ops[j], &wj, rj);
-      int clash = spans_meet(wk, wj);
-      for (unsigned i = 0; i < nk; i++) clash |= spans_meet(rk[i], wj);
-      for (unsigned i = 0; i < nj; i++) clash |= spans_meet(rj[i], wk);
-      if (clash) rc = fail(AMDC_EINVAL, "chain op %u and op %u share bytes one of them writes, without a sync between them", k, j);
+      if (chain_clash(&ops[k], &ops[j])) rc = fail(AMDC_EINVAL, "chain op %u and op %u share bytes one of them writes, without a sync between them", k, j);
     }
     if (o->sync) seg0 = k + 1u;
   }
@@ -1375,13 +1458,17 @@ int amdc_chain_create_form(const amdc_chain_op *ops, uint32_t n, int form, void 
   u32 kinds = 0, ngemv = 0;
   for (u32 k = 0; k < n; k++) {
     if (d[k].type == 0u) continue;
+    if (d[k].type >= 7u) { /* a producer operation: the persistent form only */
+      kinds |= 8u;
+      continue;
+    }
     ngemv++;
     kinds |= d[k].type == 1u || d[k].type == 3u ? 1u : d[k].type == 2u || d[k].type == 4u ? 2u : 4u;
   }
   const int can_stream = ngemv && (kinds == 1u || kinds == 2u);
   if (form == AMDC_CHAIN_STREAMING && !can_stream) {
     free(d);
-    return fail(AMDC_EINVAL, "chain_create: the streaming form needs at least one GEMV and every GEMV Q4_0, or every one Q4_K");
+    return fail(AMDC_EINVAL, "chain_create: the streaming form needs at least one GEMV, every GEMV Q4_0 or every one Q4_K, and no producer operation");
   }
   const int streaming = form == AMDC_CHAIN_STREAMING || (form == AMDC_CHAIN_AUTO && can_stream);
   const int kk = streaming ? K_CHAIN_S + (kinds == 2u ? 1 : 0) : K_CHAIN;
@@ -1483,6 +1570,51 @@ int amdc_chain_destroy(void *chain) {
   HIPCALL(H.Free(c->ops));
   free(c);
   return AMDC_OK;
+}
+
+/* The recorder: amdc_chain_record_begin(stream) turns it on; the recordable operators called on that
+ * stream then append to the list (rec_put) and launch nothing; amdc_chain_record_end builds the chain.
+ * A grid barrier goes after an operation exactly when the next one shares bytes that one of them
+ * writes with an operation since the last barrier (the rule amdc_chain_create checks), so independent
+ * operations run concurrently, as the reference's megakernel joins independent GEMVs. */
+static int rec_put(const amdc_chain_op *o) {
+  if (g_rec.n == g_rec.cap) {
+    const u32 cap = g_rec.cap ? 2u * g_rec.cap : 64u;
+    amdc_chain_op *p = (amdc_chain_op *)realloc(g_rec.ops, (size_t)cap * sizeof *p);
+    if (!p) {
+      g_rec.err = 1;
+      return fail(AMDC_EINVAL, "chain_record: out of host memory");
+    }
+    g_rec.ops = p, g_rec.cap = cap;
+  }
+  for (u32 j = g_rec.seg0; j < g_rec.n; j++)
+    if (chain_clash(o, &g_rec.ops[j])) {
+      g_rec.ops[g_rec.n - 1u].sync = 1;
+      g_rec.seg0 = g_rec.n;
+      break;
+    }
+  g_rec.ops[g_rec.n] = *o;
+  g_rec.ops[g_rec.n].sync = 0;
+  g_rec.n++;
+  return AMDC_OK;
+}
+
+int amdc_chain_record_begin(void *stream) {
+  NEED_OPEN();
+  if (g_rec.on) return fail(AMDC_EINVAL, "chain_record_begin: a recording is already on");
+  g_rec.on = 1, g_rec.stream = stream, g_rec.n = 0, g_rec.seg0 = 0, g_rec.err = 0;
+  return AMDC_OK;
+}
+
+int amdc_chain_record_end(void *stream, int form, void **chain) {
+  NEED_OPEN();
+  if (!g_rec.on || stream != g_rec.stream) return fail(AMDC_EINVAL, "chain_record_end: no recording on this stream");
+  g_rec.on = 0;
+  if (!chain) return fail(AMDC_EINVAL, "chain_record_end: chain is NULL");
+  *chain = NULL;
+  if (g_rec.err) return fail(AMDC_EINVAL, "chain_record_end: an operator was refused while recording; no chain");
+  if (!g_rec.n) return fail(AMDC_EINVAL, "chain_record_end: nothing was recorded");
+  return amdc_chain_create_form(g_rec.ops, g_rec.n, form, chain);
 }
 
 /* ---------------------------------------------------------------- the streaming matrix load */

@@ -24,8 +24,9 @@
 //                      integer block sums (ie_gemm_q4kr, ie_gemm_q8r, ie_gemm_q6kr)
 //   amdc_gemm_q4_k_n{64,128}
 //                      the same on int8 MFMA (a tuning alternative)
-//   amdc_chain         a list of quantize / decode-GEMV operations in one
-//                      persistent launch (the megakernel's GEMV chain)
+//   amdc_chain         a list of quantize / decode-GEMV / RMSNorm+Q8 / SwiGLU+Q8
+//                      operations in one persistent launch (the megakernel's
+//                      command list for these operations)
 //   amdc_dots_{q4_0,q4_k,q8_0,q6_k}
 //                      the per-block int32 dot products (parity check)
 //   amdc_probe_read, amdc_probe_copy
@@ -208,7 +209,11 @@ extern "C" __global__ __launch_bounds__(256) void amdc_quant_q8(const float *__r
 // and its Q8 copy (the arithmetic of amdc_quant_q8 on that result) in one
 // launch. Grid (ceil(n / 256), T); token t at byte offsets t xs, t ys, t qs.
 
-// half a wave quantizes the block of 32 values v (one per lane) into q
+#define CPOL_SC1 16 // cache policy of agent-coherent buffer accesses (gfx94x / gfx950 SC1)
+
+// half a wave quantizes the block of 32 values v (one per lane) into q; COH: agent-coherent stores
+// (the chain kernel's operations, read by other workgroups of the launch)
+template <bool COH = false>
 __device__ __forceinline__ void quant_half(float v, u32 b, uint8_t *__restrict__ q, u32 nb) {
   const u32 j = threadIdx.x & 31u;
   float a = __builtin_fabsf(v);
@@ -216,15 +221,69 @@ __device__ __forceinline__ void quant_half(float v, u32 b, uint8_t *__restrict__
   for (u32 o = 1; o < 32u; o <<= 1) a = __builtin_fmaxf(a, __shfl_xor(a, (int)o));
   const float d = a / 127.0f;
   const int qi = d != 0.0f ? (int)__builtin_roundf(v / d) : 0;
-  ((int8_t *)q)[32u * b + j] = (int8_t)qi;
   u32 s = (u32)qi;
 #pragma unroll
   for (u32 o = 1; o < 32u; o <<= 1) s += (u32)__shfl_xor((int)s, (int)o);
-  if (j == 0u) {
-    ((float *)(q + 32u * nb))[b] = d;
-    ((u32 *)(q + 36u * nb))[b] = s;
+  if constexpr (COH) {
+    const __amdgpu_buffer_rsrc_t rq = rsrc(q, 40u * nb);
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)qi, rq, 32u * b + j, 0, CPOL_SC1);
+    if (j == 0u) {
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(u32, d), rq, 32u * nb + 4u * b, 0, CPOL_SC1);
+      __builtin_amdgcn_raw_buffer_store_b32(s, rq, 36u * nb + 4u * b, 0, CPOL_SC1);
+    }
+  } else {
+    ((int8_t *)q)[32u * b + j] = (int8_t)qi;
+    if (j == 0u) {
+      ((float *)(q + 32u * nb))[b] = d;
+      ((u32 *)(q + 36u * nb))[b] = s;
+    }
   }
 }
+
+// a float of x[i]: a plain load, or (COH) an agent-coherent one through the resource r
+template <bool COH>
+__device__ __forceinline__ float ldf(const float *__restrict__ x, __amdgpu_buffer_rsrc_t r, u32 i) {
+  if constexpr (COH) return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, 4u * i, 0, CPOL_SC1));
+  else return x[i];
+}
+
+// The RMS scale s = 1 / sqrt(sum x^2 / n + eps) of n floats by the 256 threads of a workgroup: each
+// thread adds the squares of its elements tid, tid + 256, ... in that order (NL loads in flight, which
+// does not change the order), then the wave and workgroup reductions. The same code, so the same bits
+// of s, in amdc_rmsnorm_q8 (NL = 8) and in the chain's RMSNorm operation (NL = 2: the chain kernel keeps
+// the next GEMV's weight loads in registers meanwhile).
+template <bool COH, u32 NL>
+__device__ __forceinline__ float rms_scale(const float *__restrict__ x, u32 n, float eps, float *s_ss) {
+  const __amdgpu_buffer_rsrc_t rx = rsrc(x, 4u * n);
+  const u32 tid = threadIdx.x;
+  float ss = 0.0f;
+  u32 i0 = tid;
+  for (; i0 + (NL - 1u) * NT < n; i0 += NL * NT) {
+    float v[NL];
+#pragma unroll
+    for (u32 k = 0; k < NL; k++) v[k] = ldf<COH>(x, rx, i0 + k * NT);
+#pragma unroll
+    for (u32 k = 0; k < NL; k++) ss += v[k] * v[k];
+  }
+  for (; i0 < n; i0 += NT) {
+    const float v = ldf<COH>(x, rx, i0);
+    ss += v * v;
+  }
+  ss += dpp<0xB1>(ss);
+  ss += dpp<0x4E>(ss);
+  ss += dpp<0x141>(ss);
+  ss += dpp<0x140>(ss);
+  ss += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, ss), 0x401F));
+  ss += __shfl_xor(ss, 32);
+  if ((tid & 63u) == 0u) s_ss[tid >> 6] = ss;
+  __syncthreads();
+  ss = (s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]);
+  __syncthreads(); // s_ss is free again
+  return 1.0f / __builtin_sqrtf(ss / (float)n + eps);
+}
+
+// SwiGLU of one element, src/cpu.c:580
+__device__ __forceinline__ float swiglu1(float g, float b) { return g / (1.0f + __builtin_expf(-g)) * b; }
 
 // y = x s w, s = 1 / sqrt(sum x^2 / n + eps) (src/cpu.c:276-281), and its Q8
 // copy when q is not NULL. Every workgroup computes the whole sum of squares
@@ -237,26 +296,7 @@ extern "C" __global__ __launch_bounds__(256) void amdc_rmsnorm_q8(const float *_
   y = (float *)((uint8_t *)y + (u64)blockIdx.y * ys);
   if (q) q += (u64)blockIdx.y * qs;
   const u32 tid = threadIdx.x;
-  float ss = 0.0f;
-  u32 i0 = tid;
-  for (; i0 + 7u * NT < n; i0 += 8u * NT) {
-    float v[8];
-#pragma unroll
-    for (u32 k = 0; k < 8u; k++) v[k] = x[i0 + k * NT];
-#pragma unroll
-    for (u32 k = 0; k < 8u; k++) ss += v[k] * v[k];
-  }
-  for (; i0 < n; i0 += NT) ss += x[i0] * x[i0];
-  ss += dpp<0xB1>(ss);
-  ss += dpp<0x4E>(ss);
-  ss += dpp<0x141>(ss);
-  ss += dpp<0x140>(ss);
-  ss += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, ss), 0x401F));
-  ss += __shfl_xor(ss, 32);
-  if ((tid & 63u) == 0u) s_ss[tid >> 6] = ss;
-  __syncthreads();
-  ss = (s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]);
-  const float s = 1.0f / __builtin_sqrtf(ss / (float)n + eps);
+  const float s = rms_scale<false, 8u>(x, n, eps, s_ss);
   const u32 nb = n >> 5, b = blockIdx.x * 8u + (tid >> 5);
   if (b >= nb) return; // whole 32-lane halves leave together
   const u32 i = 32u * b + (tid & 31u);
@@ -274,8 +314,7 @@ extern "C" __global__ __launch_bounds__(256) void amdc_swiglu_q8(float *__restri
   if (q) q += (u64)blockIdx.y * qs;
   const u32 i = blockIdx.x * NT + threadIdx.x;
   if (i >= n) return; // whole 32-lane halves leave together
-  const float g = a[i];
-  const float v = g / (1.0f + __builtin_expf(-g)) * b[i];
+  const float v = swiglu1(a[i], b[i]);
   a[i] = v;
   if (q) quant_half(v, i >> 5, q, n >> 5);
 }
@@ -987,7 +1026,9 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_p2(const uint8_
 struct ChainOp { // the host's amdc_chain_op, resolved (amdc_host.c): 64 bytes
   u32 type;      // 0: quantize a -> b (nb blocks); 1, 2: GEMV Q4_0 / Q4_K, W a, Q8 vector b -> y;
                  // 3, 4: the same with the f32 vector b, quantized by every workgroup into its LDS;
-                 // 5, 6: GEMV Q8_0 / Q6_K, W a, Q8 vector b -> y
+                 // 5, 6: GEMV Q8_0 / Q6_K, W a, Q8 vector b -> y;
+                 // 7: RMSNorm of a (32 nb floats) with the weights bias -> y, its Q8 copy -> b (if not NULL),
+                 //    eps the float bits of pad; 8: SwiGLU y = silu(y) up a in place, its Q8 copy -> b (if not NULL)
   u32 sync;      // grid barrier after this operation
   u32 rows, nb, L, pad;
   const void *a;
@@ -995,8 +1036,6 @@ struct ChainOp { // the host's amdc_chain_op, resolved (amdc_host.c): 64 bytes
   float *y;
   const float *bias, *res;
 };
-#define CPOL_SC1 16 // cache policy of agent-coherent buffer accesses (gfx94x / gfx950 SC1)
-
 // The grid barrier. Arrivals are counted per group of workgroups
 // (blockIdx.x mod NGRP, one counter per 128-byte line: few atomics on any one
 // address); the last arrival of a group counts the group, the last group
@@ -1079,10 +1118,11 @@ __device__ __forceinline__ void chain_gemv(const ChainOp &op, Item (&it)[CHI], b
   if (FQ) { // the f32 vector (written by other workgroups: coherent loads), quantized as amdc_quant_q8
     const __amdgpu_buffer_rsrc_t rx = rsrc(xq, 128u * nb);
     const u32 e = tid & 7u;
-    FusedQ8T<4> fq; // 4 passes of 32 blocks in flight: the chain kernel keeps 2 workgroups per CU
-    for (u32 b0 = 0; b0 < nblk; b0 += 32u * 4u) {
+    FusedQ8T<2> fq; // 2 passes of 32 blocks in flight: the chain kernel keeps 2 workgroups per CU and
+                    // the next GEMV's first weights in registers
+    for (u32 b0 = 0; b0 < nblk; b0 += 32u * 2u) {
 #pragma unroll
-      for (u32 c = 0; c < 4u; c++) {
+      for (u32 c = 0; c < 2u; c++) {
         const u32 b = b0 + 32u * c + (tid >> 3);
         fq.xv[c] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rx, b < nb ? 128u * b + 16u * e : 0xFFFFFFF0u, 0, CPOL_SC1));
       }
@@ -1196,6 +1236,39 @@ __device__ __forceinline__ void chain_gemv_k8(const ChainOp &op, uint8_t *smem) 
   __syncthreads(); // the LDS vector is free for the next operation
 }
 
+// The Q8 producers as chain operations: amdc_rmsnorm_q8 / amdc_swiglu_q8 of one token (the same device
+// code: bit-equal), every workgroup taking blocks of 8 (RMSNorm: each first computes the whole scale,
+// as every workgroup of the separate launch does), inputs and outputs agent-coherent.
+__device__ __forceinline__ void chain_rmsnorm(const ChainOp &op) {
+  __shared__ float s_ss[4];
+  const u32 nb = op.nb, n = 32u * nb, tid = threadIdx.x;
+  const float *x = (const float *)op.a, *w = op.bias;
+  const float s = rms_scale<true, 2u>(x, n, __builtin_bit_cast(float, op.pad), s_ss);
+  const __amdgpu_buffer_rsrc_t rx = rsrc(x, 4u * n), rw = rsrc(w, 4u * n), ry = rsrc(op.y, 4u * n);
+  for (u32 b0 = 8u * blockIdx.x; b0 < nb; b0 += 8u * gridDim.x) {
+    const u32 b = b0 + (tid >> 5);
+    if (b < nb) { // whole 32-lane halves
+      const u32 i = 32u * b + (tid & 31u);
+      const float v = ldf<true>(x, rx, i) * s * ldf<true>(w, rw, i);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(u32, v), ry, 4u * i, 0, CPOL_SC1);
+      if (op.b) quant_half<true>(v, b, (uint8_t *)op.b, nb);
+    }
+  }
+}
+__device__ __forceinline__ void chain_swiglu(const ChainOp &op) {
+  const u32 nb = op.nb, n = 32u * nb;
+  const float *u = (const float *)op.a;
+  const __amdgpu_buffer_rsrc_t rg = rsrc(op.y, 4u * n), ru = rsrc(u, 4u * n);
+  for (u32 i0 = NT * blockIdx.x; i0 < n; i0 += NT * gridDim.x) {
+    const u32 i = i0 + threadIdx.x;
+    if (i < n) { // n is a multiple of 32: whole halves
+      const float v = swiglu1(ldf<true>(op.y, rg, i), ldf<true>(u, ru, i));
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(u32, v), rg, 4u * i, 0, CPOL_SC1);
+      if (op.b) quant_half<true>(v, i >> 5, (uint8_t *)op.b, nb);
+    }
+  }
+}
+
 __device__ __forceinline__ void chain_quant(const ChainOp &op) {
   const u32 nb = op.nb, tid = threadIdx.x, e = tid & 7u;
   const __amdgpu_buffer_rsrc_t rx = rsrc(op.a, 128u * nb), rq = rsrc(op.b, 40u * nb);
@@ -1248,11 +1321,14 @@ extern "C" __global__ __launch_bounds__(256, 2) void amdc_chain(const ChainOp *_
     else if (op.type == 3u) chain_gemv<AMDC_Q4_0, true>(op, it, pre == k, smem);
     else if (op.type == 4u) chain_gemv<AMDC_Q4_K, true>(op, it, pre == k, smem);
     else if (op.type == 5u) chain_gemv_k8<AMDC_Q8_0>(op, smem);
-    else chain_gemv_k8<AMDC_Q6_K>(op, smem);
+    else if (op.type == 6u) chain_gemv_k8<AMDC_Q6_K>(op, smem);
+    else if (op.type == 7u) chain_rmsnorm(op);
+    else chain_swiglu(op);
     if (op.sync && k + 1u < n) {
-      // the next GEMV's first weights go out before the wait (quantizations between do not touch it[])
+      // the next GEMV's first weights go out before the wait (quantizations and producers between do
+      // not touch it[])
       u32 j = k + 1u;
-      while (j < n && ops[j].type == 0u) j++;
+      while (j < n && (ops[j].type == 0u || ops[j].type >= 7u)) j++;
       if (j < n && pre != j && chain_preload(ops[j], it[0])) pre = j;
       nbar++;
       if (!chain_barrier(sync, nbar, spin_ns)) break;

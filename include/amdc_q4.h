@@ -275,7 +275,7 @@ int amdc_block_dots(int kind, const void *w, const uint8_t *xq, int32_t *out, ui
  * AMDC_GEMV_FORM. */
 int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kernel, int gemm_ksplit, int gemv_form);
 
-/* A GEMV chain: a list of quantize and decode-GEMV operations run by ONE
+/* A GEMV chain: a list of quantize, decode-GEMV and Q8-producer operations run by ONE
  * persistent launch, a grid barrier after every operation marked sync (the
  * reference's megakernel command list, kernels/ie_mk.c with mk_put in
  * src/hip.c:530, and its GEMV chain probe ie_mk_gemv_chain,
@@ -291,6 +291,13 @@ int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kern
  *   AMDC_CHAIN_GEMV_X: Q4_0 / Q4_K on x (32 nb floats): every workgroup
  *                     quantizes x into its LDS (as amdc_gemv_q4_x, no Q8
  *                     buffer, no barrier between quantization and GEMV)
+ *   AMDC_CHAIN_RMSNORM_Q8: y = RMSNorm of x (32 nb floats) with the weights
+ *                     w (32 nb floats) and eps, its Q8 copy -> q when q is
+ *                     not NULL (amdc_rmsnorm_q8 of one token, bit-equal)
+ *   AMDC_CHAIN_SWIGLU_Q8: y = silu(y) x in place (32 nb floats each), its
+ *                     Q8 copy -> q when q is not NULL (amdc_swiglu_q8 of one
+ *                     token with a = y, b = x, bit-equal)
+ * Lists with the producer operations run in the persistent form.
  * Operations between two syncs run concurrently: when one writes bytes that
  * another reads or writes, the later one must come after a sync (the check
  * compares the byte ranges of every operand). All workgroups must be resident at
@@ -298,7 +305,7 @@ int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kern
  * streaming form); nothing else
  * should run on the device meanwhile. A barrier that waits longer than 200 ms
  * aborts the launch (every workgroup leaves); amdc_chain_check reports it. */
-enum { AMDC_CHAIN_QUANT = 0, AMDC_CHAIN_GEMV = 1, AMDC_CHAIN_GEMV_X = 2 };
+enum { AMDC_CHAIN_QUANT = 0, AMDC_CHAIN_GEMV = 1, AMDC_CHAIN_GEMV_X = 2, AMDC_CHAIN_RMSNORM_Q8 = 3, AMDC_CHAIN_SWIGLU_Q8 = 4 };
 typedef struct {
   int type, kind, sync;
   uint32_t rows, nb;
@@ -308,6 +315,7 @@ typedef struct {
   const uint8_t *xq;
   float *y;
   const float *bias, *res;
+  float eps; /* AMDC_CHAIN_RMSNORM_Q8 */
 } amdc_chain_op;
 /* Validate the list, upload it and the barrier counters (allocates: call
  * before any graph capture); *chain receives the handle. */
@@ -342,6 +350,22 @@ int amdc_chain_launch(void *chain, void *stream);
  * barrier (the counters are then reset). */
 int amdc_chain_check(void *chain);
 int amdc_chain_destroy(void *chain);
+/* The recorder (the reference's mk_put / mk_flush, src/hip.c:475-567, which
+ * append the kernels of launch_op to the megakernel's command list instead of
+ * launching them): after amdc_chain_record_begin(stream), these calls on that
+ * stream launch nothing and append chain operations: amdc_quant_q8,
+ * amdc_rmsnorm_q8, amdc_swiglu_q8 (T = 1), amdc_gemv_q4 / _q4k / _q8 / _q6k,
+ * amdc_op_gemv with T = 1, and amdc_gemv_*_x (with q8: a quantize into q8
+ * and the GEMV on it; without, Q4_0 / Q4_K only: AMDC_CHAIN_GEMV_X). Any
+ * other launch on that stream fails (and so does the recording). A grid
+ * barrier goes between two operations exactly where the later one shares
+ * bytes that one of them writes with an operation since the last barrier.
+ * amdc_chain_record_end(stream, form, &chain) ends the recording and creates
+ * the chain (amdc_chain_create_form: allocates, not inside a graph capture);
+ * launching it computes what the calls would have, bit for bit. One recording
+ * at a time. */
+int amdc_chain_record_begin(void *stream);
+int amdc_chain_record_end(void *stream, int form, void **chain);
 
 /* Bandwidth yardsticks (no reference counterpart): stream nbytes (a multiple
  * of 16) through a plain read kernel (one u32 per workgroup may be written to

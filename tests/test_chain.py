@@ -1,7 +1,8 @@
-"""The GEMV chain (amdc_chain_*): a list of quantize and decode-GEMV operations in one persistent launch
-with grid barriers. Every result equals the separate launches (amdc_quant_q8, then amdc_gemv_q4 / _q4k with
-the same lane split, amdc_gemv_q8 / _q6k) bit for bit, across repeated launches and graph replays, and the
-GEMVs match the oracle to the GEMV tolerance."""
+"""The GEMV chain (amdc_chain_*): a list of quantize, decode-GEMV and Q8-producer operations in one
+persistent launch with grid barriers, and its recorder (amdc_chain_record_begin / _end, the reference's
+mk_put / mk_flush, src/hip.c:475-567). Every result equals the separate launches (amdc_quant_q8, then
+amdc_gemv_q4 / _q4k with the same lane split, amdc_gemv_q8 / _q6k, amdc_rmsnorm_q8, amdc_swiglu_q8) bit for
+bit, across repeated launches and graph replays, and the GEMVs match the oracle to the GEMV tolerance."""
 import numpy as np
 import pytest
 
@@ -366,3 +367,139 @@ def test_chain_trace(dev, orc):
     ch2 = dev.Chain(ops, form=dev.CHAIN_PERSISTENT)
     with pytest.raises(dev.AmdcError, match="timeline"):
         ch2.trace(TB)
+
+
+def _layer(dev, orc, seed):
+    """The buffers of a decode layer's tail: x -> RMSNorm+Q8 -> gate, up (Q4_K) -> SwiGLU+Q8 -> down (Q6_K,
+    residual x) -> y -> RMSNorm+Q8 -> a Q8_0 GEMV -> z."""
+    nbD, nbH = 16, 48
+    D, H = 32 * nbD, 32 * nbH
+    g = np.random.default_rng(seed)
+    L = {"nbD": nbD, "nbH": nbH, "D": D, "H": H}
+    L["Wg"] = Case(dev, orc, 3, H, nbD, seed=seed + 1).W
+    L["Wu"] = Case(dev, orc, 3, H, nbD, seed=seed + 2).W
+    L["Wd"] = Case(dev, orc, 4, D, nbH, seed=seed + 3).W
+    L["Wo"] = Case(dev, orc, 2, 96, nbD, seed=seed + 4).W
+    L["x"] = dev.DevBuf.of(g.standard_normal(D).astype(np.float32))
+    L["wn"] = dev.DevBuf.of((1.0 + 0.1 * g.standard_normal(D)).astype(np.float32))
+    return L
+
+
+def _outs(dev, L):
+    nbD, nbH, D, H = L["nbD"], L["nbH"], L["D"], L["H"]
+    o = {"xn": dev.DevBuf(4 * D), "q1": dev.DevBuf(q8_stride(nbD)), "gt": dev.DevBuf(4 * H), "up": dev.DevBuf(4 * H),
+         "q2": dev.DevBuf(q8_stride(nbH)), "y": dev.DevBuf(4 * D), "yn": dev.DevBuf(4 * D), "q3": dev.DevBuf(q8_stride(nbD)),
+         "z": dev.DevBuf(4 * 96)}
+    for b in o.values():
+        b.fill(0)
+    return o
+
+
+def _run_layer(dev, L, o, stream=None):
+    """The layer as operator calls (launched, or recorded when a recording is on for `stream`)."""
+    S = stream.s if stream is not None else None
+    nbD, nbH, D, H = L["nbD"], L["nbH"], L["D"], L["H"]
+    dev.rmsnorm_q8(L["x"], L["wn"], o["xn"], D, 1e-5, q=o["q1"], stream=S)
+    dev.gemv(3, L["Wg"], o["q1"], o["gt"], H, nbD, stream=S)
+    dev.gemv(3, L["Wu"], o["q1"], o["up"], H, nbD, stream=S)
+    dev.swiglu_q8(o["gt"], o["up"], H, q=o["q2"], stream=S)
+    dev.gemv(4, L["Wd"], o["q2"], o["y"], D, nbH, res=L["x"], stream=S)
+    dev.rmsnorm_q8(o["y"], L["wn"], o["yn"], D, 1e-5, q=o["q3"], stream=S)
+    dev.gemv(2, L["Wo"], o["q3"], o["z"], 96, nbD, stream=S)
+
+
+def _same(dev, L, a, b):
+    for k in a:
+        n = {"q1": 40 * L["nbD"], "q3": 40 * L["nbD"], "q2": 40 * L["nbH"]}.get(k)
+        x, y = a[k].download(np.uint8), b[k].download(np.uint8)
+        if n:
+            x, y = x[:n], y[:n]
+        assert np.array_equal(x, y), k
+
+
+def test_chain_producers_equal_separate_launches(dev, orc):
+    """AMDC_CHAIN_RMSNORM_Q8 and AMDC_CHAIN_SWIGLU_Q8 in a persistent chain with GEMVs of three kinds: every
+    float and Q8 output equals the separate launches (amdc_rmsnorm_q8, amdc_swiglu_q8, the GEMVs) bit for
+    bit, over repeated launches; gate and up run in one segment (no barrier between them)."""
+    L = _layer(dev, orc, 40)
+    want = _outs(dev, L)
+    _run_layer(dev, L, want)
+    dev.sync()
+    o = _outs(dev, L)
+    nbD, nbH, D, H = L["nbD"], L["nbH"], L["D"], L["H"]
+    ops = [dev.chain_rmsnorm_q8(L["x"], L["wn"], o["xn"], nbD, 1e-5, q=o["q1"]),
+           dev.chain_gemv(3, L["Wg"], o["q1"], o["gt"], H, nbD, sync=False),
+           dev.chain_gemv(3, L["Wu"], o["q1"], o["up"], H, nbD),
+           dev.chain_swiglu_q8(o["gt"], o["up"], nbH, q=o["q2"]),
+           dev.chain_gemv(4, L["Wd"], o["q2"], o["y"], D, nbH, res=L["x"]),
+           dev.chain_rmsnorm_q8(o["y"], L["wn"], o["yn"], nbD, 1e-5, q=o["q3"]),
+           dev.chain_gemv(2, L["Wo"], o["q3"], o["z"], 96, nbD)]
+    ch = dev.Chain(ops)
+    for rep in range(3):
+        for b in o.values():
+            b.fill(0)
+        ch.launch()
+        ch.check()
+        _same(dev, L, o, want)
+    # the streaming form takes no producer operation
+    with pytest.raises(dev.AmdcError, match="streaming form"):
+        dev.Chain(ops, form=dev.CHAIN_STREAMING)
+    # a producer that reads what the operation before it writes, without a barrier, is refused
+    bad = list(ops)
+    bad[2] = dev.chain_gemv(3, L["Wu"], o["q1"], o["up"], H, nbD, sync=False)
+    with pytest.raises(dev.AmdcError, match="without a sync"):
+        dev.Chain(bad)
+
+
+def test_chain_recorder(dev, orc):
+    """amdc_chain_record_begin / _end: the same operator calls on a recording stream build a chain (barriers
+    placed from the operands' byte ranges) whose launch equals the calls launched, bit for bit, also as a
+    replayed HIP graph; a call that cannot be recorded fails, and so does the recording."""
+    L = _layer(dev, orc, 50)
+    want = _outs(dev, L)
+    _run_layer(dev, L, want)
+    dev.sync()
+    o = _outs(dev, L)
+    S = dev.Stream()
+    with dev.ChainRecorder(S) as rec:
+        _run_layer(dev, L, o, stream=S)
+    dev.sync()
+    for b in o.values():  # nothing ran while recording
+        assert not b.download(np.uint8).any()
+    rec.chain.launch(S.s)
+    S.sync()
+    rec.chain.check()
+    _same(dev, L, o, want)
+    gph = dev.Graph(S, lambda s: rec.chain.launch(s))
+    for rep in range(3):
+        for b in o.values():
+            b.fill(0)
+        dev.sync()
+        gph.launch()
+        S.sync()
+        _same(dev, L, o, want)
+    rec.chain.check()
+    # an f32-input GEMV records as one operation (Q4_0 / Q4_K) or, with q8, as quantize + GEMV
+    A = Case(dev, orc, 3, 300, 32, seed=61)
+    x = dev.DevBuf.of(A.x[0])
+    y0, y1, y2, q8 = dev.DevBuf(4 * 300), dev.DevBuf(4 * 300), dev.DevBuf(4 * 300), dev.DevBuf(q8_stride(32))
+    dev.gemv_x(3, A.W, x, y0, 300, 32)
+    with dev.ChainRecorder(S) as rec2:
+        dev.gemv_x(3, A.W, x, y1, 300, 32, stream=S.s)
+        dev.gemv_x(3, A.W, x, y2, 300, 32, q8=q8, stream=S.s)
+    rec2.chain.launch(S.s)
+    S.sync()
+    w0 = y0.download(np.uint32)
+    assert np.array_equal(y1.download(np.uint32), w0) and np.array_equal(y2.download(np.uint32), w0)
+    assert rel_err(y0.download(np.float32), A.y_oracle(0), A.mag(0)) < TOL
+    # refused: a verify GEMV (T = 2) on the recording stream; the recording then yields no chain
+    B = Case(dev, orc, 3, 64, 8, T=2, seed=62)
+    B.quant()
+    with pytest.raises(dev.AmdcError, match="refused|cannot be recorded"):
+        with dev.ChainRecorder(S):
+            dev.gemv_t(3, B.W, B.Q, B.Y, 64, 8, 2, B.xs, 64, stream=S.s)
+    # other streams launch as usual during a recording
+    with dev.ChainRecorder(S) as rec3:
+        dev.gemv(3, B.W, B.Q, B.Y, 64, 8)
+        dev.gemv(3, B.W, B.Q, B.Y, 64, 8, stream=S.s)
+    del rec3
