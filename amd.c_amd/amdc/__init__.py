@@ -126,6 +126,7 @@ ABI = {
     "amdc_chain_launch": (C.c_int, [_P, _P]),
     "amdc_chain_check": (C.c_int, [_P]),
     "amdc_chain_destroy": (C.c_int, [_P]),
+    "amdc_gemv_norm": (C.c_int, [C.c_int, _P, _P, _P, _U32, _U32, _P, _P, _P, _P, _P, C.c_float, _P]),
     "amdc_chain_record_begin": (C.c_int, [_P]),
     "amdc_chain_record_end": (C.c_int, [_P, C.c_int, C.POINTER(_P)]),
 }
@@ -433,6 +434,11 @@ def probe_copy(dst, src, nbytes, grid, stream=None):
 def rmsnorm_q8(x, w, y, n, eps, q=None, T=1, xs=0, ys=0, qs=0, stream=None):
     """amdc_rmsnorm_q8: y = rmsnorm(x) w and, when q is given, its Q8 copy."""
     _check(lib().amdc_rmsnorm_q8(_p(x), _p(w), _p(y), n, eps, _p(q), T, xs, ys, qs, stream))
+
+
+def gemv_norm(kind, w, xq, y, rows, nb, nw, ny, eps, nq=None, bias=None, res=None, stream=None):
+    """amdc_gemv_norm: the decode GEMV y and, from its last workgroup, ny = rmsnorm(y) nw and its Q8 copy nq."""
+    _check(lib().amdc_gemv_norm(kind, _p(w), _p(xq), _p(y), rows, nb, _p(bias), _p(res), _p(nw), _p(ny), _p(nq), eps, stream))
 
 
 def swiglu_q8(a, b, n, q=None, T=1, as_=0, qs=0, stream=None):

@@ -277,7 +277,9 @@ enum {
   K_CHAIN_S = K_GEMVM_Q4 + 2, /* amdc_chain_s_q4_0, amdc_chain_s_q4_k */
   K_GEMVXW_Q4 = K_CHAIN_S + 2, /* amdc_gemv_q4_0_xw1, amdc_gemv_q4_k_xw1, _xw2 */
   K_GEMVK_Q4 = K_GEMVXW_Q4 + 3, /* amdc_gemv_q4_0_k, _xk, amdc_gemv_q4_k_k, _xk */
-  K_N = K_GEMVK_Q4 + 4
+  K_GEMVSN_Q4 = K_GEMVK_Q4 + 4, /* amdc_gemv_q4_0_n1 .. _n4, amdc_gemv_q4_k_n1 .. _n4 (fused RMSNorm tail) */
+  K_GEMV2N = K_GEMVSN_Q4 + 8,   /* amdc_gemv_q8_0_pn, _q6_k_pn */
+  K_N = K_GEMV2N + 2
 };
 static const char *const kname[K_N] = {
     "amdc_quant_q8",           "amdc_dots_q4_0",          "amdc_dots_q4_k",          "amdc_gemm_q4_k_n128",
@@ -296,13 +298,17 @@ static const char *const kname[K_N] = {
     "amdc_gemv_q4_k_xs1",      "amdc_gemv_q4_k_xs2",      "amdc_gemv_q4_k_xs3",      "amdc_gemv_q4_k_xs4",
     "amdc_gemv_q4_0_m1",       "amdc_gemv_q4_k_m1",       "amdc_chain_s_q4_0",       "amdc_chain_s_q4_k",
     "amdc_gemv_q4_0_xw1",      "amdc_gemv_q4_k_xw1",      "amdc_gemv_q4_k_xw2",      "amdc_gemv_q4_0_k",
-    "amdc_gemv_q4_0_xk",       "amdc_gemv_q4_k_k",        "amdc_gemv_q4_k_xk"};
+    "amdc_gemv_q4_0_xk",       "amdc_gemv_q4_k_k",        "amdc_gemv_q4_k_xk",
+    "amdc_gemv_q4_0_n1",       "amdc_gemv_q4_0_n2",       "amdc_gemv_q4_0_n3",       "amdc_gemv_q4_0_n4",
+    "amdc_gemv_q4_k_n1",       "amdc_gemv_q4_k_n2",       "amdc_gemv_q4_k_n3",       "amdc_gemv_q4_k_n4",
+    "amdc_gemv_q8_0_pn",       "amdc_gemv_q6_k_pn"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
 static int g_occ[K_N]; /* resident workgroups per CU, looked up at a kernel's first use (0: not yet) */
 static int g_open, g_cus;
 static int t_lanes = -1, t_unroll = -1, t_wgs = -1, t_gemm = -1, t_gemm_min = -1, t_ksplit = -1;
+static u32 *g_norm_cnt; /* the fused-norm GEMVs' arrival counter (device, 0 between launches) */
 static u32 x_fuse_nb = 128; /* amdc_gemv_q4_x / _q4k_x: the largest nb quantized inside the GEMV */
 /* The chain recorder (amdc_chain_record_begin / _end): while it is on, the recordable operators
  * called on its stream append chain operations instead of launching; every other launch on that
@@ -424,6 +430,9 @@ int amdc_open(const char *hsaco) {
     if (!g_split_cnt || cb < AMDC_SPLIT_TILES * sizeof(u32))
       return fail(AMDC_EHIP, "amdc_kernels.hsaco: split_count array of %zu bytes, expected %zu", cb, AMDC_SPLIT_TILES * sizeof(u32));
     HIPCALL(H.Memset(g_split_cnt, 0, AMDC_SPLIT_TILES * sizeof(u32))); /* each launch leaves them at 0 again */
+    HIPCALL(H.ModuleGetGlobal((void **)&g_norm_cnt, &cb, g_mod, "norm_count"));
+    if (!g_norm_cnt || cb < sizeof(u32)) return fail(AMDC_EHIP, "amdc_kernels.hsaco: no norm_count counter");
+    HIPCALL(H.Memset(g_norm_cnt, 0, cb));
   }
   HIPCALL(H.DeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, 0));
   if (t_lanes < 0) t_lanes = envi("AMDC_GEMV_L", 0);
@@ -1105,6 +1114,37 @@ int amdc_gemv_q6k(const void *w, const uint8_t *xq, float *y, uint32_t rows, uin
   int rc = check_mat("gemv_q6k", AMDC_KIND_Q6_K, w, xq, y, rows, nb);
   if (!rc && rec_on(stream)) return rec_gemv(AMDC_KIND_Q6_K, w, xq, y, rows, nb, bias, res);
   return rc ? rc : gemv_launch(AMDC_KIND_Q6_K, w, xq, y, rows, nb, bias, res, 1, 0, 0, 0, stream);
+}
+
+/* The decode GEMV with the fused RMSNorm tail: the single-shot kernels (Q4_0 / Q4_K) or the second
+ * form (Q8_0, Q6_K), with the lane split of amdc_gemv_* (the same y), whose last workgroup writes ny
+ * and nq as amdc_rmsnorm_q8 of y. */
+int amdc_gemv_norm(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                   const float *nw, float *ny, uint8_t *nq, float eps, void *stream) {
+  NEED_OPEN();
+  int rc = check_mat("gemv_norm", kind, w, xq, y, rows, nb);
+  if (rc) return rc;
+  if (!nw || !ny) return fail(AMDC_EINVAL, "gemv_norm: nw and ny are required");
+  if (rows % 32u || rows > 8192u) return fail(AMDC_EINVAL, "gemv_norm: rows %u (a multiple of 32, the norm's Q8 blocks, at most 8192)", rows);
+  if (!(eps >= 0.0f)) return fail(AMDC_EINVAL, "gemv_norm: eps must be >= 0");
+  const u32 ng = amdc_ngroups(nb);
+  if (kind == AMDC_KIND_Q4_0 || kind == AMDC_KIND_Q4_K) { /* check_mat: nb <= 2048, so ng <= 256 */
+    const u32 L = gemvs_lanes(ng, rows, 0), ni = (ng + L - 1u) / L, rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
+    if (ni > 4u) return fail(AMDC_EINVAL, "gemv_norm: %u super-groups on %u lanes (at most 4 per lane)", ng, L);
+    void *a[] = {&w, &xq, &y, &rows, &nb, &bias, &res, (void *)&L, &nw, &ny, &nq, &eps, &g_norm_cnt};
+    return launch(K_GEMVSN_Q4 + (kind == AMDC_KIND_Q4_K ? 4 : 0) + (int)ni - 1, nrg, 1, 320u * ng, stream, a);
+  }
+  const u64 rb = amdc_row_bytes_k(kind, nb);
+  if ((u64)rows * rb + rb >= (1ull << 32))
+    return fail(AMDC_EINVAL, "gemv_norm: %u rows of %llu bytes: the matrix must be under 4 GiB", rows, (unsigned long long)rb);
+  /* the lane split of the T = 1 launch of gemv_k8_launch */
+  const u32 L = gemv2_lanes(ng, rows, 1), rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
+  const u32 cap = 2u * (g_cus > 0 ? (u32)g_cus : 256u), g = nrg < cap ? nrg : cap;
+  const u32 lds = (kind == AMDC_KIND_Q6_K ? 352u : 320u) * ng + 4u * rpg * ((nrg + g - 1u) / g);
+  if (lds > GEMV_LDS_T1) return fail(AMDC_EINVAL, "gemv_norm: nb %u too large for the staged vector (%u bytes of LDS)", nb, lds);
+  const int k = K_GEMV2N + (kind == AMDC_KIND_Q6_K ? 1 : 0);
+  void *a[] = {&w, &xq, &y, &rows, &nb, &bias, &res, (void *)&L, &nw, &ny, &nq, &eps, &g_norm_cnt};
+  return launch(k, g, 1, lds, stream, a);
 }
 
 int amdc_gemv_q8_t(const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,

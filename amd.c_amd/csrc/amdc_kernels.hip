@@ -240,6 +240,57 @@ __device__ __forceinline__ void quant_half(float v, u32 b, uint8_t *__restrict__
   }
 }
 
+// quant_half of N blocks at once (block b[k] of the 32 values v[k], one per lane; skipped where
+// on[k] is false, uniform over the half-wave): the same values per block, the N independent
+// reductions interleaved instead of one after the other
+template <u32 N>
+__device__ __forceinline__ void quant_halves(const float (&v)[N], const u32 (&b)[N], const bool (&on)[N], uint8_t *__restrict__ q, u32 nb) {
+  const u32 j = threadIdx.x & 31u;
+  float a[N];
+#pragma unroll
+  for (u32 k = 0; k < N; k++) a[k] = __builtin_fabsf(v[k]);
+  // max and the integer sum are exact in any order: DPP inside rows of 16 and a swizzle across the
+  // two rows of the half (as seg_sum) give the values quant_half's xor shuffles give
+#pragma unroll
+  for (u32 k = 0; k < N; k++) a[k] = __builtin_fmaxf(a[k], dpp<0xB1>(a[k]));
+#pragma unroll
+  for (u32 k = 0; k < N; k++) a[k] = __builtin_fmaxf(a[k], dpp<0x4E>(a[k]));
+#pragma unroll
+  for (u32 k = 0; k < N; k++) a[k] = __builtin_fmaxf(a[k], dpp<0x141>(a[k]));
+#pragma unroll
+  for (u32 k = 0; k < N; k++) a[k] = __builtin_fmaxf(a[k], dpp<0x140>(a[k]));
+#pragma unroll
+  for (u32 k = 0; k < N; k++) a[k] = __builtin_fmaxf(a[k], __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, a[k]), 0x401F)));
+  int qi[N];
+  u32 sm[N];
+  float d[N];
+#pragma unroll
+  for (u32 k = 0; k < N; k++) {
+    d[k] = a[k] / 127.0f;
+    qi[k] = d[k] != 0.0f ? (int)__builtin_roundf(v[k] / d[k]) : 0;
+    sm[k] = (u32)qi[k];
+  }
+#pragma unroll
+  for (u32 k = 0; k < N; k++) sm[k] += (u32)__builtin_amdgcn_update_dpp(0, (int)sm[k], 0xB1, 0xF, 0xF, false);
+#pragma unroll
+  for (u32 k = 0; k < N; k++) sm[k] += (u32)__builtin_amdgcn_update_dpp(0, (int)sm[k], 0x4E, 0xF, 0xF, false);
+#pragma unroll
+  for (u32 k = 0; k < N; k++) sm[k] += (u32)__builtin_amdgcn_update_dpp(0, (int)sm[k], 0x141, 0xF, 0xF, false);
+#pragma unroll
+  for (u32 k = 0; k < N; k++) sm[k] += (u32)__builtin_amdgcn_update_dpp(0, (int)sm[k], 0x140, 0xF, 0xF, false);
+#pragma unroll
+  for (u32 k = 0; k < N; k++) sm[k] += (u32)__builtin_amdgcn_ds_swizzle((int)sm[k], 0x401F);
+#pragma unroll
+  for (u32 k = 0; k < N; k++) {
+    if (!on[k]) continue;
+    ((int8_t *)q)[32u * b[k] + j] = (int8_t)qi[k];
+    if (j == 0u) {
+      ((float *)(q + 32u * nb))[b[k]] = d[k];
+      ((u32 *)(q + 36u * nb))[b[k]] = sm[k];
+    }
+  }
+}
+
 // a float of x[i]: a plain load, or (COH) an agent-coherent one through the resource r
 template <bool COH>
 __device__ __forceinline__ float ldf(const float *__restrict__ x, __amdgpu_buffer_rsrc_t r, u32 i) {
@@ -252,6 +303,7 @@ __device__ __forceinline__ float ldf(const float *__restrict__ x, __amdgpu_buffe
 // does not change the order), then the wave and workgroup reductions. The same code, so the same bits
 // of s, in amdc_rmsnorm_q8 (NL = 8) and in the chain's RMSNorm operation (NL = 2: the chain kernel keeps
 // the next GEMV's weight loads in registers meanwhile).
+__device__ __forceinline__ float rms_reduce(float ss, u32 n, float eps, float *s_ss);
 template <bool COH, u32 NL>
 __device__ __forceinline__ float rms_scale(const float *__restrict__ x, u32 n, float eps, float *s_ss) {
   const __amdgpu_buffer_rsrc_t rx = rsrc(x, 4u * n);
@@ -269,6 +321,12 @@ __device__ __forceinline__ float rms_scale(const float *__restrict__ x, u32 n, f
     const float v = ldf<COH>(x, rx, i0);
     ss += v * v;
   }
+  return rms_reduce(ss, n, eps, s_ss);
+}
+
+// s from each thread's sum of squares: the wave and workgroup reductions of rms_scale
+__device__ __forceinline__ float rms_reduce(float ss, u32 n, float eps, float *s_ss) {
+  const u32 tid = threadIdx.x;
   ss += dpp<0xB1>(ss);
   ss += dpp<0x4E>(ss);
   ss += dpp<0x141>(ss);
@@ -580,10 +638,74 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_k_x1(const uint8_
 // summation order are those of gemv1_body (bit-equal results).
 // QCN > 0 (the xw kernels): QCN passes of quantization loads in flight, and
 // the workgroup's size taken at run time (blockDim.x <= NTH threads).
-template <int KIND, u32 NI, bool FQ, u32 NTH, u32 QCN = 0u>
+// The fused RMSNorm of a decode GEMV's result (the reference's gemv_norm_tail, kernels/ie_kernels.c:
+// 267-283, IE_NORM_FUSE): the GEMV's workgroups store y agent-coherently; after its stores each
+// workgroup counts itself on cnt; the last of the gridDim.x computes ny = rmsnorm(y) nw (rows <= 8192 floats)
+// and, when nq is not NULL, its Q8 copy, with the device code of amdc_rmsnorm_q8 (256 threads: the
+// same bits), and sets cnt back to 0. Every thread of every workgroup calls it.
+struct NormTail {
+  const float *nw;
+  float *ny;
+  uint8_t *nq;
+  float eps;
+  u32 *cnt;
+};
+__device__ __forceinline__ void put_y(float *y, float v, bool coh) {
+  if (coh) __hip_atomic_store(y, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *y = v;
+}
+__device__ __forceinline__ void norm_tail(const float *__restrict__ y, u32 rows, const NormTail &nt) {
+  __shared__ u32 s_last;
+  __shared__ float s_ss[4];
+  __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this thread's stores of y are complete
+  __syncthreads();
+  if (threadIdx.x == 0u) {
+    const bool last = __hip_atomic_fetch_add(nt.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u == gridDim.x;
+    if (last) __hip_atomic_store(nt.cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // every element of y once, coherently, all in flight: thread tid holds y[tid + 256 k] (k < rows / 256,
+  // rows <= 8192), which is both rms_scale's order for the sum of squares and the element (block 8 k +
+  // tid / 32, lane tid % 32) it normalizes
+  const u32 nb = rows >> 5, tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t ry = rsrc(y, 4u * rows);
+  const __amdgpu_buffer_rsrc_t rw = rsrc(nt.nw, 4u * rows);
+  float yv[32], wv[32]; // with the norm weights, all loads in flight together
+#pragma unroll
+  for (u32 k = 0; k < 32u; k++) {
+    const u32 i = tid + NT * k < rows ? 4u * (tid + NT * k) : 0xFFFFFFF0u;
+    yv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ry, i, 0, CPOL_SC1));
+    wv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rw, i, 0, 0));
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (u32 k = 0; k < 32u; k++)
+    if (tid + NT * k < rows) ss += yv[k] * yv[k];
+  const float s = rms_reduce(ss, rows, nt.eps, s_ss);
+  // 8 blocks per half-wave at a time, their quantizations interleaved
+#pragma unroll
+  for (u32 k0 = 0; k0 < 32u; k0 += 8u) {
+    if (8u * k0 >= nb) break; // no half-wave has blocks from here on (uniform)
+    float v[8];
+    u32 b[8];
+    bool on[8];
+#pragma unroll
+    for (u32 k = 0; k < 8u; k++) {
+      b[k] = (tid >> 5) + 8u * (k0 + k), on[k] = b[k] < nb; // whole 32-lane halves
+      v[k] = yv[k0 + k] * s * wv[k0 + k];
+      if (on[k]) nt.ny[tid + NT * (k0 + k)] = v[k];
+    }
+    if (nt.nq) quant_halves<8>(v, b, on, nt.nq, nb);
+  }
+}
+
+template <int KIND, u32 NI, bool FQ, u32 NTH, u32 QCN = 0u, bool TAIL = false>
 __device__ __forceinline__ void gemvs_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
                                            u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 L,
-                                           const float *__restrict__ xf = nullptr, uint8_t *__restrict__ q8out = nullptr) {
+                                           const float *__restrict__ xf = nullptr, uint8_t *__restrict__ q8out = nullptr,
+                                           const NormTail &ntl = NormTail{}) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const u32 nth = QCN ? blockDim.x : NTH;
   const u32 ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
@@ -697,8 +819,9 @@ __device__ __forceinline__ void gemvs_body(const uint8_t *__restrict__ W, const 
     float o = v;
     if (bias) o = o + bias[r];
     if (res) o = res[r] + o;
-    y[r] = o;
+    put_y(&y[r], o, TAIL);
   }
+  if constexpr (TAIL) norm_tail(y, rows, ntl);
 }
 
 #define GEMVS_KERNELS(KN, KIND, NI, TAG, NTH)                                                                                            \
@@ -719,6 +842,23 @@ GEMVS_KERNELS(q4_k, AMDC_Q4_K, 1, s, 256)
 GEMVS_KERNELS(q4_k, AMDC_Q4_K, 2, s, 256)
 GEMVS_KERNELS(q4_k, AMDC_Q4_K, 3, s, 256)
 GEMVS_KERNELS(q4_k, AMDC_Q4_K, 4, s, 256)
+
+// The single-shot kernels with the fused RMSNorm tail (amdc_gemv_norm)
+#define GEMVSN_KERNEL(KN, KIND, NI)                                                                                                  \
+  extern "C" __global__ __launch_bounds__(256) void amdc_gemv_##KN##_n##NI(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, \
+                                                                           u32 nb, const float *bias, const float *res, u32 L,      \
+                                                                           const float *nw, float *ny, uint8_t *nq, float eps,      \
+                                                                           u32 *cnt) {                                              \
+    gemvs_body<KIND, NI, false, 256u, 0u, true>(W, xq, y, rows, nb, bias, res, L, nullptr, nullptr, NormTail{nw, ny, nq, eps, cnt}); \
+  }
+GEMVSN_KERNEL(q4_0, AMDC_Q4_0, 1)
+GEMVSN_KERNEL(q4_0, AMDC_Q4_0, 2)
+GEMVSN_KERNEL(q4_0, AMDC_Q4_0, 3)
+GEMVSN_KERNEL(q4_0, AMDC_Q4_0, 4)
+GEMVSN_KERNEL(q4_k, AMDC_Q4_K, 1)
+GEMVSN_KERNEL(q4_k, AMDC_Q4_K, 2)
+GEMVSN_KERNEL(q4_k, AMDC_Q4_K, 3)
+GEMVSN_KERNEL(q4_k, AMDC_Q4_K, 4)
 
 // The single-shot form with the quantization fused, sized to one workgroup per
 // CU (amdc_gemv_q4_0_xw1, amdc_gemv_q4_k_xw1 / _xw2: blockDim.x threads, up
@@ -876,14 +1016,18 @@ __device__ __forceinline__ void item_load(typename ItemOf<KIND>::type &w, __amdg
   }
 }
 
-template <int KIND>
+template <int KIND, bool TAIL = false>
 __device__ __forceinline__ void gemv2_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
-                                           u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 L) {
+                                           u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 L,
+                                           const NormTail &ntl = NormTail{}) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const u32 ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
   const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw;
   const u32 nrg = (rows + rpg - 1u) / rpg, ni = (ng + L - 1u) / L;
-  if (blockIdx.x >= nrg) return; // the whole workgroup
+  if (blockIdx.x >= nrg) { // the whole workgroup (with the tail it still counts itself)
+    if constexpr (TAIL) norm_tail(y, rows, ntl);
+    return;
+  }
   const u32 RB = (u32)amdc_row_bytes_k(KIND, nb), NR = rows * RB; // the host checks NR + RB < 2^32
   const u32 nblk = 8u * ng;
   u32x4 *s_lo = (u32x4 *)smem;
@@ -982,8 +1126,9 @@ __device__ __forceinline__ void gemv2_body(const uint8_t *__restrict__ W, const 
   const u32 ny = (n / ni) * rpg;
   for (u32 k = tid; k < ny; k += NT) {
     const u32 r = (blockIdx.x + (k / rpg) * gridDim.x) * rpg + k % rpg;
-    if (r < rows) y[r] = s_y[k];
+    if (r < rows) put_y(&y[r], s_y[k], TAIL);
   }
+  if constexpr (TAIL) norm_tail(y, rows, ntl);
 }
 
 extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q4_0_p2(const uint8_t *W, const uint8_t *xq, float *y, u32 rows, u32 nb,
@@ -1002,6 +1147,16 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_p2(const uint8_
                                                                    const float *bias, const float *res, u32 L) {
   gemv2_body<AMDC_Q6_K>(W, xq, y, rows, nb, bias, res, L);
 }
+// the Q8_0 / Q6_K decode form with the fused RMSNorm tail (amdc_gemv_norm)
+#define GEMV2N_KERNEL(KN, KIND)                                                                                                      \
+  extern "C" __global__ __launch_bounds__(256) void amdc_gemv_##KN##_pn(const uint8_t *W, const uint8_t *xq, float *y, u32 rows,    \
+                                                                        u32 nb, const float *bias, const float *res, u32 L,         \
+                                                                        const float *nw, float *ny, uint8_t *nq, float eps,         \
+                                                                        u32 *cnt) {                                                 \
+    gemv2_body<KIND, true>(W, xq, y, rows, nb, bias, res, L, NormTail{nw, ny, nq, eps, cnt});                                       \
+  }
+GEMV2N_KERNEL(q8_0, AMDC_Q8_0)
+GEMV2N_KERNEL(q6_k, AMDC_Q6_K)
 
 // ------------------------------------------------------------------ GEMV chain (one launch)
 
@@ -2407,6 +2562,8 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemm_reduce(const float *
 // after the barrier that follows it. No cache-wide writeback or invalidation
 // is needed (agent-scope fences, one per workgroup, made the launch 2x slower).
 __device__ __align__(256) u32 split_count[AMDC_SPLIT_TILES];
+// the arrival counter of the GEMVs with the fused RMSNorm tail (norm_tail; 0 between launches)
+__device__ __align__(256) u32 norm_count[64];
 
 __device__ __forceinline__ void split_put(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 

@@ -445,6 +445,25 @@ def producers_set(timer):
         else:
             t = timer.per_launch_ms(lambda j, s: amdc.swiglu_q8(X, Wt, n, Q, stream=s), 64)
         out[f"{name}_{n}"] = {"us": round(t * 1e3, 3)}
+    # the decode GEMV with the fused RMSNorm tail (amdc_gemv_norm) against the GEMV and a separate
+    # amdc_rmsnorm_q8 launch, over rotating weight copies (HBM), on the c1 o and c2 attn_out shapes
+    for kind, r, c in ((synth.KIND_Q4_0, 4096, 4096), (synth.KIND_Q4_K, 5120, 6144)):
+        nb = c // 32
+        M = Mats(kind, [("w", r, c)], 70 + r, min_bytes=1 << 30)
+        X = amdc.DevBuf.of(g.standard_normal(c).astype(np.float32))
+        Q, Y = amdc.DevBuf(q8_stride(nb)), amdc.DevBuf(4 * r)
+        amdc.quant_q8(X, Q, nb)
+        Wn, Ny, Nq = amdc.DevBuf.of(np.ones(r, np.float32)), amdc.DevBuf(4 * r), amdc.DevBuf(q8_stride(r // 32))
+
+        def two(j, s):
+            amdc.gemv(kind, M.dev[j % M.copies][0], Q, Y, r, nb, stream=s)
+            amdc.rmsnorm_q8(Y, Wn, Ny, r, 1e-6, Nq, stream=s)
+
+        t2 = timer.per_launch_ms(two, M.copies)
+        t1 = timer.per_launch_ms(lambda j, s: amdc.gemv_norm(kind, M.dev[j % M.copies][0], Q, Y, r, nb, Wn, Ny, 1e-6, nq=Nq, stream=s),
+                                 M.copies)
+        out[f"gemv_norm_{r}x{c}"] = {"fused_us": round(t1 * 1e3, 3), "gemv_then_rmsnorm_us": round(t2 * 1e3, 3)}
+        del M
     return out
 
 

@@ -155,6 +155,17 @@ int amdc_rmsnorm_q8(const float *x, const float *w, float *y, uint32_t n, float 
                     uint32_t qs, void *stream);
 int amdc_swiglu_q8(float *a, const float *b, uint32_t n, uint8_t *q, uint32_t T, uint32_t as, uint32_t qs, void *stream);
 
+/* The decode GEMV (T = 1, any kind) with the fused RMSNorm of its result:
+ * the reference's GEMV launch with NW / NY / NQ / eps (IE_NORM_FUSE,
+ * src/hip.c:928-931; the tail gemv_norm_tail, kernels/ie_kernels.c:267-283).
+ * y as amdc_gemv_q4 / _q4k / _q8 / _q6k; then the GEMV's last workgroup
+ * writes ny = rmsnorm(y) nw (rows floats) and, when nq is not NULL, its Q8
+ * copy: the bits of amdc_rmsnorm_q8(y, nw, ny, rows, eps, nq). rows is a
+ * multiple of 32, at most 8192. The workgroups count themselves on a library counter that
+ * each launch leaves at 0: two of these GEMVs must not run concurrently. */
+int amdc_gemv_norm(int kind, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias, const float *res,
+                   const float *nw, float *ny, uint8_t *nq, float eps, void *stream);
+
 /* The decode GEMV of an f32 input x (32 nb floats, 16-byte aligned): the
  * pair OP_QUANT + OP_GEMV_Q4 / OP_GEMV_Q4K (src/hip.c:922-933, 1023-1024).
  * For nb <= 128 (AMDC_GEMVX_FUSE_NB) one launch: every workgroup quantizes x
