@@ -279,7 +279,8 @@ enum {
   K_GEMVK_Q4 = K_GEMVXW_Q4 + 3, /* amdc_gemv_q4_0_k, _xk, amdc_gemv_q4_k_k, _xk */
   K_GEMVSN_Q4 = K_GEMVK_Q4 + 4, /* amdc_gemv_q4_0_n1 .. _n4, amdc_gemv_q4_k_n1 .. _n4 (fused RMSNorm tail) */
   K_GEMV2N = K_GEMVSN_Q4 + 8,   /* amdc_gemv_q8_0_pn, _q6_k_pn */
-  K_N = K_GEMV2N + 2
+  K_GEMMH_M128 = K_GEMV2N + 2,  /* amdc_gemmh_m128_n128 */
+  K_N = K_GEMMH_M128 + 1
 };
 static const char *const kname[K_N] = {
     "amdc_quant_q8",           "amdc_dots_q4_0",          "amdc_dots_q4_k",          "amdc_gemm_q4_k_n128",
@@ -301,7 +302,7 @@ static const char *const kname[K_N] = {
     "amdc_gemv_q4_0_xk",       "amdc_gemv_q4_k_k",        "amdc_gemv_q4_k_xk",
     "amdc_gemv_q4_0_n1",       "amdc_gemv_q4_0_n2",       "amdc_gemv_q4_0_n3",       "amdc_gemv_q4_0_n4",
     "amdc_gemv_q4_k_n1",       "amdc_gemv_q4_k_n2",       "amdc_gemv_q4_k_n3",       "amdc_gemv_q4_k_n4",
-    "amdc_gemv_q8_0_pn",       "amdc_gemv_q6_k_pn"};
+    "amdc_gemv_q8_0_pn",       "amdc_gemv_q6_k_pn",       "amdc_gemmh_m128_n128"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -470,7 +471,7 @@ int amdc_set_tuning(int gemv_lanes, int gemv_unroll, int gemv_wgs, int gemm_kern
   if (gemv_lanes && (gemv_lanes < 4 || gemv_lanes > 64 || (gemv_lanes & (gemv_lanes - 1))))
     return fail(AMDC_EINVAL, "gemv lanes %d: 4..64, a power of two", gemv_lanes);
   if (gemv_unroll < 0 || gemv_unroll > 2) return fail(AMDC_EINVAL, "gemv unroll %d: 0, 1 or 2", gemv_unroll);
-  if (gemm_kernel < 0 || gemm_kernel > 4) return fail(AMDC_EINVAL, "gemm kernel %d: 0..4", gemm_kernel);
+  if (gemm_kernel < 0 || gemm_kernel > 5) return fail(AMDC_EINVAL, "gemm kernel %d: 0..5", gemm_kernel);
   if (gemm_ksplit < 0 || gemm_ksplit > 16) return fail(AMDC_EINVAL, "gemm ksplit %d: 0..16", gemm_ksplit);
   if (gemv_wgs < 0) return fail(AMDC_EINVAL, "gemv workgroups %d", gemv_wgs);
   if (gemv_form < 0 || gemv_form > 4) return fail(AMDC_EINVAL, "gemv form %d: 0..4", gemv_form);
@@ -1204,7 +1205,7 @@ static int ws_take(size_t n, void **p) {
 static const struct {
   int k;
   u32 mr, nt, threads;
-} gh[2] = {{K_GEMMH_M64_N128, 64, 128, 256}, {K_GEMMH_M64_N64, 64, 64, 256}};
+} gh[3] = {{K_GEMMH_M64_N128, 64, 128, 256}, {K_GEMMH_M64_N64, 64, 64, 256}, {K_GEMMH_M128, 128, 128, 512}};
 
 /* The prefill GEMM on the f16-MFMA kernels (every kind). */
 static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *xq, float *y, uint32_t rows, uint32_t nb, const float *bias,
@@ -1226,7 +1227,10 @@ static int gemm_launch(int kind, const char *op, const void *w, const uint8_t *x
   const u32 ng = amdc_ngroups(nb), cus = g_cus > 0 ? (u32)g_cus : 256u;
   /* 64-token tiles for Q4_0 at any T (its 128-token kernel holds 284 VGPRs, one wave per SIMD:
      measured 150 / 188 TOPS against 140 / 169 on 11008 x 4096 / 4096 x 11008, T = 256) */
-  const int v = t_gemm >= 3 ? t_gemm - 3 : (T > 64u && kind != AMDC_KIND_Q4_0 ? 0 : 1);
+  /* Q4_K with more than 64 tokens: 128-row tiles below 65536 rows (amdc_gemmh_m128_n128 lists the
+     measurements) */
+  int v = t_gemm >= 3 ? t_gemm - 3 : (T > 64u && kind != AMDC_KIND_Q4_0 ? (kind == AMDC_KIND_Q4_K && rows < 65536u ? 2 : 0) : 1);
+  if (v >= 2 && kind != AMDC_KIND_Q4_K) v = 0; /* the 128-row tile is built for Q4_K */
   const int kk = kind == AMDC_KIND_Q8_0 ? (v ? K_GEMMH_Q8_N64 : K_GEMMH_Q8_N128)
                  : kind == AMDC_KIND_Q6_K ? (v ? K_GEMMH_Q6K_N64 : K_GEMMH_Q6K_N128)
                  : kind == AMDC_KIND_Q4_0 ? (v ? K_GEMMH_Q4_N64 : K_GEMMH_Q4_N128)

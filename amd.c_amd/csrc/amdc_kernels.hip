@@ -2220,20 +2220,20 @@ __device__ __forceinline__ void a_frag_q6(u32 w0, u32 w1, u32 hw, u32 h, int sc,
 // whose partial sums go to part[split][t][r - r0] (r0 the tail's first row,
 // row stride rows - r0) for amdc_gemm_reduce to add in split order. nfull is
 // a whole number of row tiles; nfull = 0 splits every tile.
-template <int NJ, int KIND>
+template <int NJ, int KIND, u32 MW = 2u>
 __device__ __forceinline__ void gemmh_body(const uint8_t *__restrict__ W, const _Float16 *__restrict__ xh, const float *__restrict__ DA,
                                            const float *__restrict__ XA, float *__restrict__ y, u32 rows, u32 nb,
                                            const float *__restrict__ bias, const float *__restrict__ res, u32 T, u32 Tp, u32 ys, u32 rs,
                                            float *__restrict__ part, u32 nfull, u32 nsplit) {
-  constexpr u32 NTH = 256u, MR = 64u, NTT = 32u * NJ;
+  constexpr u32 NTH = 128u * MW, MR = 32u * MW, NTT = 32u * NJ; // MW waves of 32 rows x 2 of 16 NJ tokens
   constexpr u32 BSTR = 72u; // halves per token per stage: 2 blocks x 32 + 8 of padding
   __shared__ __attribute__((aligned(16))) _Float16 sb[2][NTT * BSTR];
   __shared__ __attribute__((aligned(16))) float sda[2][2][NTT];
   __shared__ __attribute__((aligned(16))) float sxa[2][8][NTT]; // d_a asum of a super-block's 8 blocks, by parity
   __shared__ float sspare[2][2u * NTT < NTH ? NTH : 1u];
   constexpr bool PB = KIND == AMDC_Q8_0 || KIND == AMDC_Q4_0;     // a d per (row, block): applied per block
-  __shared__ __attribute__((aligned(16))) float sdw[PB ? 4 : 1][2][8][16]; // per wave: d [row tile][block][row]
-  const u32 ng = KIND == AMDC_Q8_0 || KIND == AMDC_Q4_0 ? amdc_ngroups(nb) : nb >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6, wm = w & 1u, wn = w >> 1;
+  __shared__ __attribute__((aligned(16))) float sdw[PB ? 2u * MW : 1][2][8][16]; // per wave: d [row tile][block][row]
+  const u32 ng = KIND == AMDC_Q8_0 || KIND == AMDC_Q4_0 ? amdc_ngroups(nb) : nb >> 3, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6, wm = w % MW, wn = w / MW;
   const u32 i16 = lane & 15u, h = lane >> 4;
   const u32 ntt = (T + NTT - 1u) / NTT, b = blockIdx.x, full = b < nfull;
   const u32 tail = (rows + MR - 1u) / MR * ntt - nfull, tj = b - nfull; // tail tiles; a tail block's index among the tail blocks
@@ -2492,6 +2492,16 @@ GEMMH_KERNEL(amdc_gemmh_q6_k_m64_n128, 4, AMDC_Q6_K)
 GEMMH_KERNEL(amdc_gemmh_q6_k_m64_n64, 2, AMDC_Q6_K)
 GEMMH_KERNEL(amdc_gemmh_q4_0_m64_n128, 4, AMDC_Q4_0)
 GEMMH_KERNEL(amdc_gemmh_q4_0_m64_n64, 2, AMDC_Q4_0)
+// 128-row tiles, 8 waves (4 x 2): the stage's activations in the LDS shared by twice the rows (Q4_K,
+// T > 64, the default below 65536 rows; measured on MI355X, T = 256, us per call with the prep, 64 /
+// 128-row tiles: 5120 x 17408 185.6 / 161.3, 17408 x 5120 161.5 / 158.1, 34816 x 5120 305 / 288, 4096 x
+// 11008 99.2 / 90.2, 6144 x 5120 82.1 / 76.3, 152064 x 5120 1116 / 1161; 128 rows x 64 tokens, 124
+// VGPRs and two workgroups per CU: 170-266 TOPS, slower everywhere)
+extern "C" __global__ __launch_bounds__(512) void amdc_gemmh_m128_n128(const uint8_t *W, const _Float16 *xh, const float *DA, const float *XA,
+                                                                      float *y, u32 rows, u32 nb, const float *bias, const float *res, u32 T,
+                                                                      u32 Tp, u32 ys, u32 rs, float *part, u32 nfull, u32 nsplit) {
+  gemmh_body<4, AMDC_Q4_K, 4u>(W, xh, DA, XA, y, rows, nb, bias, res, T, Tp, ys, rs, part, nfull, nsplit);
+}
 
 // The split-K sums: y[t][r] = the pairwise tree (adjacent splits first, a
 // split past nks counting as +0.0) of part[0][t][r], part[1][t][r], ...,

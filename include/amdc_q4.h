@@ -274,7 +274,7 @@ int amdc_block_dots(int kind, const void *w, const uint8_t *xq, int32_t *out, ui
  * two); the decode kernel (0: the pipelined one; 1 or 2: the multi-vector
  * kernel with 1 or 2 super-groups of loads per step); workgroups of a GEMV
  * launch; the GEMM kernel (1, 2: int8 MFMA with 64 or 128 tokens per
- * workgroup; 3, 4: f16 MFMA, rows x tokens 64x128, 64x64);
+ * workgroup; 3, 4, 5: f16 MFMA, rows x tokens 64x128, 64x64, 128x128 (Q4_K));
  * the GEMM's K split (1..16); the decode kernel's form when gemv_unroll is 0
  * (1: the persistent pipelined form, 2: the buffer-load form that keeps the
  * next super-group in flight, 3: the single-shot form, one row group per

@@ -111,11 +111,11 @@ def test_exact_verify(dev, orc, kind, rows, nb):
 @pytest.mark.gpu
 @pytest.mark.parametrize("kind,rows,nb", SHAPES)
 def test_exact_gemm(dev, orc, kind, rows, nb):
-    """The prefill GEMMs (f16-MFMA 64 / 128-token tiles, the int8-MFMA Q4_K kernels) with and without split K
+    """The prefill GEMMs (f16-MFMA 64 / 128-token tiles, 128-row tiles for Q4_K, the int8-MFMA Q4_K kernels) with and without split K
     return the exact sums."""
     T = 80
     e = Exact(orc, kind, rows, nb, T, seed=kind * 30 + nb, dev=dev)
-    kerns = [(0, 0), (3, 0), (4, 0), (3, 2), (4, 4), (3, 8)] + ([(1, 0), (2, 0)] if kind == 3 else [])
+    kerns = [(0, 0), (3, 0), (4, 0), (3, 2), (4, 4), (3, 8)] + ([(1, 0), (2, 0), (5, 0), (5, 3)] if kind == 3 else [])
     try:
         for kern, ks in kerns:
             dev.set_tuning(gemm_kernel=kern, gemm_ksplit=ks)

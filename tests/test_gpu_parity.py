@@ -177,7 +177,7 @@ def test_gemv_multi(dev, orc, kind, rows, nb, T, path):
 
 # ---------------------------------------------------------------- prefill GEMM
 
-@pytest.mark.parametrize("kern,ks", [(0, 0), (1, 0), (2, 0), (3, 1), (4, 2), (3, 4), (4, 3)])
+@pytest.mark.parametrize("kern,ks", [(0, 0), (1, 0), (2, 0), (3, 1), (4, 2), (3, 4), (4, 3), (5, 1), (5, 3)])
 @pytest.mark.parametrize("rows,nb,T", [(1, 8, 17), (63, 16, 64), (64, 160, 65), (130, 40, 130), (300, 24, 256), (70, 544, 33)])
 def test_gemm_q4k(dev, orc, rows, nb, T, kern, ks):
     c = Case(dev, orc, 3, rows, nb, T, seed=rows + T)
@@ -251,7 +251,7 @@ def test_graph_replay_matches_eager(dev, orc):
     assert rel_err(Y1.download(np.float32), c.y_oracle(0), c.mag(0)) < TOL
 
 
-@pytest.mark.parametrize("kern,ks", [(0, 0), (1, 0), (3, 2), (4, 4)])
+@pytest.mark.parametrize("kern,ks", [(0, 0), (1, 0), (3, 2), (4, 4), (5, 2)])
 def test_gemm_deterministic(dev, orc, kern, ks):
     """Repeated GEMMs give the same bits: the kernels have a fixed summation order, so any
     difference between runs would be a race between waves."""
