@@ -280,7 +280,8 @@ enum {
   K_GEMVSN_Q4 = K_GEMVK_Q4 + 4, /* amdc_gemv_q4_0_n1 .. _n4, amdc_gemv_q4_k_n1 .. _n4 (fused RMSNorm tail) */
   K_GEMV2N = K_GEMVSN_Q4 + 8,   /* amdc_gemv_q8_0_pn, _q6_k_pn */
   K_GEMMH_M128 = K_GEMV2N + 2,  /* amdc_gemmh_m128_n128 */
-  K_N = K_GEMMH_M128 + 1
+  K_GEMVM8 = K_GEMMH_M128 + 1,  /* amdc_gemv_q8_0_m1, amdc_gemv_q6_k_m1 */
+  K_N = K_GEMVM8 + 2
 };
 static const char *const kname[K_N] = {
     "amdc_quant_q8",           "amdc_dots_q4_0",          "amdc_dots_q4_k",          "amdc_gemm_q4_k_n128",
@@ -302,7 +303,8 @@ static const char *const kname[K_N] = {
     "amdc_gemv_q4_0_xk",       "amdc_gemv_q4_k_k",        "amdc_gemv_q4_k_xk",
     "amdc_gemv_q4_0_n1",       "amdc_gemv_q4_0_n2",       "amdc_gemv_q4_0_n3",       "amdc_gemv_q4_0_n4",
     "amdc_gemv_q4_k_n1",       "amdc_gemv_q4_k_n2",       "amdc_gemv_q4_k_n3",       "amdc_gemv_q4_k_n4",
-    "amdc_gemv_q8_0_pn",       "amdc_gemv_q6_k_pn",       "amdc_gemmh_m128_n128"};
+    "amdc_gemv_q8_0_pn",       "amdc_gemv_q6_k_pn",       "amdc_gemmh_m128_n128",
+    "amdc_gemv_q8_0_m1",       "amdc_gemv_q6_k_m1"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -310,6 +312,8 @@ static int g_occ[K_N]; /* resident workgroups per CU, looked up at a kernel's fi
 static int g_open, g_cus;
 static int t_lanes = -1, t_unroll = -1, t_wgs = -1, t_gemm = -1, t_gemm_min = -1, t_ksplit = -1;
 static u32 *g_norm_cnt; /* the fused-norm GEMVs' arrival counter (device, 0 between launches) */
+/* The largest T x rows x super-groups that runs on the few-vector Q8_0 / Q6_K kernels (tuning: AMDC_GEMVM8_MAX) */
+static u64 M8_MAX = 786432u;
 static u32 x_fuse_nb = 128; /* amdc_gemv_q4_x / _q4k_x: the largest nb quantized inside the GEMV */
 /* The chain recorder (amdc_chain_record_begin / _end): while it is on, the recordable operators
  * called on its stream append chain operations instead of launching; every other launch on that
@@ -445,6 +449,7 @@ int amdc_open(const char *hsaco) {
      variable when set; else 0, the MI355X rule of use_gemm */
   if (t_gemm_min < 0) t_gemm_min = envi("IE_GEMM_MIN", 0);
   x_fuse_nb = (u32)envi("AMDC_GEMVX_FUSE_NB", 128);
+  M8_MAX = (u64)envi("AMDC_GEMVM8_MAX", 786432);
   t_form = envi("AMDC_GEMV_FORM", 0);
   g_open = 1;
   return AMDC_OK;
@@ -895,6 +900,25 @@ static int gemv_launch(int kind, const void *w, const uint8_t *xq, float *y, uin
                        const float *res, uint32_t T, uint32_t xs, uint32_t ys, uint32_t rs, void *stream) {
   if (kind == AMDC_KIND_Q8_0 || kind == AMDC_KIND_Q6_K) {
     if (T == 1u || t_unroll > 0) return gemv_k8_launch(kind, w, xq, y, rows, nb, bias, res, T, xs, ys, rs, stream);
+    if (T <= 8u && t_ksplit == 0) {
+      /* a few vectors on a small matrix: the decode items and arithmetic for every vector
+         (amdc_gemv_{q8_0,q6_k}_m1), one launch, the vectors in LDS, one super-group per lane (the
+         kernels with two hold 229 / 321 VGPRs) */
+      const u32 ng = amdc_ngroups(nb), bpb = kind == AMDC_KIND_Q6_K ? 44u : 40u, lds = bpb * 8u * ng * T;
+      u32 L = 4u;
+      while (L < 64u && L < ng) L <<= 1;
+      const u32 ni = (ng + L - 1u) / L, rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
+      const u64 rb = amdc_row_bytes_k(kind, nb);
+      /* measured on MI355X (us, this kernel / the MFMA verify kernel): Q6_K 1024 x 5120 T = 2, 4, 8 5.2 /
+         14.3, 6.9 / 14.4, 10.3 / 17.8; 4096 x 4096 6.6 / 15.4, 8.2 / 15.4, 11.5 / 18.6; 6144 x 5120 T = 4
+         15.7 / 17.2. Q8_0 4096 x 4096 6.4 / 9.5, 7.8 / 9.6, 10.6 / 10.1; 11008 x 4096 T = 2, 4 12.3 /
+         15.2, 15.4 / 14.9; 1024 x 2048 T = 8 7.6 / 6.5: Q8_0 only up to T = 4 and half the size */
+      const u64 lim = kind == AMDC_KIND_Q6_K ? M8_MAX : T <= 4u ? M8_MAX * 2u / 3u : 0u;
+      if (ni == 1u && lds <= 64u * 1024u && (u64)T * rows * ng <= lim && (u64)rows * rb + rb < (1ull << 32)) {
+        void *a[] = {&w, &xq, &y, &rows, &nb, &bias, &res, (void *)&L, &T, &xs, &ys, &rs};
+        return launch(K_GEMVM8 + (kind == AMDC_KIND_Q6_K ? 1 : 0), nrg, 1, lds, stream, a);
+      }
+    }
   } else if (T > 1u && t_unroll > 0) { /* tuning: one decode launch per vector */
     for (u32 t = 0; t < T; t++) {
       int rc = gemv_launch(kind, w, xq + (u64)t * xs, y + (u64)t * ys, rows, nb, bias, res ? res + (u64)t * rs : NULL, 1u, 0u, 0u, 0u, stream);

@@ -1158,6 +1158,95 @@ extern "C" __global__ __launch_bounds__(256) void amdc_gemv_q6_k_p2(const uint8_
 GEMV2N_KERNEL(q8_0, AMDC_Q8_0)
 GEMV2N_KERNEL(q6_k, AMDC_Q6_K)
 
+// A few vectors (T <= 8) on a small Q8_0 / Q6_K matrix (amdc_gemv_{q8_0,q6_k}_m1): the decode GEMV's
+// items and block arithmetic (gemv2_body's, one row group per workgroup, NI super-groups per lane) with
+// the Q8 vectors of all T tokens staged in the LDS; each lane dots its items with every token (the
+// decode arithmetic per token: bit-equal to T decode GEMVs), weights read once, no K split.
+template <int KIND, u32 NI>
+__device__ __forceinline__ void gemvm8_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ xq, float *__restrict__ y, u32 rows,
+                                            u32 nb, const float *__restrict__ bias, const float *__restrict__ res, u32 L, u32 T, u32 xs,
+                                            u32 ys, u32 rs) {
+  constexpr u32 TM = 8u, BPB = KIND == AMDC_Q6_K ? 44u : 40u; // vectors per launch; LDS bytes per block
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const u32 ng = amdc_ngroups(nb), tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const u32 l = lane & (L - 1u), q = lane / L, rpw = 64u / L, rpg = 4u * rpw;
+  const u32 RB = (u32)amdc_row_bytes_k(KIND, nb), NR = rows * RB; // the host checks NR + RB < 2^32
+  const u32 nblk = 8u * ng, tb = BPB * nblk; // LDS bytes per token
+  const u32 r = blockIdx.x * rpg + wv * rpw + q;
+  const __amdgpu_buffer_rsrc_t rw = rsrc(W, NR);
+  typename ItemOf<KIND>::type it[NI];
+#pragma unroll
+  for (u32 i = 0; i < NI; i++) {
+    const u32 g = l + L * i;
+    item_load<KIND, 0>(it[i], rw, g < ng && r < rows ? r * RB : NR, g, ng);
+  }
+  __asm__ volatile("" ::: "memory"); // the weight loads ahead of the vectors'
+  // stage (token, block) pairs, 4 per thread in flight at a time, permuted as gemv2_body stages them
+  for (u32 j0 = tid; j0 < T * nblk; j0 += 4u * NT) {
+    u32x4 lo[4], hi[4];
+    float d[4];
+#pragma unroll
+    for (u32 c = 0; c < 4u; c++) {
+      const u32 j = j0 + c * NT, t = j / nblk, jb = j - t * nblk;
+      const bool in = j < T * nblk && jb < nb;
+      const uint8_t *xt = xq + (u64)(in ? t : 0u) * xs;
+      const u32 jj = in ? jb : 0u;
+      lo[c] = *(const u32x4 *)(xt + 32u * jj);
+      hi[c] = *(const u32x4 *)(xt + 32u * jj + 16u);
+      d[c] = ((const float *)(xt + 32u * nb))[jj];
+      if (!in) lo[c] = (u32x4)(0u), hi[c] = (u32x4)(0u), d[c] = 0.0f;
+    }
+#pragma unroll
+    for (u32 c = 0; c < 4u; c++) {
+      const u32 j = j0 + c * NT;
+      if (j < T * nblk) {
+        const u32 t = j / nblk, jb = j - t * nblk, p = (jb & 7u) * ng + (jb >> 3);
+        uint8_t *base = smem + t * tb;
+        ((u32x4 *)base)[p] = lo[c];
+        ((u32x4 *)base + nblk)[p] = hi[c];
+        ((float *)(base + 32u * nblk))[p] = d[c];
+        if constexpr (KIND == AMDC_Q6_K) // 32 x the sum of each half of the block, as gemv2_body stages it
+          ((u32x2 *)(base + 36u * nblk))[p] = (u32x2){32u * (u32)hsum16(lo[c]), 32u * (u32)hsum16(hi[c])};
+      }
+    }
+  }
+  __syncthreads();
+  ItemTree tr[TM];
+#pragma unroll
+  for (u32 i = 0; i < NI; i++) {
+    const u32 g = l + L * i;
+#pragma unroll
+    for (u32 t = 0; t < TM; t++) {
+      if (t < T) {
+        const uint8_t *base = smem + t * tb;
+        const float leaf = item_dot<KIND>(it[i], g < ng ? g : 0u, ng, (const u32x4 *)base, (const u32x4 *)base + nblk,
+                                          (const float *)(base + 32u * nblk), (const u32 *)(base + 36u * nblk), 0.0f);
+        tr[t].add(seg_sum(g < ng ? leaf : 0.0f, L), i);
+      }
+    }
+  }
+  if (l == 0u && r < rows) {
+    const float b = bias ? bias[r] : 0.0f;
+#pragma unroll
+    for (u32 t = 0; t < TM; t++) {
+      if (t < T) {
+        float o = tr[t].sum(NI);
+        if (bias) o = o + b;
+        if (res) o = res[(u64)t * rs + r] + o;
+        y[(u64)t * ys + r] = o;
+      }
+    }
+  }
+}
+#define GEMVM8_KERNEL(KN, KIND, NI)                                                                                                        \
+  extern "C" __global__ __launch_bounds__(256) void amdc_gemv_##KN##_m##NI(const uint8_t *W, const uint8_t *xq, float *y, u32 rows,    \
+                                                                           u32 nb, const float *bias, const float *res, u32 L, u32 T,  \
+                                                                           u32 xs, u32 ys, u32 rs) {                                   \
+    gemvm8_body<KIND, NI>(W, xq, y, rows, nb, bias, res, L, T, xs, ys, rs);                                                              \
+  }
+GEMVM8_KERNEL(q8_0, AMDC_Q8_0, 1)
+GEMVM8_KERNEL(q6_k, AMDC_Q6_K, 1)
+
 // ------------------------------------------------------------------ GEMV chain (one launch)
 
 // A list of quantize and decode-GEMV operations run by one persistent launch
