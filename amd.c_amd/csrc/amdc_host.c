@@ -281,7 +281,8 @@ enum {
   K_GEMV2N = K_GEMVSN_Q4 + 8,   /* amdc_gemv_q8_0_pn, _q6_k_pn */
   K_GEMMH_M128 = K_GEMV2N + 2,  /* amdc_gemmh_m128_n128 */
   K_GEMVM8 = K_GEMMH_M128 + 1,  /* amdc_gemv_q8_0_m1, amdc_gemv_q6_k_m1 */
-  K_N = K_GEMVM8 + 2
+  K_GEMVS1W = K_GEMVM8 + 2,     /* amdc_gemv_q4_0_s1w, amdc_gemv_q4_k_s1w */
+  K_N = K_GEMVS1W + 2
 };
 static const char *const kname[K_N] = {
     "amdc_quant_q8",           "amdc_dots_q4_0",          "amdc_dots_q4_k",          "amdc_gemm_q4_k_n128",
@@ -304,7 +305,7 @@ static const char *const kname[K_N] = {
     "amdc_gemv_q4_0_n1",       "amdc_gemv_q4_0_n2",       "amdc_gemv_q4_0_n3",       "amdc_gemv_q4_0_n4",
     "amdc_gemv_q4_k_n1",       "amdc_gemv_q4_k_n2",       "amdc_gemv_q4_k_n3",       "amdc_gemv_q4_k_n4",
     "amdc_gemv_q8_0_pn",       "amdc_gemv_q6_k_pn",       "amdc_gemmh_m128_n128",
-    "amdc_gemv_q8_0_m1",       "amdc_gemv_q6_k_m1"};
+    "amdc_gemv_q8_0_m1",       "amdc_gemv_q6_k_m1",       "amdc_gemv_q4_0_s1w",      "amdc_gemv_q4_k_s1w"};
 
 static hipModule_t g_mod;
 static hipFunction_t g_k[K_N];
@@ -865,6 +866,11 @@ static int gemvs_launch(int kind, const void *w, const void *in, int fq, float *
   const u32 rpg = 4u * (64u / L), nrg = (rows + rpg - 1u) / rpg;
   if (ni > 4u) return fail(AMDC_EINVAL, "gemv: %u super-groups on %u lanes (at most 4 per lane)", ng, L);
   const int k = (fq ? K_GEMVXS_Q4 : K_GEMVS_Q4) + (kind == AMDC_KIND_Q4_K ? 4 : 0) + (int)ni - 1;
+  if (!fq && ni == 1u && rows >= 16384u) { /* 512-thread workgroups: the vector staged once per 8 waves */
+    const u32 rpgw = 8u * (64u / L), nrgw = (rows + rpgw - 1u) / rpgw;
+    void *a[] = {&w, &in, &y, &rows, &nb, &bias, &res, (void *)&L};
+    return launch_nt(K_GEMVS1W + (kind == AMDC_KIND_Q4_K ? 1 : 0), nrgw, 1, 512u, 320u * ng, stream, a);
+  }
   if (fq) {
     void *a[] = {&w, &in, &y, &rows, &nb, &bias, &res, (void *)&L, &q8};
     return launch(k, nrg, 1, 320u * ng, stream, a);

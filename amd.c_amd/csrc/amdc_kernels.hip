@@ -842,6 +842,18 @@ GEMVS_KERNELS(q4_k, AMDC_Q4_K, 1, s, 256)
 GEMVS_KERNELS(q4_k, AMDC_Q4_K, 2, s, 256)
 GEMVS_KERNELS(q4_k, AMDC_Q4_K, 3, s, 256)
 GEMVS_KERNELS(q4_k, AMDC_Q4_K, 4, s, 256)
+// The one-item single-shot kernels on 512-thread workgroups (amdc_gemv_{q4_0,q4_k}_s1w): the Q8 vector
+// staged once per 8 waves instead of 4, for matrices of many rows (the host takes them from 16384
+// rows; MI355X, us, 256 / 512 threads: 152064 x 5120 Q4_K 74.2 / 69.9, 34816 x 5120 20.3 / 19.6,
+// 32000 x 4096 Q4_0 13.9 / 13.8; 6144 x 5120 Q4_K 6.9 / 7.1, 4096 x 4096 Q4_0 4.4 / 4.8). Same lanes per
+// row and summation order: the same bits.
+#define GEMVS_KERNEL_512(KN, KIND)                                                                                                  \
+  extern "C" __global__ __launch_bounds__(512) void amdc_gemv_##KN##_s1w(const uint8_t *W, const uint8_t *xq, float *y, u32 rows,  \
+                                                                         u32 nb, const float *bias, const float *res, u32 L) {     \
+    gemvs_body<KIND, 1, false, 512u>(W, xq, y, rows, nb, bias, res, L);                                                           \
+  }
+GEMVS_KERNEL_512(q4_0, AMDC_Q4_0)
+GEMVS_KERNEL_512(q4_k, AMDC_Q4_K)
 
 // The single-shot kernels with the fused RMSNorm tail (amdc_gemv_norm)
 #define GEMVSN_KERNEL(KN, KIND, NI)                                                                                                  \

@@ -203,3 +203,23 @@ def test_fused_quant_halfway(dev, orc, kind, rows, nb):
     ch.launch()
     ch.check()
     assert np.array_equal(Y3.download(np.uint32), Y2.download(np.uint32))
+
+
+@pytest.mark.parametrize("kind,rows,nb", [(0, 16400, 128), (3, 17000, 160), (0, 20000, 13)])
+def test_decode_512_thread_single_shot_equal(dev, kind, rows, nb):
+    """From 16384 rows the one-item single-shot GEMV runs on 512-thread workgroups (amdc_gemv_*_s1w): its
+    bits equal the persistent form's (form 1) and the 256-thread single-shot form's (a partial last
+    workgroup included)."""
+    W, X, Q, xs = setup(dev, kind, rows, nb, 1, seed=rows)
+    Y = dev.DevBuf(4 * rows)
+    dev.gemv(kind, W, Q, Y, rows, nb)
+    assert dev.last_kernel().endswith("_s1w"), dev.last_kernel()
+    got = Y.download(np.uint32)
+    try:
+        for form in (1, 2):
+            dev.set_tuning(form=form)
+            Y.fill(0xFF)
+            dev.gemv(kind, W, Q, Y, rows, nb)
+            assert np.array_equal(Y.download(np.uint32), got), form
+    finally:
+        dev.set_tuning()

@@ -121,7 +121,7 @@ def test_no_packed_fp32(code):
 
 def test_decode_dots_on_dot4(code):
     funcs, _ = code
-    dec = [k for k in funcs if re.match(r"amdc_gemv_q(4_0|4_k|8_0|6_k)_(s\d|xs\d|xw\d|n\d|p1|p2|pn|x1|m1)$", k)]
+    dec = [k for k in funcs if re.match(r"amdc_gemv_q(4_0|4_k|8_0|6_k)_(s\d|s1w|xs\d|xw\d|n\d|p1|p2|pn|x1|m1)$", k)]
     assert len(dec) >= 16
     for k in dec:
         n = sum(re.match(r"v_dot4c?_i32_i8", mn) is not None for _, mn, _ in funcs[k])
