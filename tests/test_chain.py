@@ -503,3 +503,29 @@ def test_chain_recorder(dev, orc):
         dev.gemv(3, B.W, B.Q, B.Y, 64, 8)
         dev.gemv(3, B.W, B.Q, B.Y, 64, 8, stream=S.s)
     del rec3
+
+
+@pytest.mark.parametrize("nb", [1, 13, 200])
+def test_chain_producers_ragged(dev, nb):
+    """The producer operations at block counts that are not multiples of a workgroup's 8 (and a single
+    block): equal to amdc_rmsnorm_q8 / amdc_swiglu_q8 bit for bit."""
+    n = 32 * nb
+    g = np.random.default_rng(nb)
+    x = dev.DevBuf.of(g.standard_normal(n).astype(np.float32))
+    w = dev.DevBuf.of((1.0 + 0.1 * g.standard_normal(n)).astype(np.float32))
+    a0 = g.standard_normal(n).astype(np.float32)
+    b = dev.DevBuf.of(g.standard_normal(n).astype(np.float32))
+    y0, q0, q1 = dev.DevBuf(4 * n), dev.DevBuf(q8_stride(nb)), dev.DevBuf(q8_stride(nb))
+    a = dev.DevBuf.of(a0)
+    dev.rmsnorm_q8(x, w, y0, n, 1e-6, q=q0)
+    dev.swiglu_q8(a, b, n, q=q1)
+    dev.sync()
+    want = [y0.download(np.uint8), q0.download(np.uint8)[:40 * nb], a.download(np.uint8), q1.download(np.uint8)[:40 * nb]]
+    y1, r0, r1 = dev.DevBuf(4 * n), dev.DevBuf(q8_stride(nb)), dev.DevBuf(q8_stride(nb))
+    a2 = dev.DevBuf.of(a0)
+    ch = dev.Chain([dev.chain_rmsnorm_q8(x, w, y1, nb, 1e-6, q=r0, sync=False), dev.chain_swiglu_q8(a2, b, nb, q=r1)])
+    ch.launch()
+    ch.check()
+    got = [y1.download(np.uint8), r0.download(np.uint8)[:40 * nb], a2.download(np.uint8), r1.download(np.uint8)[:40 * nb]]
+    for i, (gt, wt) in enumerate(zip(got, want)):
+        assert np.array_equal(gt, wt), i
